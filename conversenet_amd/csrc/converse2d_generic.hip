@@ -1,0 +1,668 @@
+// Converse2D forward, generic multi-pass path (any plane size up to kMaxFftLen per dimension).
+//
+// Algorithm (per (b, c) plane; notation: y = padded input (h x w), s = scale, Hs = h s, Ws = w s,
+// K = OTF of the psf at (Hs, Ws), lambda = sigmoid(bias - 9) + eps):
+//   * module path (util_converse.py:142-192, x0 = nearest(y)):
+//       X = Phi * tile_s(F_hw(y)),   out = crop(Re F^-1_{Hs Ws}(X))
+//     with Phi = Hn + conj(K) (1 - M(K Hn)) / (M(|K|^2) + lambda), Hn the nearest-hold response
+//     sum_{a<s} exp(-2 pi i u a / Hs) per axis and M the mean over the s*s alias group of a bin.
+//     This is the reference solve (FR - FBC*invWBR)/lambda rewritten without the division by
+//     lambda, which cancels exactly; Phi is evaluated in fp64 once per channel (or per sample).
+//   * op path (converse2d.cpp:165-209, arbitrary x0):
+//       X = X0 + conj(K) (tile_s(F(y)) - M(K X0)) / (M(|K|^2) + lambda),   out = Re F^-1(X).
+//
+// Kernels:
+//   k_phi_module / k_phi_op : transfer tables in fp64 (one block per channel column class)
+//   k_rows_fwd               : padding on load, R2C along rows (two real rows per complex FFT),
+//                              writes the half spectrum column-major  S[plane][col][row]
+//   k_cols_module            : per HR column: LR column FFT, tile, * Phi, inverse HR column FFT
+//   k_cols_op                : per alias class: LR and x0 column FFTs, alias-group solve, inverse
+//   k_rows_inv               : C2R along rows (two rows per complex FFT), crop + activation on store
+#include <math.h>
+
+#include <algorithm>
+
+#include "cvn_common.h"
+
+namespace cvn {
+
+// ------------------------------------------------------------------------------------------------
+// padding index map (F.pad semantics); returns -1 for a zero sample
+// ------------------------------------------------------------------------------------------------
+__device__ __forceinline__ int pad_src(int i, int n, int p, int mode) {
+  int j = i - p;
+  if (j >= 0 && j < n) return j;
+  switch (mode) {
+    case CVN_PAD_CIRCULAR: j %= n; return j < 0 ? j + n : j;
+    case CVN_PAD_REPLICATE: return j < 0 ? 0 : n - 1;
+    case CVN_PAD_REFLECT: return j < 0 ? -j : 2 * (n - 1) - j;
+    default: return -1;
+  }
+}
+
+__device__ __forceinline__ float gelu_exact(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
+
+__device__ __forceinline__ double2 dcmul(double2 a, double2 b) {
+  return make_double2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+}
+__device__ __forceinline__ double2 dexpi(double num, double den) {  // exp(-2 pi i num / den)
+  double sn, cs;
+  sincospi(-2.0 * num / den, &sn, &cs);
+  return make_double2(cs, sn);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Transfer tables (fp64 arithmetic).  One block per (psf plane, LR column class v0); threads over
+// the LR row class u0.  Members of a class: (u0 + a h, v0 + b w), a, b in [0, s).
+// ------------------------------------------------------------------------------------------------
+struct PhiArgs {
+  const float* psf;   // (Cp, kh, kw)
+  const float* bias;  // (C)
+  int64_t Cp;
+  int C, kh, kw, s, h, w, Hs, Ws, NCs;
+  int nv0;            // number of column classes handled
+  double eps;
+  float2* phi;        // module: (Cp, NCs, Hs);  op: A (Cp, Ws, Hs)
+  float2* kf;         // op only: K (Cp, Ws, Hs)
+};
+
+// P[b][i] = sum_j psf[i][j] exp(-2 pi i v_b (j - kw/2) / Ws), into LDS.
+__device__ void phi_row_sums(const PhiArgs& a, const float* psf, int v0, double2* P) {
+  const int n = a.s * a.kh;
+  for (int e = threadIdx.x; e < n; e += blockDim.x) {
+    const int b = e / a.kh, i = e - b * a.kh;
+    const int64_t vb = v0 + (int64_t)b * a.w;
+    double2 acc = make_double2(0.0, 0.0);
+    const double2 r = dexpi((double)vb, (double)a.Ws);
+    double2 ph = dexpi(-(double)(vb * (a.kw / 2) % a.Ws), (double)a.Ws);  // exp(+2 pi i vb cw / Ws)
+    for (int j = 0; j < a.kw; ++j) {
+      const double t = (double)psf[i * a.kw + j];
+      acc.x += t * ph.x;
+      acc.y += t * ph.y;
+      ph = dcmul(ph, r);
+    }
+    P[e] = acc;
+  }
+}
+
+// K(u_a, v_b) = sum_i exp(-2 pi i u_a (i - kh/2) / Hs) P[b][i]
+__device__ __forceinline__ double2 phi_otf(const PhiArgs& a, const double2* P, int b, int64_t ua) {
+  const double2 r = dexpi((double)ua, (double)a.Hs);
+  double2 e = dexpi(-(double)(ua * (a.kh / 2) % a.Hs), (double)a.Hs);
+  double2 acc = make_double2(0.0, 0.0);
+  const double2* Pb = P + b * a.kh;
+  for (int i = 0; i < a.kh; ++i) {
+    const double2 t = dcmul(e, Pb[i]);
+    acc.x += t.x;
+    acc.y += t.y;
+    e = dcmul(e, r);
+  }
+  return acc;
+}
+
+// sum_{t<s} exp(-2 pi i u t / N)
+__device__ __forceinline__ double2 hold(int s, int64_t u, int N) {
+  double2 acc = make_double2(1.0, 0.0);
+  for (int t = 1; t < s; ++t) {
+    const double2 e = dexpi((double)((u * t) % N), (double)N);
+    acc.x += e.x;
+    acc.y += e.y;
+  }
+  return acc;
+}
+
+__device__ __forceinline__ double lambda_of(const PhiArgs& a, int c) {
+  const double b = (double)a.bias[c] - 9.0;
+  return 1.0 / (1.0 + exp(-b)) + a.eps;
+}
+
+__global__ void k_phi_module(PhiArgs a) {
+  extern __shared__ double2 Psm[];
+  const int64_t cp = blockIdx.x / a.nv0;
+  const int v0 = (int)(blockIdx.x - cp * a.nv0);
+  const int c = (int)(cp % a.C);
+  phi_row_sums(a, a.psf + cp * a.kh * a.kw, v0, Psm);
+  __syncthreads();
+  const double lmb = lambda_of(a, c);
+  const double inv_s2 = 1.0 / ((double)a.s * a.s);
+  const double norm = 1.0 / ((double)a.Hs * (double)a.Ws);
+  for (int u0 = threadIdx.x; u0 < a.h; u0 += blockDim.x) {
+    double2 mkh = make_double2(0.0, 0.0);
+    double mk2 = 0.0;
+    for (int b = 0; b < a.s; ++b) {
+      const int64_t vb = v0 + (int64_t)b * a.w;
+      const double2 hv = hold(a.s, vb, a.Ws);
+      for (int aa = 0; aa < a.s; ++aa) {
+        const int64_t ua = u0 + (int64_t)aa * a.h;
+        const double2 K = phi_otf(a, Psm, b, ua);
+        const double2 hn = dcmul(hold(a.s, ua, a.Hs), hv);
+        const double2 kh = dcmul(K, hn);
+        mkh.x += kh.x;
+        mkh.y += kh.y;
+        mk2 += K.x * K.x + K.y * K.y;
+      }
+    }
+    mkh.x *= inv_s2;
+    mkh.y *= inv_s2;
+    const double D = mk2 * inv_s2 + lmb;
+    const double2 g = make_double2((1.0 - mkh.x) / D, -mkh.y / D);  // (1 - M(K Hn)) / D
+    for (int b = 0; b < a.s; ++b) {
+      const int64_t vb = v0 + (int64_t)b * a.w;
+      if (vb > a.Ws / 2) continue;
+      const double2 hv = hold(a.s, vb, a.Ws);
+      for (int aa = 0; aa < a.s; ++aa) {
+        const int64_t ua = u0 + (int64_t)aa * a.h;
+        const double2 K = phi_otf(a, Psm, b, ua);
+        const double2 hn = dcmul(hold(a.s, ua, a.Hs), hv);
+        const double2 t = dcmul(make_double2(K.x, -K.y), g);
+        const double2 ph = make_double2((hn.x + t.x) * norm, (hn.y + t.y) * norm);
+        a.phi[(cp * a.NCs + vb) * a.Hs + ua] = make_float2((float)ph.x, (float)ph.y);
+      }
+    }
+  }
+}
+
+// op-path tables over the full width: kf = K, phi = conj(K) / (M(|K|^2) + lambda) / (Hs Ws)
+__global__ void k_phi_op(PhiArgs a) {
+  extern __shared__ double2 Psm[];
+  const int64_t cp = blockIdx.x / a.nv0;
+  const int v0 = (int)(blockIdx.x - cp * a.nv0);
+  const int c = (int)(cp % a.C);
+  phi_row_sums(a, a.psf + cp * a.kh * a.kw, v0, Psm);
+  __syncthreads();
+  const double lmb = lambda_of(a, c);
+  const double inv_s2 = 1.0 / ((double)a.s * a.s);
+  const double norm = 1.0 / ((double)a.Hs * (double)a.Ws);
+  for (int u0 = threadIdx.x; u0 < a.h; u0 += blockDim.x) {
+    double mk2 = 0.0;
+    for (int b = 0; b < a.s; ++b)
+      for (int aa = 0; aa < a.s; ++aa) {
+        const double2 K = phi_otf(a, Psm, b, u0 + (int64_t)aa * a.h);
+        mk2 += K.x * K.x + K.y * K.y;
+      }
+    const double Dinv = norm / (mk2 * inv_s2 + lmb);
+    for (int b = 0; b < a.s; ++b) {
+      const int64_t vb = v0 + (int64_t)b * a.w;
+      for (int aa = 0; aa < a.s; ++aa) {
+        const int64_t ua = u0 + (int64_t)aa * a.h;
+        const double2 K = phi_otf(a, Psm, b, ua);
+        const int64_t o = (cp * a.Ws + vb) * a.Hs + ua;
+        a.kf[o] = make_float2((float)K.x, (float)K.y);
+        a.phi[o] = make_float2((float)(K.x * Dinv), (float)(-K.y * Dinv));
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Forward row pass: real rows of a (possibly padded) plane -> half spectrum S[plane][c][r]
+// ------------------------------------------------------------------------------------------------
+struct RowFwdArgs {
+  const float* x;  // (P, Hin, Win)
+  int Hin, Win, h, w, pad, mode;
+  int NC;          // w / 2 + 1
+  int rpb;         // rows per block (even)
+  FftPlan plan;    // length w
+  float2* S;       // (P, NC, h)
+};
+
+__global__ void __launch_bounds__(256) k_rows_fwd(RowFwdArgs a) {
+  extern __shared__ float2 sm[];
+  const int L = a.w, ntr = a.rpb / 2, ld = L + 2;
+  float2* tw = sm;
+  float2* A = tw + L;
+  float2* Bf = A + ntr * ld;
+  const int64_t plane = blockIdx.y;
+  const int r0 = blockIdx.x * a.rpb;
+  const int tid = threadIdx.x, nth = blockDim.x;
+  build_twiddles(tw, L, tid, nth);
+  const float* xp = a.x + plane * (int64_t)a.Hin * a.Win;
+  for (int idx = tid; idx < ntr * L; idx += nth) {
+    const int t = idx / L, c = idx - t * L;
+    const int ra = r0 + 2 * t, rb = ra + 1;
+    const int sc = pad_src(c, a.Win, a.pad, a.mode);
+    float va = 0.f, vb = 0.f;
+    if (sc >= 0) {
+      if (ra < a.h) {
+        const int sr = pad_src(ra, a.Hin, a.pad, a.mode);
+        if (sr >= 0) va = xp[(int64_t)sr * a.Win + sc];
+      }
+      if (rb < a.h) {
+        const int sr = pad_src(rb, a.Hin, a.pad, a.mode);
+        if (sr >= 0) vb = xp[(int64_t)sr * a.Win + sc];
+      }
+    }
+    A[t * L + c] = make_float2(va, vb);
+  }
+  __syncthreads();
+  const float2* Z = fft_lds<false>(a.plan, A, Bf, ntr, tw, tid, nth);
+  // unpack two real rows: Ya = (Z[c] + conj Z[-c]) / 2, Yb = (Z[c] - conj Z[-c]) / (2i)
+  float2* Sp = a.S + plane * (int64_t)a.NC * a.h;
+  for (int idx = tid; idx < a.NC * a.rpb; idx += nth) {
+    const int c = idx / a.rpb, rl = idx - c * a.rpb;
+    const int r = r0 + rl;
+    if (r >= a.h) continue;
+    const int t = rl >> 1;
+    const float2 z = Z[t * L + c];
+    const float2 zm = Z[t * L + (c == 0 ? 0 : L - c)];
+    float2 v;
+    if ((rl & 1) == 0)
+      v = make_float2(0.5f * (z.x + zm.x), 0.5f * (z.y - zm.y));
+    else
+      v = make_float2(0.5f * (z.y + zm.y), 0.5f * (zm.x - z.x));
+    Sp[(int64_t)c * a.h + r] = v;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Module column pass: per HR column v in [0, NCs): LR column FFT (h), tile to Hs, * Phi, inverse.
+// ------------------------------------------------------------------------------------------------
+struct ColModArgs {
+  const float2* S;    // (P, NC, h)
+  const float2* phi;  // (Cp, NCs, Hs)
+  float2* SH;         // (P, NCs, Hs)   (may alias S when s == 1)
+  int64_t C, psf_batch;
+  int h, w, Hs, Ws, NC, NCs, cpb;
+  FftPlan plan_h, plan_H;
+};
+
+__global__ void __launch_bounds__(256) k_cols_module(ColModArgs a) {
+  extern __shared__ float2 sm[];
+  const int tid = threadIdx.x, nth = blockDim.x;
+  float2* twh = sm;
+  float2* twH = twh + a.h;
+  float2* A = twH + a.Hs;
+  float2* Bf = A + a.cpb * a.Hs;
+  const int64_t plane = blockIdx.y;
+  const int v0 = blockIdx.x * a.cpb;
+  const int ncol = min(a.cpb, a.NCs - v0);
+  const int64_t cp = (a.psf_batch == 1) ? (plane % a.C) : plane;
+  build_twiddles(twh, a.h, tid, nth);
+  if (a.Hs != a.h) build_twiddles(twH, a.Hs, tid, nth);
+  const float2* tH = (a.Hs != a.h) ? twH : twh;
+  const float2* Sp = a.S + plane * (int64_t)a.NC * a.h;
+  for (int idx = tid; idx < a.cpb * a.h; idx += nth) {
+    const int cl = idx / a.h, u = idx - cl * a.h;
+    float2 val = make_float2(0.f, 0.f);
+    if (cl < ncol) {
+      const int vv = (v0 + cl) % a.w;
+      // row spectra of a real row are Hermitian in the column index (same row)
+      val = vv <= a.w / 2 ? Sp[(int64_t)vv * a.h + u] : cconj(Sp[(int64_t)(a.w - vv) * a.h + u]);
+    }
+    A[cl * a.h + u] = val;
+  }
+  __syncthreads();
+  float2* Y = fft_lds<false>(a.plan_h, A, Bf, a.cpb, twh, tid, nth);
+  float2* X = (Y == A) ? Bf : A;
+  const float2* ph = a.phi + cp * (int64_t)a.NCs * a.Hs;
+  for (int idx = tid; idx < a.cpb * a.Hs; idx += nth) {
+    const int cl = idx / a.Hs, u = idx - cl * a.Hs;
+    float2 val = make_float2(0.f, 0.f);
+    if (cl < ncol) val = cmul(Y[cl * a.h + (u % a.h)], ph[(int64_t)(v0 + cl) * a.Hs + u]);
+    X[cl * a.Hs + u] = val;
+  }
+  __syncthreads();
+  const float2* R = fft_lds<true>(a.plan_H, X, (X == A) ? Bf : A, a.cpb, tH, tid, nth);
+  float2* SHp = a.SH + plane * (int64_t)a.NCs * a.Hs;
+  for (int idx = tid; idx < ncol * a.Hs; idx += nth) {
+    const int cl = idx / a.Hs, u = idx - cl * a.Hs;
+    SHp[(int64_t)(v0 + cl) * a.Hs + u] = R[cl * a.Hs + u];
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Op column pass: one block per (plane, LR column class v0 in [0, w)); members v0 + b w.
+// ------------------------------------------------------------------------------------------------
+struct ColOpArgs {
+  const float2* S;    // (P, NC, h)      row spectra of y
+  const float2* S0;   // (P, NCs, Hs)    row spectra of x0
+  const float2* kf;   // (C, Ws, Hs)
+  const float2* A;    // (C, Ws, Hs)     conj(K) / D / (Hs Ws)
+  float2* SH;         // (P, NCs, Hs)
+  int64_t C;
+  int h, w, s, Hs, Ws, NC, NCs;
+  FftPlan plan_h, plan_H;
+};
+
+__global__ void __launch_bounds__(256) k_cols_op(ColOpArgs a) {
+  extern __shared__ float2 sm[];
+  const int tid = threadIdx.x, nth = blockDim.x;
+  float2* twh = sm;
+  float2* twH = twh + a.h;
+  float2* Ya = twH + a.Hs;             // h
+  float2* Yb = Ya + a.h;               // h
+  float2* Xa = Yb + a.h;               // s * Hs
+  float2* Xb = Xa + a.s * a.Hs;        // s * Hs
+  const int64_t plane = blockIdx.y;
+  const int v0 = blockIdx.x;
+  const int64_t c = plane % a.C;
+  // any member with an output column?
+  if (v0 > a.Ws / 2) return;  // member b = 0 is the smallest
+  build_twiddles(twh, a.h, tid, nth);
+  build_twiddles(twH, a.Hs, tid, nth);
+  const float2* Sp = a.S + plane * (int64_t)a.NC * a.h;
+  const float2* S0p = a.S0 + plane * (int64_t)a.NCs * a.Hs;
+  for (int u = tid; u < a.h; u += nth) {
+    Ya[u] = v0 <= a.w / 2 ? Sp[(int64_t)v0 * a.h + u] : cconj(Sp[(int64_t)(a.w - v0) * a.h + u]);
+  }
+  for (int idx = tid; idx < a.s * a.Hs; idx += nth) {
+    const int b = idx / a.Hs, u = idx - b * a.Hs;
+    const int vb = v0 + b * a.w;
+    Xa[b * a.Hs + u] = vb <= a.Ws / 2 ? S0p[(int64_t)vb * a.Hs + u]
+                                      : cconj(S0p[(int64_t)(a.Ws - vb) * a.Hs + u]);
+  }
+  __syncthreads();
+  const float2* Y = fft_lds<false>(a.plan_h, Ya, Yb, 1, twh, tid, nth);
+  float2* X0 = fft_lds<false>(a.plan_H, Xa, Xb, a.s, twH, tid, nth);
+  float2* Xo = (X0 == Xa) ? Xb : Xa;
+  const float2* kf = a.kf + c * (int64_t)a.Ws * a.Hs;
+  const float2* Am = a.A + c * (int64_t)a.Ws * a.Hs;
+  const float inv_s2 = 1.0f / (float)(a.s * a.s);
+  const float norm = 1.0f / ((float)a.Hs * (float)a.Ws);
+  for (int u0 = tid; u0 < a.h; u0 += nth) {
+    float2 m = make_float2(0.f, 0.f);
+    for (int b = 0; b < a.s; ++b)
+      for (int aa = 0; aa < a.s; ++aa) {
+        const int ua = u0 + aa * a.h;
+        const float2 t = cmul(kf[(int64_t)(v0 + b * a.w) * a.Hs + ua], X0[b * a.Hs + ua]);
+        m.x += t.x;
+        m.y += t.y;
+      }
+    const float2 d = make_float2(Y[u0].x - m.x * inv_s2, Y[u0].y - m.y * inv_s2);
+    for (int b = 0; b < a.s; ++b)
+      for (int aa = 0; aa < a.s; ++aa) {
+        const int ua = u0 + aa * a.h;
+        const float2 x0v = X0[b * a.Hs + ua];
+        const float2 t = cmul(Am[(int64_t)(v0 + b * a.w) * a.Hs + ua], d);
+        Xo[b * a.Hs + ua] = make_float2(fmaf(x0v.x, norm, t.x), fmaf(x0v.y, norm, t.y));
+      }
+  }
+  __syncthreads();
+  const float2* R = fft_lds<true>(a.plan_H, Xo, (Xo == Xa) ? Xb : Xa, a.s, twH, tid, nth);
+  float2* SHp = a.SH + plane * (int64_t)a.NCs * a.Hs;
+  for (int idx = tid; idx < a.s * a.Hs; idx += nth) {
+    const int b = idx / a.Hs, u = idx - b * a.Hs;
+    const int vb = v0 + b * a.w;
+    if (vb <= a.Ws / 2) SHp[(int64_t)vb * a.Hs + u] = R[b * a.Hs + u];
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Inverse row pass: half spectra SH[plane][v][u] -> real rows, crop + activation on store.
+// ------------------------------------------------------------------------------------------------
+struct RowInvArgs {
+  const float2* SH;  // (P, NCs, Hs)
+  float* out;        // (P, nrows, ncols)
+  int Hs, Ws, NCs;
+  int row0, nrows, col0, ncols;  // crop window
+  int rpb, act;
+  FftPlan plan;      // length Ws
+};
+
+__global__ void __launch_bounds__(256) k_rows_inv(RowInvArgs a) {
+  extern __shared__ float2 sm[];
+  const int tid = threadIdx.x, nth = blockDim.x;
+  const int L = a.Ws, ntr = a.rpb / 2, ld = L + 2;
+  float2* tw = sm;
+  float2* A = tw + L;
+  float2* Bf = A + ntr * ld;
+  const int64_t plane = blockIdx.y;
+  const int r0 = blockIdx.x * a.rpb;  // local output row
+  build_twiddles(tw, L, tid, nth);
+  const float2* SHp = a.SH + plane * (int64_t)a.NCs * a.Hs;
+  // stage the half spectra: Bf[rl * NCs + v]
+  for (int idx = tid; idx < a.NCs * a.rpb; idx += nth) {
+    const int v = idx / a.rpb, rl = idx - v * a.rpb;
+    const int r = r0 + rl;
+    float2 val = make_float2(0.f, 0.f);
+    if (r < a.nrows) val = SHp[(int64_t)v * a.Hs + a.row0 + r];
+    if (v == 0 || 2 * v == L) val.y = 0.f;
+    Bf[rl * a.NCs + v] = val;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < ntr * L; idx += nth) {
+    const int t = idx / L, v = idx - t * L;
+    const bool lo = v <= L / 2;
+    const int vv = lo ? v : L - v;
+    float2 ha = Bf[(2 * t) * a.NCs + vv], hb = Bf[(2 * t + 1) * a.NCs + vv];
+    if (!lo) { ha.y = -ha.y; hb.y = -hb.y; }
+    A[t * L + v] = make_float2(ha.x - hb.y, ha.y + hb.x);
+  }
+  __syncthreads();
+  const float2* Z = fft_lds<true>(a.plan, A, Bf, ntr, tw, tid, nth);
+  float* op = a.out + plane * (int64_t)a.nrows * a.ncols;
+  for (int idx = tid; idx < a.rpb * a.ncols; idx += nth) {
+    const int rl = idx / a.ncols, cc = idx - rl * a.ncols;
+    const int r = r0 + rl;
+    if (r >= a.nrows) continue;
+    const float2 z = Z[(rl >> 1) * L + a.col0 + cc];
+    float v = (rl & 1) ? z.y : z.x;
+    if (a.act == CVN_ACT_GELU) v = gelu_exact(v);
+    op[(int64_t)r * a.ncols + cc] = v;
+  }
+}
+
+// ================================================================================================
+// host side
+// ================================================================================================
+namespace {
+
+constexpr int kThreads = 256;
+constexpr size_t kLdsLimit = 160 * 1024;
+
+bool g_attr_done = false;
+void set_lds_attrs() {
+  if (g_attr_done) return;
+  hipFuncSetAttribute((const void*)k_rows_fwd, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+  hipFuncSetAttribute((const void*)k_cols_module, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+  hipFuncSetAttribute((const void*)k_cols_op, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+  hipFuncSetAttribute((const void*)k_rows_inv, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+  hipGetLastError();
+  g_attr_done = true;
+}
+
+// rows per block (even) for a row pass of length L
+int rows_per_block(int L, int nrows) {
+  int ntr = std::max(1, std::min(8, 2048 / std::max(L, 1)));
+  while (ntr > 1 && (size_t)(L + 2 * ntr * (L + 2)) * sizeof(float2) > 96 * 1024) --ntr;
+  int rpb = 2 * ntr;
+  while (rpb > 2 && rpb - 2 >= nrows) rpb -= 2;
+  return rpb;
+}
+size_t rows_lds(int L, int rpb) { return (size_t)(L + 2 * (rpb / 2) * (L + 2)) * sizeof(float2); }
+
+int cols_per_block(int h, int Hs) {
+  int cpb = std::max(1, std::min(16, 2048 / std::max(Hs, 1)));
+  while (cpb > 1 && (size_t)(h + Hs + 2 * cpb * Hs) * sizeof(float2) > 96 * 1024) --cpb;
+  return cpb;
+}
+size_t cols_lds(int h, int Hs, int cpb) { return (size_t)(h + Hs + 2 * cpb * Hs) * sizeof(float2); }
+
+struct Geo {
+  int64_t B, C, P, Cp;
+  int H, W, kh, kw, s, pad, h, w, Hs, Ws, NC, NCs;
+};
+
+int module_geo(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, int kh, int kw,
+               int scale, int pad, Geo* g) {
+  if (B < 0 || C < 1 || H < 1 || W < 1) return fail(CVN_ERR_ARG, "bad input shape");
+  if (kh < 1 || kw < 1) return fail(CVN_ERR_ARG, "bad psf shape");
+  if (psf_batch != 1 && psf_batch != B) return fail(CVN_ERR_ARG, "psf batch must be 1 or B");
+  if (scale < 1) return fail(CVN_ERR_ARG, "scale must be >= 1");
+  if (pad < 0) return fail(CVN_ERR_ARG, "padding must be >= 0");
+  g->B = B; g->C = C; g->P = B * C; g->Cp = psf_batch * C;
+  g->H = (int)H; g->W = (int)W; g->kh = kh; g->kw = kw; g->s = scale; g->pad = pad;
+  g->h = (int)H + 2 * pad; g->w = (int)W + 2 * pad;
+  g->Hs = g->h * scale; g->Ws = g->w * scale;
+  g->NC = g->w / 2 + 1; g->NCs = g->Ws / 2 + 1;
+  if (g->Hs > kMaxFftLen || g->Ws > kMaxFftLen)
+    return fail(CVN_ERR_UNSUPPORTED, "padded plane %dx%d exceeds %d", g->Hs, g->Ws, kMaxFftLen);
+  if ((int64_t)scale * kh > 4096 || kh > 1024 || kw > 1024)
+    return fail(CVN_ERR_UNSUPPORTED, "psf too large");
+  return CVN_OK;
+}
+
+struct ModWs {
+  size_t phi, S, SH, total;
+};
+ModWs module_ws(const Geo& g) {
+  ModWs w;
+  w.phi = 0;
+  size_t o = align_up((size_t)g.Cp * g.NCs * g.Hs * sizeof(float2));
+  w.S = o;
+  o += align_up((size_t)g.P * g.NC * g.h * sizeof(float2));
+  if (g.s == 1) {
+    w.SH = w.S;  // in-place column pass
+  } else {
+    w.SH = o;
+    o += align_up((size_t)g.P * g.NCs * g.Hs * sizeof(float2));
+  }
+  w.total = o;
+  return w;
+}
+
+int launch_phi(const float* psf, const float* bias, float eps, const Geo& g, bool op, float2* phi,
+               float2* kf, hipStream_t st) {
+  PhiArgs a;
+  a.psf = psf; a.bias = bias; a.Cp = g.Cp; a.C = (int)g.C; a.kh = g.kh; a.kw = g.kw; a.s = g.s;
+  a.h = g.h; a.w = g.w; a.Hs = g.Hs; a.Ws = g.Ws; a.NCs = g.NCs; a.eps = (double)eps;
+  a.phi = phi; a.kf = kf;
+  a.nv0 = (!op && g.s == 1) ? g.NC : g.w;
+  const size_t lds = (size_t)g.s * g.kh * sizeof(double2);
+  const int64_t blocks = g.Cp * a.nv0;
+  if (blocks > 0x7fffffff) return fail(CVN_ERR_UNSUPPORTED, "too many transfer blocks");
+  if (op)
+    hipLaunchKernelGGL(k_phi_op, dim3((unsigned)blocks), dim3(kThreads), lds, st, a);
+  else
+    hipLaunchKernelGGL(k_phi_module, dim3((unsigned)blocks), dim3(kThreads), lds, st, a);
+  return check_launch("transfer table");
+}
+
+int launch_rows_fwd(const float* x, int64_t P, int Hin, int Win, int pad, int mode, int h, int w,
+                    float2* S, hipStream_t st) {
+  RowFwdArgs a;
+  a.x = x; a.Hin = Hin; a.Win = Win; a.h = h; a.w = w; a.pad = pad; a.mode = mode;
+  a.NC = w / 2 + 1;
+  a.rpb = rows_per_block(w, h);
+  if (!make_plan(w, &a.plan)) return fail(CVN_ERR_UNSUPPORTED, "no plan for length %d", w);
+  a.S = S;
+  dim3 grid((h + a.rpb - 1) / a.rpb, (unsigned)P);
+  hipLaunchKernelGGL(k_rows_fwd, grid, dim3(kThreads), rows_lds(w, a.rpb), st, a);
+  return check_launch("row forward pass");
+}
+
+int launch_rows_inv(const float2* SH, const Geo& g, int row0, int nrows, int col0, int ncols,
+                    int act, float* out, hipStream_t st) {
+  RowInvArgs a;
+  a.SH = SH; a.out = out; a.Hs = g.Hs; a.Ws = g.Ws; a.NCs = g.NCs;
+  a.row0 = row0; a.nrows = nrows; a.col0 = col0; a.ncols = ncols; a.act = act;
+  a.rpb = rows_per_block(g.Ws, nrows);
+  if (!make_plan(g.Ws, &a.plan)) return fail(CVN_ERR_UNSUPPORTED, "no plan for length %d", g.Ws);
+  dim3 grid((nrows + a.rpb - 1) / a.rpb, (unsigned)g.P);
+  hipLaunchKernelGGL(k_rows_inv, grid, dim3(kThreads), rows_lds(g.Ws, a.rpb), st, a);
+  return check_launch("row inverse pass");
+}
+
+}  // namespace
+}  // namespace cvn
+
+using namespace cvn;
+
+extern "C" size_t cvn_converse2d_fwd_workspace(int64_t B, int64_t C, int64_t H, int64_t W,
+                                               int64_t psf_batch, int kh, int kw, int scale,
+                                               int pad) {
+  Geo g;
+  if (module_geo(B, C, H, W, psf_batch, kh, kw, scale, pad, &g) != CVN_OK) return 0;
+  return module_ws(g).total;
+}
+
+extern "C" int cvn_converse2d_fwd_f32(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
+                                      const float* psf, int64_t psf_batch, int kh, int kw,
+                                      const float* bias, float eps, int scale, int pad,
+                                      int pad_mode, int act, float* out, void* workspace,
+                                      size_t workspace_bytes, cvn_stream_t stream) {
+  Geo g;
+  int rc = module_geo(B, C, H, W, psf_batch, kh, kw, scale, pad, &g);
+  if (rc != CVN_OK) return rc;
+  if (pad_mode < CVN_PAD_ZEROS || pad_mode > CVN_PAD_CIRCULAR) return fail(CVN_ERR_ARG, "bad padding mode");
+  if (pad_mode == CVN_PAD_REFLECT && (pad >= H || pad >= W))
+    return fail(CVN_ERR_ARG, "reflect padding must be smaller than the input size");
+  if (pad_mode == CVN_PAD_CIRCULAR && (pad > H || pad > W))
+    return fail(CVN_ERR_ARG, "circular padding must not exceed the input size");
+  if (act != CVN_ACT_NONE && act != CVN_ACT_GELU) return fail(CVN_ERR_ARG, "bad activation");
+  if (!x || !psf || !bias || !out) return fail(CVN_ERR_ARG, "null pointer");
+  if (B == 0) return CVN_OK;
+  const ModWs ws = module_ws(g);
+  if (!workspace || workspace_bytes < ws.total)
+    return fail(CVN_ERR_WORKSPACE, "workspace too small: need %zu bytes", ws.total);
+  if (g.P > 65535) return fail(CVN_ERR_UNSUPPORTED, "B*C = %lld planes exceeds 65535", (long long)g.P);
+  set_lds_attrs();
+  hipStream_t st = (hipStream_t)stream;
+  char* base = (char*)workspace;
+  float2* phi = (float2*)(base + ws.phi);
+  float2* S = (float2*)(base + ws.S);
+  float2* SH = (float2*)(base + ws.SH);
+  if ((rc = launch_phi(psf, bias, eps, g, false, phi, nullptr, st)) != CVN_OK) return rc;
+  if ((rc = launch_rows_fwd(x, g.P, g.H, g.W, g.pad, pad_mode, g.h, g.w, S, st)) != CVN_OK) return rc;
+  ColModArgs ca;
+  ca.S = S; ca.phi = phi; ca.SH = SH; ca.C = g.C; ca.psf_batch = g.Cp / g.C;
+  ca.h = g.h; ca.w = g.w; ca.Hs = g.Hs; ca.Ws = g.Ws; ca.NC = g.NC; ca.NCs = g.NCs;
+  ca.cpb = cols_per_block(g.h, g.Hs);
+  if (!make_plan(g.h, &ca.plan_h) || !make_plan(g.Hs, &ca.plan_H))
+    return fail(CVN_ERR_UNSUPPORTED, "no plan for column length");
+  hipLaunchKernelGGL(k_cols_module, dim3((g.NCs + ca.cpb - 1) / ca.cpb, (unsigned)g.P), dim3(kThreads),
+                     cols_lds(g.h, g.Hs, ca.cpb), st, ca);
+  if ((rc = check_launch("column pass")) != CVN_OK) return rc;
+  const int ps = g.pad * g.s;
+  return launch_rows_inv(SH, g, ps, g.H * g.s, ps, g.W * g.s, act, out, st);
+}
+
+extern "C" size_t cvn_converse2d_op_workspace(int64_t B, int64_t C, int64_t h, int64_t w, int kh,
+                                              int kw, int scale) {
+  Geo g;
+  if (module_geo(B, C, h, w, 1, kh, kw, scale, 0, &g) != CVN_OK) return 0;
+  size_t o = 0;
+  o += 2 * align_up((size_t)g.C * g.Ws * g.Hs * sizeof(float2));  // kf, A
+  o += align_up((size_t)g.P * g.NC * g.h * sizeof(float2));        // S
+  o += align_up((size_t)g.P * g.NCs * g.Hs * sizeof(float2));      // S0
+  o += align_up((size_t)g.P * g.NCs * g.Hs * sizeof(float2));      // SH
+  return o;
+}
+
+extern "C" int cvn_converse2d_op_f32(const float* x, const float* x0, int64_t B, int64_t C,
+                                     int64_t h, int64_t w, const float* psf, int kh, int kw,
+                                     const float* bias, float eps, int scale, float* out,
+                                     void* workspace, size_t workspace_bytes,
+                                     cvn_stream_t stream) {
+  Geo g;
+  int rc = module_geo(B, C, h, w, 1, kh, kw, scale, 0, &g);
+  if (rc != CVN_OK) return rc;
+  if (!x || !x0 || !psf || !bias || !out) return fail(CVN_ERR_ARG, "null pointer");
+  if (B == 0) return CVN_OK;
+  const size_t need = cvn_converse2d_op_workspace(B, C, h, w, kh, kw, scale);
+  if (!workspace || workspace_bytes < need)
+    return fail(CVN_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
+  if (g.P > 65535) return fail(CVN_ERR_UNSUPPORTED, "B*C exceeds 65535");
+  set_lds_attrs();
+  hipStream_t st = (hipStream_t)stream;
+  char* base = (char*)workspace;
+  size_t o = 0;
+  float2* kf = (float2*)(base + o); o += align_up((size_t)g.C * g.Ws * g.Hs * sizeof(float2));
+  float2* Am = (float2*)(base + o); o += align_up((size_t)g.C * g.Ws * g.Hs * sizeof(float2));
+  float2* S = (float2*)(base + o); o += align_up((size_t)g.P * g.NC * g.h * sizeof(float2));
+  float2* S0 = (float2*)(base + o); o += align_up((size_t)g.P * g.NCs * g.Hs * sizeof(float2));
+  float2* SH = (float2*)(base + o);
+  if ((rc = launch_phi(psf, bias, eps, g, true, Am, kf, st)) != CVN_OK) return rc;
+  if ((rc = launch_rows_fwd(x, g.P, g.h, g.w, 0, CVN_PAD_ZEROS, g.h, g.w, S, st)) != CVN_OK) return rc;
+  if ((rc = launch_rows_fwd(x0, g.P, g.Hs, g.Ws, 0, CVN_PAD_ZEROS, g.Hs, g.Ws, S0, st)) != CVN_OK) return rc;
+  ColOpArgs ca;
+  ca.S = S; ca.S0 = S0; ca.kf = kf; ca.A = Am; ca.SH = SH; ca.C = g.C;
+  ca.h = g.h; ca.w = g.w; ca.s = g.s; ca.Hs = g.Hs; ca.Ws = g.Ws; ca.NC = g.NC; ca.NCs = g.NCs;
+  if (!make_plan(g.h, &ca.plan_h) || !make_plan(g.Hs, &ca.plan_H))
+    return fail(CVN_ERR_UNSUPPORTED, "no plan for column length");
+  const size_t lds = (size_t)(2 * g.h + g.Hs + 2 * g.h + 2 * g.s * g.Hs) * sizeof(float2);
+  if (lds > kLdsLimit) return fail(CVN_ERR_UNSUPPORTED, "column class does not fit in LDS");
+  hipLaunchKernelGGL(k_cols_op, dim3(g.w, (unsigned)g.P), dim3(kThreads), lds, st, ca);
+  if ((rc = check_launch("op column pass")) != CVN_OK) return rc;
+  return launch_rows_inv(SH, g, 0, g.Hs, 0, g.Ws, CVN_ACT_NONE, out, st);
+}

@@ -1,0 +1,279 @@
+// Device-side FFT building blocks for gfx950 (wave64): complex helpers, fixed-radix DFT butterflies,
+// and a mixed-radix Stockham pass over batches of transforms held in LDS.
+//
+// Conventions: forward transforms use exp(-2 pi i n k / L); inverse transforms use the conjugate
+// root and are unnormalised (callers fold 1/L into their spectral scale factor).  Twiddle tables
+// hold exp(-2 pi i m / L) for m in [0, L), evaluated in fp64 and rounded once to fp32, so no
+// fast-math sin/cos enters the transform.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cvn {
+
+__device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
+__device__ __forceinline__ float2 csub(float2 a, float2 b) { return make_float2(a.x - b.x, a.y - b.y); }
+__device__ __forceinline__ float2 cmul(float2 a, float2 b) {
+  return make_float2(fmaf(a.x, b.x, -(a.y * b.y)), fmaf(a.x, b.y, a.y * b.x));
+}
+__device__ __forceinline__ float2 cconj(float2 a) { return make_float2(a.x, -a.y); }
+__device__ __forceinline__ float2 cscale(float2 a, float s) { return make_float2(a.x * s, a.y * s); }
+// Multiply by -i (forward) or +i (inverse).
+template <bool INV>
+__device__ __forceinline__ float2 rot(float2 a) {
+  return INV ? make_float2(-a.y, a.x) : make_float2(a.y, -a.x);
+}
+template <bool INV>
+__device__ __forceinline__ float2 twid(float2 w) {  // table entry -> direction-specific root
+  return INV ? make_float2(w.x, -w.y) : w;
+}
+
+// cos / sin of 2 pi m / R, m in [0, R), for the odd prime radices (values computed in double and
+// rounded to float).
+template <int R> struct Roots;
+template <> struct Roots<3> {
+  static constexpr float c[3] = {1.0f, -0.5f, -0.5f};
+  static constexpr float s[3] = {0.0f, 0.8660254037844387f, -0.8660254037844387f};
+};
+template <> struct Roots<5> {
+  static constexpr float c[5] = {1.0f, 0.30901699437494745f, -0.8090169943749473f,
+                                 -0.8090169943749473f, 0.30901699437494745f};
+  static constexpr float s[5] = {0.0f, 0.9510565162951535f, 0.5877852522924732f,
+                                 -0.5877852522924732f, -0.9510565162951535f};
+};
+template <> struct Roots<7> {
+  static constexpr float c[7] = {1.0f, 0.6234898018587336f, -0.22252093395631434f,
+                                 -0.900968867902419f, -0.900968867902419f, -0.22252093395631434f,
+                                 0.6234898018587336f};
+  static constexpr float s[7] = {0.0f, 0.7818314824680298f, 0.9749279121818236f,
+                                 0.43388373911755823f, -0.43388373911755823f,
+                                 -0.9749279121818236f, -0.7818314824680298f};
+};
+template <> struct Roots<11> {
+  static constexpr float c[11] = {1.0f, 0.8412535328311812f, 0.41541501300188644f,
+                                  -0.142314838273285f, -0.654860733945285f, -0.9594929736144974f,
+                                  -0.9594929736144974f, -0.654860733945285f, -0.142314838273285f,
+                                  0.41541501300188644f, 0.8412535328311812f};
+  static constexpr float s[11] = {0.0f, 0.5406408174555976f, 0.9096319953545183f,
+                                  0.9898214418809328f, 0.7557495743542583f, 0.28173255684142967f,
+                                  -0.28173255684142967f, -0.7557495743542583f, -0.9898214418809328f,
+                                  -0.9096319953545183f, -0.5406408174555976f};
+};
+template <> struct Roots<13> {
+  static constexpr float c[13] = {1.0f, 0.8854560256532099f, 0.5680647467311559f,
+                                  0.120536680255323f, -0.35460488704253545f, -0.7485107481711012f,
+                                  -0.970941817426052f, -0.970941817426052f, -0.7485107481711012f,
+                                  -0.35460488704253545f, 0.120536680255323f, 0.5680647467311559f,
+                                  0.8854560256532099f};
+  static constexpr float s[13] = {0.0f, 0.4647231720437685f, 0.8229838658936564f,
+                                  0.992708874098054f, 0.9350162426854148f, 0.6631226582407952f,
+                                  0.23931566428755768f, -0.23931566428755768f, -0.6631226582407952f,
+                                  -0.9350162426854148f, -0.992708874098054f, -0.8229838658936564f,
+                                  -0.4647231720437685f};
+};
+
+// ----------------------------------------------------------------------------------------------
+// In-register DFTs of a fixed radix R on u[0..R-1] (in place, natural order in and out).
+// ----------------------------------------------------------------------------------------------
+template <int R, bool INV> struct Dft;
+
+template <bool INV> struct Dft<2, INV> {
+  static __device__ __forceinline__ void run(float2* u) {
+    float2 a = u[0], b = u[1];
+    u[0] = cadd(a, b);
+    u[1] = csub(a, b);
+  }
+};
+
+template <bool INV> struct Dft<4, INV> {
+  static __device__ __forceinline__ void run(float2* u) {
+    float2 s02 = cadd(u[0], u[2]), d02 = csub(u[0], u[2]);
+    float2 s13 = cadd(u[1], u[3]), d13 = rot<INV>(csub(u[1], u[3]));
+    u[0] = cadd(s02, s13);
+    u[2] = csub(s02, s13);
+    u[1] = cadd(d02, d13);
+    u[3] = csub(d02, d13);
+  }
+};
+
+template <bool INV> struct Dft<8, INV> {
+  static __device__ __forceinline__ void run(float2* u) {
+    constexpr float r = 0.70710678118654752f;
+    float2 e[4] = {u[0], u[2], u[4], u[6]};
+    float2 o[4] = {u[1], u[3], u[5], u[7]};
+    Dft<4, INV>::run(e);
+    Dft<4, INV>::run(o);
+    // o[k] *= w8^k  (w8 = exp(-+ 2 pi i / 8))
+    float2 o1 = INV ? make_float2(r * (o[1].x - o[1].y), r * (o[1].x + o[1].y))
+                    : make_float2(r * (o[1].x + o[1].y), r * (o[1].y - o[1].x));
+    float2 o2 = rot<INV>(o[2]);
+    float2 o3 = INV ? make_float2(-r * (o[3].x + o[3].y), r * (o[3].x - o[3].y))
+                    : make_float2(r * (o[3].y - o[3].x), -r * (o[3].x + o[3].y));
+    u[0] = cadd(e[0], o[0]);
+    u[4] = csub(e[0], o[0]);
+    u[1] = cadd(e[1], o1);
+    u[5] = csub(e[1], o1);
+    u[2] = cadd(e[2], o2);
+    u[6] = csub(e[2], o2);
+    u[3] = cadd(e[3], o3);
+    u[7] = csub(e[3], o3);
+  }
+};
+
+// Odd prime radix via conjugate-pair sums: X_q = A_q -+ i B_q, X_{R-q} = A_q +- i B_q with
+// A_q = u0 + sum_j cos(2 pi j q / R)(u_j + u_{R-j}),  B_q = sum_j sin(2 pi j q / R)(u_j - u_{R-j}).
+template <int R, bool INV> struct DftOdd {
+  static __device__ __forceinline__ void run(float2* u) {
+    constexpr int H = (R - 1) / 2;
+    float2 a[H], b[H];
+    float2 sum = u[0];
+#pragma unroll
+    for (int j = 1; j <= H; ++j) {
+      a[j - 1] = cadd(u[j], u[R - j]);
+      b[j - 1] = csub(u[j], u[R - j]);
+      sum = cadd(sum, a[j - 1]);
+    }
+    float2 out[R];
+    out[0] = sum;
+#pragma unroll
+    for (int q = 1; q <= H; ++q) {
+      float2 A = u[0], Bv = make_float2(0.f, 0.f);
+#pragma unroll
+      for (int j = 1; j <= H; ++j) {
+        const int m = (j * q) % R;
+        const float c = Roots<R>::c[m], s = Roots<R>::s[m];
+        A.x = fmaf(c, a[j - 1].x, A.x);
+        A.y = fmaf(c, a[j - 1].y, A.y);
+        Bv.x = fmaf(s, b[j - 1].x, Bv.x);
+        Bv.y = fmaf(s, b[j - 1].y, Bv.y);
+      }
+      if (!INV) {
+        out[q] = make_float2(A.x + Bv.y, A.y - Bv.x);
+        out[R - q] = make_float2(A.x - Bv.y, A.y + Bv.x);
+      } else {
+        out[q] = make_float2(A.x - Bv.y, A.y + Bv.x);
+        out[R - q] = make_float2(A.x + Bv.y, A.y - Bv.x);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < R; ++k) u[k] = out[k];
+  }
+};
+template <bool INV> struct Dft<3, INV> : DftOdd<3, INV> {};
+template <bool INV> struct Dft<5, INV> : DftOdd<5, INV> {};
+template <bool INV> struct Dft<7, INV> : DftOdd<7, INV> {};
+template <bool INV> struct Dft<11, INV> : DftOdd<11, INV> {};
+template <bool INV> struct Dft<13, INV> : DftOdd<13, INV> {};
+
+// ----------------------------------------------------------------------------------------------
+// FFT plan: a length L = prod(radix[i]) decomposed into Stockham passes.
+// ----------------------------------------------------------------------------------------------
+constexpr int kMaxStages = 24;
+struct FftPlan {
+  int L;
+  int nst;
+  int radix[kMaxStages];
+};
+
+// One radix-R Stockham pass over `ntr` transforms of length L stored back to back (src -> dst).
+// p is the product of the radices already applied.  Output position of butterfly i, leg j is
+// (i - k) * R + k + j * p with k = i mod p; leg j is pre-multiplied by exp(-+2 pi i j k / (p R)).
+template <int R, bool INV>
+__device__ void stockham_pass(const float2* __restrict__ src, float2* __restrict__ dst, int L, int p,
+                              int ntr, const float2* __restrict__ tw, int tid, int nth) {
+  const int T = L / R;
+  const int twstep = L / (p * R);
+  const int total = T * ntr;
+  for (int idx = tid; idx < total; idx += nth) {
+    const int t = idx / T;
+    const int i = idx - t * T;
+    const int k = i % p;
+    const float2* s = src + t * L;
+    float2* d = dst + t * L;
+    float2 u[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) u[j] = s[i + j * T];
+    if (p > 1) {
+#pragma unroll
+      for (int j = 1; j < R; ++j) u[j] = cmul(u[j], twid<INV>(tw[j * k * twstep]));
+    }
+    Dft<R, INV>::run(u);
+    const int j0 = (i - k) * R + k;
+#pragma unroll
+    for (int j = 0; j < R; ++j) d[j0 + j * p] = u[j];
+  }
+}
+
+// Same pass for any radix R (runtime), O(R^2) per butterfly; used for prime factors > 13.
+template <bool INV>
+__device__ void stockham_pass_generic(const float2* __restrict__ src, float2* __restrict__ dst, int L,
+                                      int R, int p, int ntr, const float2* __restrict__ tw, int tid,
+                                      int nth) {
+  const int T = L / R;
+  const int twstep = L / (p * R);
+  const int rstep = L / R;
+  const int total = T * ntr;
+  for (int idx = tid; idx < total; idx += nth) {
+    const int t = idx / T;
+    const int i = idx - t * T;
+    const int k = i % p;
+    const float2* s = src + t * L;
+    float2* d = dst + t * L;
+    const int j0 = (i - k) * R + k;
+    for (int q = 0; q < R; ++q) {
+      float2 acc = make_float2(0.f, 0.f);
+      int m = 0;  // (j * q) mod R
+      for (int j = 0; j < R; ++j) {
+        float2 v = s[i + j * T];
+        if (j > 0 && p > 1) v = cmul(v, twid<INV>(tw[j * k * twstep]));
+        const float2 w = twid<INV>(tw[m * rstep]);
+        acc.x = fmaf(v.x, w.x, fmaf(-v.y, w.y, acc.x));
+        acc.y = fmaf(v.x, w.y, fmaf(v.y, w.x, acc.y));
+        m += q;
+        if (m >= R) m -= R;
+      }
+      d[j0 + q * p] = acc;
+    }
+  }
+}
+
+// Runs the whole plan on `ntr` transforms held in buffer a (workspace b of equal size).  Returns
+// the buffer holding the result.  All threads of the block must call it; it synchronises.
+template <bool INV>
+__device__ float2* fft_lds(const FftPlan& plan, float2* a, float2* b, int ntr, const float2* tw,
+                           int tid, int nth) {
+  int p = 1;
+  float2* src = a;
+  float2* dst = b;
+  for (int st = 0; st < plan.nst; ++st) {
+    const int R = plan.radix[st];
+    switch (R) {
+      case 2: stockham_pass<2, INV>(src, dst, plan.L, p, ntr, tw, tid, nth); break;
+      case 3: stockham_pass<3, INV>(src, dst, plan.L, p, ntr, tw, tid, nth); break;
+      case 4: stockham_pass<4, INV>(src, dst, plan.L, p, ntr, tw, tid, nth); break;
+      case 5: stockham_pass<5, INV>(src, dst, plan.L, p, ntr, tw, tid, nth); break;
+      case 7: stockham_pass<7, INV>(src, dst, plan.L, p, ntr, tw, tid, nth); break;
+      case 8: stockham_pass<8, INV>(src, dst, plan.L, p, ntr, tw, tid, nth); break;
+      case 11: stockham_pass<11, INV>(src, dst, plan.L, p, ntr, tw, tid, nth); break;
+      case 13: stockham_pass<13, INV>(src, dst, plan.L, p, ntr, tw, tid, nth); break;
+      default: stockham_pass_generic<INV>(src, dst, plan.L, R, p, ntr, tw, tid, nth); break;
+    }
+    __syncthreads();
+    p *= R;
+    float2* t = src;
+    src = dst;
+    dst = t;
+  }
+  return src;
+}
+
+// exp(-2 pi i m / L) for m in [0, L), fp64-evaluated, written cooperatively into LDS.
+__device__ __forceinline__ void build_twiddles(float2* tw, int L, int tid, int nth) {
+  for (int m = tid; m < L; m += nth) {
+    double sn, cs;
+    sincospi(-2.0 * (double)m / (double)L, &sn, &cs);
+    tw[m] = make_float2((float)cs, (float)sn);
+  }
+}
+
+}  // namespace cvn

@@ -1,0 +1,195 @@
+"""Tensor-level wrappers over the HIP C ABI (fp32, HIP device tensors only, forward only).
+
+Each wrapper validates shapes the way the reference does (TORCH_CHECK -> RuntimeError,
+Converse2D/torch_converse2d/converse2d.cpp:167-172), makes inputs contiguous like the reference op
+(:174-177), allocates outputs and workspace through torch's caching allocator and enqueues the
+kernels on torch's current stream.  No CPU fallback exists here: a missing library raises.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_ws_cache: dict = {}
+
+
+def _stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _need_hip(*ts):
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError("conversenet_amd HIP path needs tensors on a HIP device")
+        if t.dtype != torch.float32:
+            raise RuntimeError("conversenet_amd HIP path computes in float32")
+
+
+def _workspace(dev, nbytes: int):
+    """A reusable uint8 scratch tensor per (device, stream); grows monotonically."""
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    buf = _ws_cache.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+        _ws_cache[key] = buf
+    return buf
+
+
+def release_workspace():
+    _ws_cache.clear()
+
+
+def converse2d_fused(x, weight, bias, scale=1, padding=2, padding_mode="circular", eps=1e-5, act=None):
+    """Converse2D.forward (util_converse.py:142-192) in one library call: pad, solve, crop.
+
+    x (B,C,H,W); weight (1,C,kh,kw) or (B,C,kh,kw) (per-sample psf, as ConvReverseDataNet);
+    bias (1,C,1,1) or (C,).  act='gelu' applies exact GELU to the output on store."""
+    lib = _lib.load()
+    _need_hip(x, weight, bias)
+    if x.dim() != 4:
+        raise RuntimeError("x must be (B,C,H,W)")
+    B, C, H, W = x.shape
+    if weight.dim() != 4 or weight.shape[1] != C or weight.shape[0] not in (1, B):
+        raise RuntimeError("weight must be (1,C,kh,kw) or (B,C,kh,kw)")
+    if bias.numel() != C:
+        raise RuntimeError("bias must hold C values")
+    if padding_mode not in _lib.PAD_MODES:
+        raise ValueError(f"unknown padding_mode {padding_mode!r}")
+    s = int(scale)
+    if s < 1:
+        raise RuntimeError("scale must be >= 1")
+    kh, kw = int(weight.shape[2]), int(weight.shape[3])
+    x = x.contiguous()
+    weight = weight.contiguous()
+    bias = bias.contiguous()
+    dev = x.device
+    out = torch.empty((B, C, H * s, W * s), dtype=torch.float32, device=dev)
+    if B == 0:
+        return out
+    nbytes = lib.cvn_converse2d_fwd_workspace(B, C, H, W, weight.shape[0], kh, kw, s, int(padding))
+    if nbytes == 0:
+        _lib.check(_lib.CVN_ERR_ARG, "converse2d_fused")
+    ws = _workspace(dev, nbytes)
+    rc = lib.cvn_converse2d_fwd_f32(
+        x.data_ptr(), B, C, H, W, weight.data_ptr(), weight.shape[0], kh, kw, bias.data_ptr(), float(eps), s,
+        int(padding), _lib.PAD_MODES[padding_mode], _lib.ACT_GELU if act == "gelu" else _lib.ACT_NONE,
+        out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
+    _lib.check(rc, "converse2d_fused")
+    return out
+
+
+def converse2d_op(x, x0, weight, bias, scale, eps=1e-5):
+    """The reference op (converse2d.cpp:165-209): x padded (B,C,h,w), x0 (B,C,h*s,w*s) arbitrary;
+    returns the uncropped (B,C,h*s,w*s) solution."""
+    lib = _lib.load()
+    if x.dim() != 4:
+        raise RuntimeError("x must be (B,C,H,W)")
+    if x0.dim() != 4:
+        raise RuntimeError("x0 must be (B,C,Hs,Ws)")
+    if weight.dim() != 4 or weight.size(0) != 1:
+        raise RuntimeError("weight must be (1,C,kh,kw)")
+    if bias.dim() != 4 or bias.size(0) != 1 or bias.size(2) != 1 or bias.size(3) != 1:
+        raise RuntimeError("bias must be (1,C,1,1)")
+    if not (x.device == x0.device == weight.device == bias.device):
+        raise RuntimeError("tensors on same device")
+    s = int(scale)
+    if s < 1:
+        raise RuntimeError("scale must be >= 1")
+    _need_hip(x, x0, weight, bias)
+    B, C, h, w = x.shape
+    if tuple(x0.shape) != (B, C, h * s, w * s) or weight.shape[1] != C or bias.shape[1] != C:
+        raise RuntimeError("shape mismatch between x, x0, weight and bias")
+    x, x0, weight, bias = x.contiguous(), x0.contiguous(), weight.contiguous(), bias.contiguous()
+    dev = x.device
+    out = torch.empty((B, C, h * s, w * s), dtype=torch.float32, device=dev)
+    if B == 0:
+        return out
+    kh, kw = int(weight.shape[2]), int(weight.shape[3])
+    nbytes = lib.cvn_converse2d_op_workspace(B, C, h, w, kh, kw, s)
+    if nbytes == 0:
+        _lib.check(_lib.CVN_ERR_ARG, "converse2d_op")
+    ws = _workspace(dev, nbytes)
+    rc = lib.cvn_converse2d_op_f32(x.data_ptr(), x0.data_ptr(), B, C, h, w, weight.data_ptr(), kh, kw,
+                                   bias.data_ptr(), float(eps), s, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                   _stream(dev))
+    _lib.check(rc, "converse2d_op")
+    return out
+
+
+def layernorm_cf(x, weight, bias, eps):
+    """LayerNorm(data_format='channels_first') (util_converse.py:63-68)."""
+    lib = _lib.load()
+    _need_hip(x, weight, bias)
+    x = x.contiguous()
+    B, C = x.shape[:2]
+    HW = x[0, 0].numel() if B > 0 else 0
+    y = torch.empty_like(x)
+    _lib.check(lib.cvn_layernorm_cf_f32(x.data_ptr(), B, C, HW, weight.contiguous().data_ptr(),
+                                        bias.contiguous().data_ptr(), float(eps), y.data_ptr(),
+                                        _stream(x.device)), "layernorm_cf")
+    return y
+
+
+def _wmat(weight):
+    return weight.reshape(weight.shape[0], -1).contiguous()
+
+
+def conv1x1(x, weight, bias=None, act=None, residual=None, res_scale=None, ln=None, out=None):
+    """act(W x + b) [then res_scale * . + residual]; nn.Conv2d(cin, cout, 1) semantics.
+    ln=(ln_weight, ln_bias, eps) applies channels-first LayerNorm to x first (fused prologue)."""
+    lib = _lib.load()
+    _need_hip(x, weight, bias, residual, res_scale)
+    x = x.contiguous()
+    B, Cin, H, W = x.shape
+    Wm = _wmat(weight)
+    Cout = Wm.shape[0]
+    if Wm.shape[1] != Cin:
+        raise RuntimeError("weight does not match input channels")
+    y = out if out is not None else torch.empty((B, Cout, H, W), dtype=torch.float32, device=x.device)
+    if residual is not None:
+        residual = residual.contiguous()
+    bptr = bias.contiguous().data_ptr() if bias is not None else None
+    rptr = residual.data_ptr() if residual is not None else None
+    sptr = res_scale.contiguous().data_ptr() if res_scale is not None else None
+    a = _lib.ACT_GELU if act == "gelu" else _lib.ACT_NONE
+    st = _stream(x.device)
+    if ln is None:
+        rc = lib.cvn_conv1x1_f32(x.data_ptr(), B, Cin, H * W, Wm.data_ptr(), bptr, Cout, a, rptr, sptr,
+                                 y.data_ptr(), st)
+    else:
+        lw, lb, leps = ln
+        rc = lib.cvn_ln_conv1x1_f32(x.data_ptr(), B, Cin, H * W, lw.contiguous().data_ptr(),
+                                    lb.contiguous().data_ptr(), float(leps), Wm.data_ptr(), bptr, Cout, a, rptr,
+                                    sptr, y.data_ptr(), st)
+    _lib.check(rc, "conv1x1")
+    return y
+
+
+def ln_mlp_residual(x, ln_w, ln_b, ln_eps, w1, b1, w2, b2, res_scale=None, out=None):
+    """x + res_scale * (W2 GELU(W1 LN(x) + b1) + b2): ConverseBlock.conv2 plus its residual."""
+    lib = _lib.load()
+    _need_hip(x, w1, b1, w2, b2, res_scale)
+    x = x.contiguous()
+    B, C, H, W = x.shape
+    W1 = _wmat(w1)
+    W2 = _wmat(w2)
+    y = out if out is not None else torch.empty_like(x)
+    rc = lib.cvn_ln_mlp_residual_f32(x.data_ptr(), B, C, H * W, ln_w.contiguous().data_ptr(),
+                                     ln_b.contiguous().data_ptr(), float(ln_eps), W1.data_ptr(),
+                                     b1.contiguous().data_ptr(), W1.shape[0], W2.data_ptr(),
+                                     b2.contiguous().data_ptr(),
+                                     res_scale.contiguous().data_ptr() if res_scale is not None else None,
+                                     y.data_ptr(), _stream(x.device))
+    _lib.check(rc, "ln_mlp_residual")
+    return y
+
+
+def copy_(dst, src):
+    """Plain device copy through the library (HBM calibration kernel)."""
+    lib = _lib.load()
+    _need_hip(dst, src)
+    _lib.check(lib.cvn_copy_f32(src.data_ptr(), dst.data_ptr(), src.numel(), _stream(src.device)), "copy")
+    return dst

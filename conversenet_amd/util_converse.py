@@ -1,0 +1,272 @@
+"""Drop-in replacement for the reference's models/util_converse.py, backed by the HIP library.
+
+Same public names, constructor signatures, parameter shapes and state-dict keys as the reference
+(models/util_converse.py): LayerNorm (:42-68), sequential (:71-91), Converse2D (:98-245),
+ConverseBlock (:253-293), ConverseBlockAlphaVariant (:296-323), ResidualBlock (:328-342).
+
+Dispatch (mirrors the reference's backend selection, util_converse.py:150-169):
+  * backend "auto": fp32 HIP tensors without a pending gradient run the fused HIP kernels;
+    anything else runs the PyTorch composition (the reference's own pure-PyTorch path).
+  * backend "cuda": requires the HIP library and a HIP tensor (RuntimeError otherwise, as :156-158).
+  * backend "pytorch": always the PyTorch composition.
+  * $CONVERSE2D_BACKEND overrides the module's backend (:150).
+The HIP kernels are forward-only; a forward that autograd must differentiate runs the composition.
+"""
+from __future__ import annotations
+
+import os
+from collections import OrderedDict
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib, composite, functional
+from . import op_registry  # noqa: F401  (registers torch.ops.converse2d)
+
+_HAS_CONVERSE2D_EXT = _lib.available()
+
+converse2d_CUDA = torch.ops.converse2d.forward
+
+# (Cin, Cout) tiles the MFMA 1x1 kernels are instantiated for; (C, Cmid) for the fused branch
+MFMA_SHAPES = {(64, 64), (64, 128), (128, 64), (128, 128), (16, 64), (64, 16), (32, 32), (32, 64), (64, 32)}
+MLP_SHAPES = {(64, 128), (32, 64)}
+
+
+def _backend(default: str) -> str:
+    return (os.environ.get("CONVERSE2D_BACKEND", "") or default).lower()
+
+
+def _hip_eligible(*ts) -> bool:
+    """True when the forward-only fp32 HIP kernels may run on these tensors."""
+    if not _HAS_CONVERSE2D_EXT:
+        return False
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda or t.dtype != torch.float32:
+            return False
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts):
+        return False
+    return True
+
+
+"""
+# --------------------------------------------
+# LayerNorm for Vision Normalization
+# --------------------------------------------
+"""
+
+
+class LayerNorm(nn.Module):
+    """LayerNorm over channels_last (F.layer_norm) or channels_first (util_converse.py:42-68)."""
+
+    def __init__(self, normalized_shape, eps=1e-6, data_format="channels_last"):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(normalized_shape))
+        self.bias = nn.Parameter(torch.zeros(normalized_shape))
+        self.eps = eps
+        self.data_format = data_format
+        if self.data_format not in ["channels_last", "channels_first"]:
+            raise NotImplementedError
+        self.normalized_shape = (normalized_shape,)
+
+    def forward(self, x):
+        if self.data_format == "channels_last":
+            return F.layer_norm(x, self.normalized_shape, self.weight, self.bias, self.eps)
+        if _hip_eligible(x, self.weight, self.bias) and x.dim() >= 2:
+            return functional.layernorm_cf(x, self.weight, self.bias, self.eps)
+        u = x.mean(1, keepdim=True)
+        s = (x - u).pow(2).mean(1, keepdim=True)
+        x = (x - u) / torch.sqrt(s + self.eps)
+        x = self.weight[:, None, None] * x + self.bias[:, None, None]
+        return x
+
+
+def sequential(*args):
+    """nn.Sequential that flattens nested Sequentials (util_converse.py:71-91)."""
+    if len(args) == 1:
+        if isinstance(args[0], OrderedDict):
+            raise NotImplementedError("sequential does not support OrderedDict input.")
+        return args[0]
+    modules = []
+    for module in args:
+        if isinstance(module, nn.Sequential):
+            for submodule in module.children():
+                modules.append(submodule)
+        elif isinstance(module, nn.Module):
+            modules.append(module)
+    return nn.Sequential(*modules)
+
+
+"""
+# --------------------------------------------
+# Converse2D operator
+# --------------------------------------------
+"""
+
+
+class Converse2D(nn.Module):
+    """Depthwise reverse convolution (util_converse.py:98-245).
+
+    Args match the reference: in_channels == out_channels (depthwise), kernel_size, scale (upsampling
+    factor), padding, padding_mode ('reflect' | 'replicate' | 'circular' | 'constant'), eps, backend
+    ('auto' | 'cuda' | 'pytorch').  Output (N, C, H*scale, W*scale).  Parameters: weight
+    (1, C, k, k), initialised as a softmax over the k*k taps of a standard normal draw; bias
+    (1, C, 1, 1) zeros; lambda = sigmoid(bias - 9) + eps is stored in self.biaseps on forward.
+    """
+
+    def __init__(self, in_channels, out_channels, kernel_size, scale=1, padding=2, padding_mode="circular",
+                 eps=1e-5, backend: str = "auto"):
+        super().__init__()
+        self.in_channels = in_channels
+        self.out_channels = out_channels
+        self.kernel_size = kernel_size
+        self.scale = scale
+        self.padding = padding
+        self.padding_mode = padding_mode
+        self.eps = eps
+        self.backend = backend.lower()
+        if self.backend not in ("auto", "cuda", "pytorch"):
+            raise ValueError(f"backend must be 'auto' | 'cuda' | 'pytorch', got: {self.backend}")
+        assert self.out_channels == self.in_channels
+        self.weight = nn.Parameter(torch.randn(1, self.in_channels, self.kernel_size, self.kernel_size))
+        self.bias = nn.Parameter(torch.zeros(1, self.in_channels, 1, 1))
+        self.weight.data = nn.functional.softmax(self.weight.data.view(1, self.in_channels, -1), dim=-1).view(
+            1, self.in_channels, self.kernel_size, self.kernel_size)
+
+    def _use_hip(self, x) -> bool:
+        backend = _backend(self.backend)
+        if backend == "cuda":
+            if not (_HAS_CONVERSE2D_EXT and x.is_cuda):
+                raise RuntimeError("Converse2D backend='cuda' but CUDA extension is unavailable.")
+            return _hip_eligible(x, self.weight, self.bias)
+        if backend == "pytorch":
+            return False
+        return _hip_eligible(x, self.weight, self.bias)
+
+    def forward(self, x, act=None):
+        """act='gelu' applies exact GELU to the output (fused on store on the HIP path)."""
+        self.biaseps = torch.sigmoid(self.bias - 9.0) + self.eps
+        if self._use_hip(x):
+            return functional.converse2d_fused(x, self.weight, self.bias.reshape(-1), self.scale, self.padding,
+                                               self.padding_mode, self.eps, act)
+        out = composite.converse2d_module(x, self.weight, self.bias, self.scale, self.padding, self.padding_mode,
+                                          self.eps)
+        return F.gelu(out) if act == "gelu" else out
+
+    # reference helpers kept for API parity (util_converse.py:194-245)
+    def splits(self, a, scale):
+        return composite.splits(a, scale)
+
+    def p2o(self, psf, shape):
+        return composite.p2o(psf, shape)
+
+    def upsample(self, x, scale=3):
+        return composite.upsample(x, scale)
+
+
+"""
+# --------------------------------------------
+# Converse Blocks
+# --------------------------------------------
+"""
+
+
+def _fused_block_forward(blk, x, alpha1=None, alpha2=None):
+    """LN+1x1+GELU -> Converse2D+GELU -> 1x1+residual -> fused LN-MLP branch + residual.
+    Returns None when a shape is outside the instantiated HIP tiles."""
+    ln1, c11, _, cv, _, c15 = blk.conv1
+    ln2, c21, _, c23 = blk.conv2
+    C = x.shape[1]
+    mid = c11.out_channels
+    if (C, mid) not in MFMA_SHAPES or (mid, C) not in MFMA_SHAPES or (C, c21.out_channels) not in MLP_SHAPES:
+        return None
+    if (x.shape[2] * x.shape[3]) % 4 != 0 or not isinstance(cv, Converse2D) or _backend(cv.backend) == "pytorch":
+        return None
+    t = functional.conv1x1(x, c11.weight, c11.bias, act="gelu", ln=(ln1.weight, ln1.bias, ln1.eps))
+    cv.biaseps = torch.sigmoid(cv.bias - 9.0) + cv.eps
+    t = functional.converse2d_fused(t, cv.weight, cv.bias.reshape(-1), cv.scale, cv.padding, cv.padding_mode,
+                                    cv.eps, act="gelu")
+    x = functional.conv1x1(t, c15.weight, c15.bias, residual=x,
+                           res_scale=alpha1.reshape(-1) if alpha1 is not None else None)
+    return functional.ln_mlp_residual(x, ln2.weight, ln2.bias, ln2.eps, c21.weight, c21.bias, c23.weight, c23.bias,
+                                      res_scale=alpha2.reshape(-1) if alpha2 is not None else None, out=x)
+
+
+def _block_params(blk):
+    return [p for p in blk.parameters()]
+
+
+class ConverseBlock(nn.Module):
+    """LN -> 1x1 -> GELU -> Converse2D -> GELU -> 1x1 (+x); LN -> 1x1 -> GELU -> 1x1 (+x)
+    (util_converse.py:253-293)."""
+
+    def __init__(self, in_channels, out_channels, kernel_size=3, scale=1, padding=2, padding_mode="replicate",
+                 eps=1e-5):
+        super().__init__()
+        self.conv1 = nn.Sequential(LayerNorm(in_channels, eps=1e-5, data_format="channels_first"),
+                                   nn.Conv2d(in_channels, 2 * out_channels, 1, 1, 0),
+                                   nn.GELU(),
+                                   Converse2D(2 * out_channels, 2 * out_channels, kernel_size, scale=scale,
+                                              padding=padding, padding_mode=padding_mode, eps=eps),
+                                   nn.GELU(),
+                                   nn.Conv2d(2 * out_channels, out_channels, 1, 1, 0))
+        self.conv2 = nn.Sequential(LayerNorm(in_channels, eps=1e-5, data_format="channels_first"),
+                                   nn.Conv2d(out_channels, 2 * out_channels, 1, 1, 0),
+                                   nn.GELU(),
+                                   nn.Conv2d(2 * out_channels, out_channels, 1, 1, 0))
+
+    def forward(self, x):
+        if _hip_eligible(x, *_block_params(self)) and self.conv1[3].scale == 1:
+            y = _fused_block_forward(self, x)
+            if y is not None:
+                return y
+        x = self.conv1(x) + x
+        x = self.conv2(x) + x
+        return x
+
+
+class ConverseBlockAlphaVariant(nn.Module):
+    """ConverseBlock with per-channel alpha scaling of both residual branches
+    (util_converse.py:296-323); alpha1/alpha2 initialise to zero."""
+
+    def __init__(self, in_channels, out_channels, kernel_size=3, scale=1, padding=2, padding_mode="replicate",
+                 eps=1e-5):
+        super().__init__()
+        self.alpha1 = nn.Parameter(torch.zeros((1, out_channels, 1, 1)), requires_grad=True)
+        self.alpha2 = nn.Parameter(torch.zeros((1, out_channels, 1, 1)), requires_grad=True)
+        self.conv1 = nn.Sequential(LayerNorm(in_channels, eps=1e-5, data_format="channels_first"),
+                                   nn.Conv2d(in_channels, 2 * out_channels, 1, 1, 0),
+                                   nn.GELU(),
+                                   Converse2D(2 * out_channels, 2 * out_channels, kernel_size, scale=scale,
+                                              padding=padding, padding_mode=padding_mode, eps=eps),
+                                   nn.GELU(),
+                                   nn.Conv2d(2 * out_channels, out_channels, 1, 1, 0))
+        self.conv2 = nn.Sequential(LayerNorm(in_channels, eps=1e-5, data_format="channels_first"),
+                                   nn.Conv2d(out_channels, 2 * out_channels, 1, 1, 0),
+                                   nn.GELU(),
+                                   nn.Conv2d(2 * out_channels, out_channels, 1, 1, 0))
+
+    def forward(self, x):
+        if _hip_eligible(x, *_block_params(self)) and self.conv1[3].scale == 1:
+            y = _fused_block_forward(self, x, self.alpha1, self.alpha2)
+            if y is not None:
+                return y
+        x = self.alpha1 * self.conv1(x) + x
+        x = self.alpha2 * self.conv2(x) + x
+        return x
+
+
+class ResidualBlock(nn.Module):
+    """---Conv-ReLU-Conv-+- (util_converse.py:328-342); plain torch convolutions."""
+
+    def __init__(self, num_features=64):
+        super().__init__()
+        self.conv1 = nn.Conv2d(num_features, num_features, 3, 1, 1, bias=True)
+        self.conv2 = nn.Conv2d(num_features, num_features, 3, 1, 1, bias=True)
+
+    def forward(self, x):
+        out = F.relu(self.conv1(x), inplace=True)
+        out = self.conv2(out)
+        return x + out

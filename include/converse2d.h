@@ -1,0 +1,116 @@
+/*
+ * converse2d.h -- C ABI of the MI355X (gfx950) Converse2D forward library (libcvn_hip.so).
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream, enqueues its kernels on
+ * that stream and returns without synchronising.  The caller owns all buffers; entry points that
+ * need scratch memory take a caller-provided workspace whose size a matching *_workspace() query
+ * returns (no entry point allocates device memory).  Entry points are re-entrant and keep no
+ * mutable global state apart from the per-thread error string.  Tensors are fp32, NCHW,
+ * contiguous.  Return value: CVN_OK, or a negative CVN_ERR_* code with a message retrievable
+ * through cvn_last_error() on the calling thread.
+ *
+ * Reference interfaces replaced (paths relative to the ConverseNet repository root):
+ *   cvn_converse2d_op_f32   <- converse2d_forward (Converse2D/torch_converse2d/converse2d.cpp:165-209),
+ *                              registered as converse2d::forward (converse2d.cpp:218-227)
+ *   cvn_converse2d_fwd_f32  <- Converse2D.forward (models/util_converse.py:142-192): padding
+ *                              (:144-145), x0 = nearest (:172-173), the solve (:175-187) and the crop
+ *                              (:189-190) in one call; also ConvReverseDataNet.forward
+ *                              (models/converse_usrnet.py:41-68) through psf_batch = B
+ *   cvn_layernorm_cf_f32    <- LayerNorm(data_format="channels_first").forward (util_converse.py:63-68)
+ *   cvn_conv1x1_f32         <- nn.Conv2d(cin, cout, 1, 1, 0) followed by nn.GELU() and/or a
+ *                              residual add, as composed in ConverseBlock (util_converse.py:278-292)
+ *                              and ConverseBlockAlphaVariant (util_converse.py:307-323)
+ *   cvn_clear_cache         <- clear_fb_cache / converse2d::clear_cache (converse2d.cpp:211-216,221)
+ */
+#ifndef CONVERSE2D_H_
+#define CONVERSE2D_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* cvn_stream_t; /* hipStream_t; NULL = default stream */
+
+enum {
+  CVN_OK = 0,
+  CVN_ERR_ARG = -1,         /* bad shape / argument (the reference raises RuntimeError) */
+  CVN_ERR_UNSUPPORTED = -2, /* valid for the reference but outside this library's limits */
+  CVN_ERR_WORKSPACE = -3,   /* workspace missing or smaller than the *_workspace() query */
+  CVN_ERR_HIP = -4          /* a HIP runtime call or kernel launch failed */
+};
+
+/* padding_mode of Converse2D (util_converse.py:112): F.pad modes */
+enum { CVN_PAD_ZEROS = 0, CVN_PAD_REFLECT = 1, CVN_PAD_REPLICATE = 2, CVN_PAD_CIRCULAR = 3 };
+
+/* activation applied to an output on store */
+enum { CVN_ACT_NONE = 0, CVN_ACT_GELU = 1 };
+
+const char* cvn_version(void);
+const char* cvn_last_error(void);
+
+/* Module-level fused forward.  x: (B,C,H,W).  psf: (psf_batch,C,kh,kw) with psf_batch 1 (shared,
+ * Converse2D.weight) or B (per-sample, ConvReverseDataNet's k).  bias: (C) (Converse2D.bias or
+ * ConvReverseDataNet.alpha), lambda = sigmoid(bias - 9) + eps.  The input is padded by `pad` on
+ * every side with `pad_mode`, upsampled by `scale`, solved, and cropped back:
+ * out: (B,C,H*scale,W*scale).  act = CVN_ACT_GELU applies exact GELU on store. */
+size_t cvn_converse2d_fwd_workspace(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch,
+                                    int kh, int kw, int scale, int pad);
+int cvn_converse2d_fwd_f32(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
+                           const float* psf, int64_t psf_batch, int kh, int kw, const float* bias,
+                           float eps, int scale, int pad, int pad_mode, int act, float* out,
+                           void* workspace, size_t workspace_bytes, cvn_stream_t stream);
+
+/* Op-level forward with the reference op's semantics: x (B,C,h,w) is the already padded input,
+ * x0 (B,C,h*scale,w*scale) is arbitrary, psf (1,C,kh,kw), bias (C).  out: (B,C,h*scale,w*scale),
+ * uncropped. */
+size_t cvn_converse2d_op_workspace(int64_t B, int64_t C, int64_t h, int64_t w, int kh, int kw,
+                                   int scale);
+int cvn_converse2d_op_f32(const float* x, const float* x0, int64_t B, int64_t C, int64_t h,
+                          int64_t w, const float* psf, int kh, int kw, const float* bias,
+                          float eps, int scale, float* out, void* workspace,
+                          size_t workspace_bytes, cvn_stream_t stream);
+
+/* The reference keeps an OTF cache (converse2d.cpp:52-102); this library evaluates the transfer
+ * function on every call and keeps none, so clearing is a no-op kept for API parity. */
+int cvn_clear_cache(void);
+
+/* y = weight[c] * (x - mean_c) / sqrt(var_c + eps) + bias[c], statistics over C per pixel.
+ * x, y: (B,C,HW). */
+int cvn_layernorm_cf_f32(const float* x, int64_t B, int64_t C, int64_t HW, const float* weight,
+                         const float* bias, float eps, float* y, cvn_stream_t stream);
+
+/* y[b,o,p] = act(sum_c W[o,c] x[b,c,p] + bias[o]);  then, if residual != NULL,
+ * y = (res_scale ? res_scale[o] : 1) * y + residual[b,o,p].  x: (B,Cin,HW), W: (Cout,Cin),
+ * bias: (Cout) or NULL, residual: (B,Cout,HW) or NULL, res_scale: (Cout) or NULL.
+ * y may alias residual.  Uses fp32 MFMA. */
+int cvn_conv1x1_f32(const float* x, int64_t B, int64_t Cin, int64_t HW, const float* weight,
+                    const float* bias, int64_t Cout, int act, const float* residual,
+                    const float* res_scale, float* y, cvn_stream_t stream);
+
+/* LayerNorm (channels_first) fused into the prologue of a 1x1 conv: the ConverseBlock front end
+ * LN -> nn.Conv2d(cin, cout, 1) -> GELU (util_converse.py:278-280, 285-287).  Arguments as in
+ * cvn_conv1x1_f32 plus the LayerNorm affine (Cin) and eps. */
+int cvn_ln_conv1x1_f32(const float* x, int64_t B, int64_t Cin, int64_t HW, const float* ln_w,
+                       const float* ln_b, float ln_eps, const float* weight, const float* bias,
+                       int64_t Cout, int act, const float* residual, const float* res_scale,
+                       float* y, cvn_stream_t stream);
+
+/* The whole ConverseBlock conv2 branch with its residual (util_converse.py:285-288,292 and the
+ * alpha-scaled form :314-317,322): y = x + res_scale * (W2 GELU(W1 LN(x) + b1) + b2).
+ * x, y: (B,C,HW) (y may alias x), w1: (Cmid,C), w2: (C,Cmid), res_scale: (C) or NULL. */
+int cvn_ln_mlp_residual_f32(const float* x, int64_t B, int64_t C, int64_t HW, const float* ln_w,
+                            const float* ln_b, float ln_eps, const float* w1, const float* b1,
+                            int64_t Cmid, const float* w2, const float* b2,
+                            const float* res_scale, float* y, cvn_stream_t stream);
+
+/* Plain device copy of n floats (bandwidth calibration). */
+int cvn_copy_f32(const float* src, float* dst, int64_t n, cvn_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CONVERSE2D_H_ */

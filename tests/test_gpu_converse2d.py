@@ -1,0 +1,94 @@
+"""HIP Converse2D forward vs the fp64 oracle (parity gate: max-abs <= 1e-4)."""
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import converse_oracle as O
+from tests.conftest import softmax_psf
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+MODES = ["circular", "reflect", "replicate", "constant"]
+
+
+def _run_fused(x, w, b, s, p, mode, eps):
+    from conversenet_amd import functional as Fh
+    dev = torch.device("cuda")
+    out = Fh.converse2d_fused(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev),
+                              torch.from_numpy(b).reshape(-1).to(dev), s, p, mode, eps)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+# the reference's test_error.py grid (B, C, H, W, k, s), padding k // 2, circular
+GRID = list(itertools.product([1, 2], [2, 3], [16, 32], [18, 40], [3, 5], [1, 2, 3]))
+
+
+@pytest.mark.parametrize("B,C,H,W,k,s", GRID)
+def test_reference_grid(B, C, H, W, k, s):
+    rng = np.random.default_rng(hash((B, C, H, W, k, s)) % (2 ** 32))
+    x = rng.standard_normal((B, C, H, W)).astype(np.float32)
+    w = softmax_psf(rng, C, k)
+    b = (0.3 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    ref = O.converse2d_module(x, w, b, s, k // 2, "circular", 1e-5)
+    got = _run_fused(x, w, b, s, k // 2, "circular", 1e-5)
+    assert got.shape == ref.shape
+    err = np.abs(got - ref).max()
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("s", [1, 2, 3, 4])
+@pytest.mark.parametrize("k", [2, 3, 4, 5, 7])
+def test_padding_modes_scales_kernels(mode, s, k):
+    rng = np.random.default_rng(1000 + 10 * s + k)
+    H, W = 13, 17
+    p = min(k - 1, 4)
+    x = rng.standard_normal((2, 3, H, W)).astype(np.float32)
+    w = softmax_psf(rng, 3, k)
+    b = (0.5 * rng.standard_normal((1, 3, 1, 1))).astype(np.float32)
+    ref = O.converse2d_module(x, w, b, s, p, mode, 1e-5)
+    got = _run_fused(x, w, b, s, p, mode, 1e-5)
+    assert np.abs(got - ref).max() <= TOL
+
+
+def test_cfg1_shape():
+    rng = np.random.default_rng(0)
+    x = rng.random((1, 64, 128, 128), dtype=np.float32)
+    w = softmax_psf(np.random.default_rng(1), 64, 5)
+    b = np.zeros((1, 64, 1, 1), np.float32)
+    ref = O.converse2d_module(x, w, b, 1, 2, "circular", 1e-5)
+    got = _run_fused(x, w, b, 1, 2, "circular", 1e-5)
+    err = np.abs(got - ref).max()
+    print("cfg1 max-abs vs fp64 oracle:", err)
+    assert err <= TOL
+
+
+def test_cfg2_shape():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((8, 64, 64, 64)).astype(np.float32)
+    w = softmax_psf(np.random.default_rng(1), 64, 3)
+    b = np.zeros((1, 64, 1, 1), np.float32)
+    ref = O.converse2d_module(x, w, b, 2, 1, "circular", 1e-5)
+    got = _run_fused(x, w, b, 2, 1, "circular", 1e-5)
+    err = np.abs(got - ref).max()
+    print("cfg2 max-abs vs fp64 oracle:", err)
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("s", [1, 2, 3])
+def test_op_level_arbitrary_x0(s):
+    from conversenet_amd import functional as Fh
+    rng = np.random.default_rng(7 + s)
+    B, C, h, w, k = 2, 3, 20, 22, 5
+    x = rng.standard_normal((B, C, h, w)).astype(np.float32)
+    x0 = rng.standard_normal((B, C, h * s, w * s)).astype(np.float32)
+    wt = softmax_psf(rng, C, k)
+    b = (0.3 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    ref = O.converse2d_op(x, x0, wt, b, s, 1e-5)
+    dev = torch.device("cuda")
+    got = Fh.converse2d_op(*(torch.from_numpy(a).to(dev) for a in (x, x0, wt, b)), s, 1e-5).cpu().numpy()
+    assert np.abs(got - ref).max() <= TOL
