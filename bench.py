@@ -1,0 +1,287 @@
+#!/usr/bin/env python3
+"""Benchmark of the Converse2D forward hot path on one MI355X.
+
+Headline (value): Converse2D forward throughput in Gpix*ch/s on the roofline workload
+(BASELINE cfg3): B=16, C=64, 256x256, k=5, scale=1, padding=2 circular, fp32, synthetic N(0,1)
+input, softmax-normalised seeded psf, zero bias.  One step = one module-level Converse2D forward
+of that batch (padding, solve and crop fused; inputs resident in HBM).
+
+The same JSON line carries:
+  roofline      the Converse2D kernel's algorithmic bytes / measured average duration (HIP events on
+                the launch stream) against 8 TB/s, plus HBM traffic per launch from the committed
+                rocprofv3 PMC summary (profiles/traffic.json) when present
+  cpu_baseline  the reference's own C++ op (oracle/_ref, built from the reference source) timed on
+                this host's cores on the same workload, in a subprocess (its op namespace collides
+                with this package's); falls back to the numpy oracle ("port") if it is not built
+  extra         LayerNorm and 1x1+GELU rooflines at the cfg3 shape, Converse-DnCNN (cfg4) images/s
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-model]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+HBM_PEAK = 8.0e12
+FP32_MFMA_PEAK = 157.3e12
+
+CFG3 = dict(B=16, C=64, H=256, W=256, k=5, scale=1, padding=2, mode="circular", eps=1e-5)
+
+
+def cfg3_bytes(c=CFG3):
+    B, C, H, W, k, s = c["B"], c["C"], c["H"], c["W"], c["k"], c["scale"]
+    return 4 * B * C * H * W + 4 * B * C * H * s * W * s + 4 * C * (k * k + 1)
+
+
+def make_cfg3_inputs(torch, c=CFG3):
+    """Seeded on the CPU (generator seeds 0 and 1) so the GPU run and the CPU baseline see the same
+    tensors."""
+    g0 = torch.Generator().manual_seed(0)
+    x = torch.randn(c["B"], c["C"], c["H"], c["W"], generator=g0)
+    g1 = torch.Generator().manual_seed(1)
+    w = torch.softmax(torch.randn(1, c["C"], c["k"] * c["k"], generator=g1), dim=-1)
+    w = w.reshape(1, c["C"], c["k"], c["k"])
+    b = torch.zeros(1, c["C"], 1, 1)
+    return x, w, b
+
+
+# ------------------------------------------------------------------------------------------------
+# CPU baseline worker (separate process: loads the reference op library, never this package)
+# ------------------------------------------------------------------------------------------------
+def cpu_worker(args):
+    import torch
+    import torch.nn.functional as F
+
+    cores = min(os.cpu_count() or 1, args.cpu_threads)
+    torch.set_num_threads(cores)
+    c = dict(CFG3)
+    x, w, b = make_cfg3_inputs(torch, c)
+    p, s = c["padding"], c["scale"]
+    ref_so = os.path.join(ROOT, "oracle", "_ref", "converse2d_ref.so")
+    if os.path.exists(ref_so):
+        torch.ops.load_library(ref_so)
+        kind = "reference"
+
+        def step():
+            y = F.pad(x, [p] * 4, mode=c["mode"])
+            x0 = y if s == 1 else F.interpolate(y, scale_factor=s, mode="nearest")
+            out = torch.ops.converse2d.forward(y, x0, w, b, s, c["eps"])
+            return out[..., p * s:-p * s, p * s:-p * s]
+    else:
+        sys.path.insert(0, ROOT)
+        import numpy as np
+
+        from oracle import converse_oracle as O
+        kind = "port"
+        xn, wn, bn = x.numpy(), w.numpy(), b.numpy()
+
+        def step():
+            return O.converse2d_module(xn, wn, bn, s, p, c["mode"], c["eps"], np.float32)
+
+    times = []
+    with torch.no_grad():
+        step()  # warmup
+        for _ in range(args.cpu_iters):
+            t0 = time.perf_counter()
+            step()
+            times.append(time.perf_counter() - t0)
+    mean = statistics.mean(times)
+    npix = c["B"] * c["C"] * c["H"] * s * c["W"] * s
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    print(json.dumps({
+        "value": npix / mean / 1e9, "unit": "Gpix*ch/s", "cores": torch.get_num_threads(), "kind": kind,
+        "sample": f"cfg3 full batch (B16 C64 256x256 k5 s1 p2 circular, fp32), F.pad + reference "
+                  f"converse2d::forward + crop, 1 warmup + {args.cpu_iters} timed calls, mean",
+        "ms_per_call": mean * 1e3, "p50_ms": statistics.median(times) * 1e3, "cpu_model": cpu_model,
+        "os_cpu_count": os.cpu_count()}))
+
+
+def run_cpu_baseline(args):
+    cmd = [sys.executable, os.path.abspath(__file__), "--cpu-worker", "--cpu-iters", str(args.cpu_iters),
+           "--cpu-threads", str(args.cpu_threads)]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        return {"value": None, "error": r.stderr[-400:]}
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+# ------------------------------------------------------------------------------------------------
+# GPU measurements
+# ------------------------------------------------------------------------------------------------
+def time_events(torch, fn, iters):
+    """Average duration per call from HIP events on the current stream (the library launches on it)."""
+    st = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(iters):
+        fn()
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / iters * 1e-3
+
+
+def load_traffic(name):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def bench_model(torch, dev, iters=3):
+    """Converse-DnCNN (cfg4): default constructor (k7, p6, circular, 20 blocks, 796,353 params),
+    random init (seed 0), B=8 1x256x256 synthetic noisy input; images/s."""
+    sys.path.insert(0, ROOT)
+    from conversenet_amd.converse_dncnn import ConverseDnCNN
+
+    torch.manual_seed(0)
+    m = ConverseDnCNN().to(dev).eval()
+    g = torch.Generator().manual_seed(0)
+    x = (torch.rand(8, 1, 256, 256, generator=g) + torch.randn(8, 1, 256, 256, generator=g) * (25 / 255)).to(dev)
+    with torch.no_grad():
+        m(x)
+        torch.cuda.synchronize()
+        t = time_events(torch, lambda: m(x), iters)
+    return {"workload": "cfg4 Converse-DnCNN B8 1x256x256 fp32 (k7 p6, 20 blocks)", "ms_per_batch": t * 1e3,
+            "images_per_s": 8 / t, "params": sum(p.numel() for p in m.parameters()), "iters": iters}
+
+
+def only_kernel(torch, Fh, args, dev, x, step):
+    """Runs one kernel family alone (warmup + steps) for rocprofv3 runs; prints a short JSON line.
+    copy: the calibration copy kernel over COPY_FLOATS floats (bytes moved = 8 * COPY_FLOATS)."""
+    if args.only == "converse2d":
+        fn = step
+    elif args.only == "layernorm":
+        lw, lb = torch.ones(64, device=dev), torch.zeros(64, device=dev)
+        fn = lambda: Fh.layernorm_cf(x, lw, lb, 1e-6)
+    elif args.only == "conv1x1":
+        torch.manual_seed(2)
+        conv = torch.nn.Conv2d(64, 64, 1).to(dev)
+        fn = lambda: Fh.conv1x1(x, conv.weight, conv.bias, act="gelu")
+    elif args.only == "copy":
+        src = torch.randn(COPY_FLOATS, device=dev)
+        dst = torch.empty_like(src)
+        fn = lambda: Fh.copy_(dst, src)
+    else:
+        raise SystemExit(f"unknown --only {args.only}")
+    for _ in range(args.warmup):
+        fn()
+    torch.cuda.synchronize()
+    t = time_events(torch, fn, args.steps)
+    print(json.dumps({"only": args.only, "steps": args.steps, "ms_per_call": t * 1e3}))
+    return 0
+
+
+COPY_FLOATS = 64 * 1024 * 1024  # 256 MiB read + 256 MiB written per copy
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-model", action="store_true")
+    ap.add_argument("--cpu-worker", action="store_true")
+    ap.add_argument("--cpu-iters", type=int, default=3)
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--only", choices=["converse2d", "layernorm", "conv1x1", "copy"],
+                    help="run one kernel family alone (for rocprofv3)")
+    args = ap.parse_args()
+
+    if args.cpu_worker:
+        cpu_worker(args)
+        return 0
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the Converse2D path shards over the batch with no exchange, "
+              "so every GPU runs this same per-GPU workload; run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from conversenet_amd import functional as Fh
+
+    dev = torch.device("cuda", 0)
+    c = CFG3
+    x, w, b = (t.to(dev) for t in make_cfg3_inputs(torch))
+    bias = b.reshape(-1)
+
+    def step():
+        return Fh.converse2d_fused(x, w, bias, c["scale"], c["padding"], c["mode"], c["eps"])
+
+    if args.only:
+        return only_kernel(torch, Fh, args, dev, x, step)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    per_call = time_events(torch, step, args.steps)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+    npix = c["B"] * c["C"] * c["H"] * c["scale"] * c["W"] * c["scale"]
+    nbytes = cfg3_bytes()
+    achieved = nbytes / per_call
+    roofline = {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK, "traffic": load_traffic("converse2d_cfg3"),
+                "kernel": "converse2d forward (all launches of one call)", "bytes_per_launch": nbytes}
+
+    extra = {}
+    # LayerNorm (eps 1e-6) and 1x1 64->64 + GELU at the cfg3 shape
+    lw = torch.ones(c["C"], device=dev)
+    lb = torch.zeros(c["C"], device=dev)
+    t_ln = time_events(torch, lambda: Fh.layernorm_cf(x, lw, lb, 1e-6), max(10, args.steps // 2))
+    ln_bytes = 8 * x.numel() + 8 * c["C"]
+    torch.manual_seed(2)
+    conv = torch.nn.Conv2d(64, 64, 1).to(dev)
+    t_cv = time_events(torch, lambda: Fh.conv1x1(x, conv.weight, conv.bias, act="gelu"), max(10, args.steps // 2))
+    cv_bytes = 4 * x.numel() * 2 + 4 * (64 * 64 + 64)
+    cv_flops = 2 * x.numel() * 64
+    extra["layernorm_cf"] = {"ms": t_ln * 1e3, "GB/s": ln_bytes / t_ln / 1e9, "frac_hbm": ln_bytes / t_ln / HBM_PEAK}
+    extra["conv1x1_gelu_64"] = {"ms": t_cv * 1e3, "GB/s": cv_bytes / t_cv / 1e9,
+                                "frac_hbm": cv_bytes / t_cv / HBM_PEAK, "TFLOP/s": cv_flops / t_cv / 1e12,
+                                "frac_mfma": cv_flops / t_cv / FP32_MFMA_PEAK}
+    if not args.no_model:
+        extra["converse_dncnn"] = bench_model(torch, dev)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = run_cpu_baseline(args)
+
+    line = {
+        "metric": "Converse2D fwd Gpix*ch/s", "value": npix / per_call / 1e9, "unit": "Gpix*ch/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": per_call * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": "cfg3 Converse2D forward B16 C64 256x256 k5 s1 p2 circular (module-level: pad, "
+                               "solve, crop)", "B": c["B"], "C": c["C"], "H": c["H"], "W": c["W"], "k": c["k"],
+                   "scale": c["scale"], "padding": c["padding"], "padding_mode": c["mode"], "parallelism": "none"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "wall_ms_per_step": wall * 1e3,
+        "extra": extra,
+        "host": platform.node(),
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

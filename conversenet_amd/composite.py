@@ -60,8 +60,25 @@ def solve(x, x0, weight, lmb, scale):
     return torch.real(torch.fft.ifftn(FX, dim=(-2, -1)))
 
 
+def check_op_args(x, x0, weight, bias, scale):
+    """The reference op's argument checks (converse2d.cpp:167-172), raising RuntimeError."""
+    if x.dim() != 4:
+        raise RuntimeError("x must be (B,C,H,W)")
+    if x0.dim() != 4:
+        raise RuntimeError("x0 must be (B,C,Hs,Ws)")
+    if weight.dim() != 4 or weight.size(0) != 1:
+        raise RuntimeError("weight must be (1,C,kh,kw)")
+    if bias.dim() != 4 or bias.size(0) != 1 or bias.size(2) != 1 or bias.size(3) != 1:
+        raise RuntimeError("bias must be (1,C,1,1)")
+    if not (x.device == x0.device == weight.device == bias.device):
+        raise RuntimeError("tensors on same device")
+    if int(scale) < 1:
+        raise RuntimeError("scale must be >= 1")
+
+
 def converse2d_op(x, x0, weight, bias, scale, eps=1e-5):
     """converse2d::forward semantics (converse2d.cpp:165-209)."""
+    check_op_args(x, x0, weight, bias, scale)
     return solve(x, x0, weight, torch.sigmoid(bias - 9.0) + eps, scale)
 
 

@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
+from . import _lib, composite
 
 _ws_cache: dict = {}
 
@@ -85,19 +85,8 @@ def converse2d_op(x, x0, weight, bias, scale, eps=1e-5):
     """The reference op (converse2d.cpp:165-209): x padded (B,C,h,w), x0 (B,C,h*s,w*s) arbitrary;
     returns the uncropped (B,C,h*s,w*s) solution."""
     lib = _lib.load()
-    if x.dim() != 4:
-        raise RuntimeError("x must be (B,C,H,W)")
-    if x0.dim() != 4:
-        raise RuntimeError("x0 must be (B,C,Hs,Ws)")
-    if weight.dim() != 4 or weight.size(0) != 1:
-        raise RuntimeError("weight must be (1,C,kh,kw)")
-    if bias.dim() != 4 or bias.size(0) != 1 or bias.size(2) != 1 or bias.size(3) != 1:
-        raise RuntimeError("bias must be (1,C,1,1)")
-    if not (x.device == x0.device == weight.device == bias.device):
-        raise RuntimeError("tensors on same device")
+    composite.check_op_args(x, x0, weight, bias, scale)
     s = int(scale)
-    if s < 1:
-        raise RuntimeError("scale must be >= 1")
     _need_hip(x, x0, weight, bias)
     B, C, h, w = x.shape
     if tuple(x0.shape) != (B, C, h * s, w * s) or weight.shape[1] != C or bias.shape[1] != C:

@@ -25,6 +25,13 @@ def pytest_collection_modifyitems(config, items):
             it.add_marker(skip)
 
 
+def seeded(*key):
+    """Reproducible generator for a test case (stable across processes, unlike hash())."""
+    import zlib
+
+    return np.random.default_rng(zlib.crc32(repr(key).encode()))
+
+
 def softmax_psf(rng, C, k, batch=1):
     """Seeded psf the way Converse2D initialises it: softmax over the k*k taps of N(0,1)."""
     w = rng.standard_normal((batch, C, k * k))
