@@ -126,6 +126,9 @@ def run_cpu_baseline(args):
 def time_events(torch, fn, iters):
     """Average duration per call from HIP events on the current stream (the library launches on it)."""
     st = torch.cuda.current_stream()
+    fn()
+    fn()
+    st.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(st)
@@ -245,6 +248,11 @@ def main():
                 "kernel": "converse2d forward (all launches of one call)", "bytes_per_launch": nbytes}
 
     extra = {}
+    # transfer-table build (runs once per weight change; cached across calls like the reference OTF)
+    t_tab = time_events(torch, lambda: Fh.converse2d_fused(x, w, bias, c["scale"], c["padding"], c["mode"],
+                                                           c["eps"], cache=False), max(5, args.steps // 4))
+    extra["converse2d_uncached_ms"] = t_tab * 1e3
+    extra["transfer_table_ms"] = (t_tab - per_call) * 1e3
     # LayerNorm (eps 1e-6) and 1x1 64->64 + GELU at the cfg3 shape
     lw = torch.ones(c["C"], device=dev)
     lb = torch.zeros(c["C"], device=dev)

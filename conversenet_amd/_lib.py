@@ -36,6 +36,12 @@ SIGNATURES = {
     "cvn_converse2d_fwd_workspace": (_size, [_i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int]),
     "cvn_converse2d_fwd_f32": (_int, [_ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _int, _int, _ptr, _f32, _int,
                                       _int, _int, _int, _ptr, _ptr, _size, _ptr]),
+    "cvn_converse2d_table_bytes": (_size, [_i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int]),
+    "cvn_converse2d_scratch_bytes": (_size, [_i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int]),
+    "cvn_converse2d_table_f32": (_int, [_ptr, _i64, _int, _int, _ptr, _f32, _i64, _i64, _i64, _i64, _int, _int,
+                                        _ptr, _size, _ptr]),
+    "cvn_converse2d_apply_f32": (_int, [_ptr, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _int, _int,
+                                        _ptr, _ptr, _size, _ptr, _ptr]),
     "cvn_converse2d_op_workspace": (_size, [_i64, _i64, _i64, _i64, _int, _int, _int]),
     "cvn_converse2d_op_f32": (_int, [_ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _int, _int, _ptr, _f32, _int, _ptr,
                                      _ptr, _size, _ptr]),

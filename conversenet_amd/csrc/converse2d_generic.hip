@@ -19,6 +19,7 @@
 //   k_cols_op                : per alias class: LR and x0 column FFTs, alias-group solve, inverse
 //   k_rows_inv               : C2R along rows (two rows per complex FFT), crop + activation on store
 #include <math.h>
+#include <stdlib.h>
 
 #include <algorithm>
 
@@ -568,41 +569,118 @@ int launch_rows_inv(const float2* SH, const Geo& g, int row0, int nrows, int col
 
 using namespace cvn;
 
-extern "C" size_t cvn_converse2d_fwd_workspace(int64_t B, int64_t C, int64_t H, int64_t W,
-                                               int64_t psf_batch, int kh, int kw, int scale,
-                                               int pad) {
-  Geo g;
-  if (module_geo(B, C, H, W, psf_batch, kh, kw, scale, pad, &g) != CVN_OK) return 0;
-  return module_ws(g).total;
+bool cvn::fused_disabled() {
+  const char* e = getenv("CVN_DISABLE_FUSED");
+  return e && e[0] == '1';
 }
 
-extern "C" int cvn_converse2d_fwd_f32(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
-                                      const float* psf, int64_t psf_batch, int kh, int kw,
-                                      const float* bias, float eps, int scale, int pad,
-                                      int pad_mode, int act, float* out, void* workspace,
-                                      size_t workspace_bytes, cvn_stream_t stream) {
-  Geo g;
-  int rc = module_geo(B, C, H, W, psf_batch, kh, kw, scale, pad, &g);
+namespace {
+
+// Which kernels serve a module-level call, and the table / scratch sizes they need.  The table
+// holds the transfer function in the layout of the chosen kernels; it depends only on the psf,
+// bias, eps and geometry, so callers may cache it across calls with unchanged weights.
+struct Route {
+  bool fused;
+  size_t table_bytes, scratch_bytes;
+};
+
+int module_route(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, int kh, int kw, int scale,
+                 int pad, Geo* g, Route* r) {
+  int rc = module_geo(B, C, H, W, psf_batch, kh, kw, scale, pad, g);
   if (rc != CVN_OK) return rc;
+  size_t fws = 0;
+  if (!fused_disabled() && kh <= 64 && fused_query(g->H, g->W, g->pad, g->s, g->Cp, &fws)) {
+    r->fused = true;
+    r->table_bytes = fws;
+    r->scratch_bytes = 0;
+  } else {
+    const ModWs w = module_ws(*g);
+    r->fused = false;
+    r->table_bytes = w.S;
+    r->scratch_bytes = w.total - w.S;
+  }
+  return CVN_OK;
+}
+
+int check_mode_act(int64_t H, int64_t W, int pad, int pad_mode, int act) {
   if (pad_mode < CVN_PAD_ZEROS || pad_mode > CVN_PAD_CIRCULAR) return fail(CVN_ERR_ARG, "bad padding mode");
   if (pad_mode == CVN_PAD_REFLECT && (pad >= H || pad >= W))
     return fail(CVN_ERR_ARG, "reflect padding must be smaller than the input size");
   if (pad_mode == CVN_PAD_CIRCULAR && (pad > H || pad > W))
     return fail(CVN_ERR_ARG, "circular padding must not exceed the input size");
   if (act != CVN_ACT_NONE && act != CVN_ACT_GELU) return fail(CVN_ERR_ARG, "bad activation");
-  if (!x || !psf || !bias || !out) return fail(CVN_ERR_ARG, "null pointer");
+  return CVN_OK;
+}
+
+}  // namespace
+
+extern "C" size_t cvn_converse2d_table_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, int kh,
+                                             int kw, int scale, int pad) {
+  Geo g;
+  Route r;
+  if (module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, &g, &r) != CVN_OK) return 0;
+  return r.table_bytes;
+}
+
+extern "C" size_t cvn_converse2d_scratch_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch,
+                                               int kh, int kw, int scale, int pad) {
+  Geo g;
+  Route r;
+  if (module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, &g, &r) != CVN_OK) return 0;
+  return r.scratch_bytes;
+}
+
+extern "C" size_t cvn_converse2d_fwd_workspace(int64_t B, int64_t C, int64_t H, int64_t W,
+                                               int64_t psf_batch, int kh, int kw, int scale,
+                                               int pad) {
+  Geo g;
+  Route r;
+  if (module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, &g, &r) != CVN_OK) return 0;
+  return align_up(r.table_bytes) + r.scratch_bytes;
+}
+
+extern "C" int cvn_converse2d_table_f32(const float* psf, int64_t psf_batch, int kh, int kw, const float* bias,
+                                        float eps, int64_t B, int64_t C, int64_t H, int64_t W, int scale, int pad,
+                                        void* table, size_t table_bytes, cvn_stream_t stream) {
+  Geo g;
+  Route r;
+  int rc = module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, &g, &r);
+  if (rc != CVN_OK) return rc;
+  if (!psf || !bias) return fail(CVN_ERR_ARG, "null pointer");
+  if (!table || table_bytes < r.table_bytes)
+    return fail(CVN_ERR_WORKSPACE, "table buffer too small: need %zu bytes", r.table_bytes);
+  hipStream_t st = (hipStream_t)stream;
+  if (r.fused) return fused_table(psf, bias, eps, g.C, g.Cp / g.C, kh, kw, g.H, g.W, g.pad, table, st);
+  return launch_phi(psf, bias, eps, g, false, (float2*)table, nullptr, st);
+}
+
+extern "C" int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
+                                        int64_t psf_batch, int kh, int kw, int scale, int pad, int pad_mode,
+                                        int act, const void* table, void* scratch, size_t scratch_bytes,
+                                        float* out, cvn_stream_t stream) {
+  Geo g;
+  Route r;
+  int rc = module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, &g, &r);
+  if (rc != CVN_OK) return rc;
+  if ((rc = check_mode_act(H, W, pad, pad_mode, act)) != CVN_OK) return rc;
+  if (!x || !table || !out) return fail(CVN_ERR_ARG, "null pointer");
   if (B == 0) return CVN_OK;
-  const ModWs ws = module_ws(g);
-  if (!workspace || workspace_bytes < ws.total)
-    return fail(CVN_ERR_WORKSPACE, "workspace too small: need %zu bytes", ws.total);
+  hipStream_t st = (hipStream_t)stream;
+  if (r.fused) {
+    if (((uintptr_t)x & 15) || ((uintptr_t)out & 15))
+      return fail(CVN_ERR_ARG, "the fused kernel needs 16-byte aligned input and output");
+    if (B * C > 0x7fffffff) return fail(CVN_ERR_UNSUPPORTED, "too many planes");
+    return fused_apply(x, B, C, g.H, g.W, g.Cp / g.C, pad, pad_mode, act, table, out, st);
+  }
+  if (!scratch || scratch_bytes < r.scratch_bytes)
+    return fail(CVN_ERR_WORKSPACE, "scratch too small: need %zu bytes", r.scratch_bytes);
   if (g.P > 65535) return fail(CVN_ERR_UNSUPPORTED, "B*C = %lld planes exceeds 65535", (long long)g.P);
   set_lds_attrs();
-  hipStream_t st = (hipStream_t)stream;
-  char* base = (char*)workspace;
-  float2* phi = (float2*)(base + ws.phi);
+  const ModWs ws = module_ws(g);
+  char* base = (char*)scratch - ws.S;  // scratch holds the workspace regions after the table
+  const float2* phi = (const float2*)table;
   float2* S = (float2*)(base + ws.S);
   float2* SH = (float2*)(base + ws.SH);
-  if ((rc = launch_phi(psf, bias, eps, g, false, phi, nullptr, st)) != CVN_OK) return rc;
   if ((rc = launch_rows_fwd(x, g.P, g.H, g.W, g.pad, pad_mode, g.h, g.w, S, st)) != CVN_OK) return rc;
   ColModArgs ca;
   ca.S = S; ca.phi = phi; ca.SH = SH; ca.C = g.C; ca.psf_batch = g.Cp / g.C;
@@ -615,6 +693,28 @@ extern "C" int cvn_converse2d_fwd_f32(const float* x, int64_t B, int64_t C, int6
   if ((rc = check_launch("column pass")) != CVN_OK) return rc;
   const int ps = g.pad * g.s;
   return launch_rows_inv(SH, g, ps, g.H * g.s, ps, g.W * g.s, act, out, st);
+}
+
+extern "C" int cvn_converse2d_fwd_f32(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
+                                      const float* psf, int64_t psf_batch, int kh, int kw,
+                                      const float* bias, float eps, int scale, int pad,
+                                      int pad_mode, int act, float* out, void* workspace,
+                                      size_t workspace_bytes, cvn_stream_t stream) {
+  Geo g;
+  Route r;
+  int rc = module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, &g, &r);
+  if (rc != CVN_OK) return rc;
+  if ((rc = check_mode_act(H, W, pad, pad_mode, act)) != CVN_OK) return rc;
+  if (!x || !psf || !bias || !out) return fail(CVN_ERR_ARG, "null pointer");
+  if (B == 0) return CVN_OK;
+  const size_t tb = align_up(r.table_bytes);
+  if (!workspace || workspace_bytes < tb + r.scratch_bytes)
+    return fail(CVN_ERR_WORKSPACE, "workspace too small: need %zu bytes", tb + r.scratch_bytes);
+  char* base = (char*)workspace;
+  rc = cvn_converse2d_table_f32(psf, psf_batch, kh, kw, bias, eps, B, C, H, W, scale, pad, base, tb, stream);
+  if (rc != CVN_OK) return rc;
+  return cvn_converse2d_apply_f32(x, B, C, H, W, psf_batch, kh, kw, scale, pad, pad_mode, act, base, base + tb,
+                                  workspace_bytes - tb, out, stream);
 }
 
 extern "C" size_t cvn_converse2d_op_workspace(int64_t B, int64_t C, int64_t h, int64_t w, int kh,

@@ -60,4 +60,14 @@ inline bool make_plan(int L, FftPlan* plan) {
   return true;
 }
 
+// Fused single-kernel path (converse2d_fused.hip): returns 1 and the workspace it needs when the
+// padded plane (H + 2 pad, W + 2 pad) at this scale has an instantiated plan.
+int fused_query(int H, int W, int pad, int scale, int64_t Cp, size_t* ws_bytes);
+int fused_table(const float* psf, const float* bias, float eps, int64_t C, int64_t psf_batch, int kh, int kw,
+                int H, int W, int pad, void* table, hipStream_t st);
+int fused_apply(const float* x, int64_t B, int64_t C, int H, int W, int64_t psf_batch, int pad, int mode, int act,
+                const void* table, float* out, hipStream_t st);
+// CVN_DISABLE_FUSED=1 in the environment routes every call through the generic multi-pass path.
+bool fused_disabled();
+
 }  // namespace cvn

@@ -126,18 +126,18 @@ template <int R, bool INV> struct DftOdd {
   static __device__ __forceinline__ void run(float2* u) {
     constexpr int H = (R - 1) / 2;
     float2 a[H], b[H];
-    float2 sum = u[0];
+    const float2 x0 = u[0];
+    float2 sum = x0;
 #pragma unroll
     for (int j = 1; j <= H; ++j) {
       a[j - 1] = cadd(u[j], u[R - j]);
       b[j - 1] = csub(u[j], u[R - j]);
       sum = cadd(sum, a[j - 1]);
     }
-    float2 out[R];
-    out[0] = sum;
+    u[0] = sum;  // inputs 1..R-1 are dead from here on: outputs overwrite them in place
 #pragma unroll
     for (int q = 1; q <= H; ++q) {
-      float2 A = u[0], Bv = make_float2(0.f, 0.f);
+      float2 A = x0, Bv = make_float2(0.f, 0.f);
 #pragma unroll
       for (int j = 1; j <= H; ++j) {
         const int m = (j * q) % R;
@@ -148,17 +148,54 @@ template <int R, bool INV> struct DftOdd {
         Bv.y = fmaf(s, b[j - 1].y, Bv.y);
       }
       if (!INV) {
-        out[q] = make_float2(A.x + Bv.y, A.y - Bv.x);
-        out[R - q] = make_float2(A.x - Bv.y, A.y + Bv.x);
+        u[q] = make_float2(A.x + Bv.y, A.y - Bv.x);
+        u[R - q] = make_float2(A.x - Bv.y, A.y + Bv.x);
       } else {
-        out[q] = make_float2(A.x - Bv.y, A.y + Bv.x);
-        out[R - q] = make_float2(A.x + Bv.y, A.y - Bv.x);
+        u[q] = make_float2(A.x - Bv.y, A.y + Bv.x);
+        u[R - q] = make_float2(A.x + Bv.y, A.y - Bv.x);
       }
     }
-#pragma unroll
-    for (int k = 0; k < R; ++k) u[k] = out[k];
   }
 };
+// In-place odd-radix DFT straight from / to memory (LDS) at a compile-time stride: inputs are
+// combined into conjugate-pair sums as they arrive and outputs are stored as soon as each pair
+// (q, R - q) is formed, so the register footprint is ~2R floats instead of ~4R.
+template <int R, int STRIDE, bool INV>
+__device__ __forceinline__ void dft_odd_mem(float2* p) {
+  constexpr int H = (R - 1) / 2;
+  float2 a[H], b[H];
+  const float2 x0 = p[0];
+  float2 sum = x0;
+#pragma unroll
+  for (int j = 1; j <= H; ++j) {
+    const float2 lo = p[j * STRIDE], hi = p[(R - j) * STRIDE];
+    a[j - 1] = cadd(lo, hi);
+    b[j - 1] = csub(lo, hi);
+    sum = cadd(sum, a[j - 1]);
+  }
+  p[0] = sum;
+#pragma unroll
+  for (int q = 1; q <= H; ++q) {
+    float2 A = x0, Bv = make_float2(0.f, 0.f);
+#pragma unroll
+    for (int j = 1; j <= H; ++j) {
+      const int m = (j * q) % R;
+      const float c = Roots<R>::c[m], s = Roots<R>::s[m];
+      A.x = fmaf(c, a[j - 1].x, A.x);
+      A.y = fmaf(c, a[j - 1].y, A.y);
+      Bv.x = fmaf(s, b[j - 1].x, Bv.x);
+      Bv.y = fmaf(s, b[j - 1].y, Bv.y);
+    }
+    if (!INV) {
+      p[q * STRIDE] = make_float2(A.x + Bv.y, A.y - Bv.x);
+      p[(R - q) * STRIDE] = make_float2(A.x - Bv.y, A.y + Bv.x);
+    } else {
+      p[q * STRIDE] = make_float2(A.x - Bv.y, A.y + Bv.x);
+      p[(R - q) * STRIDE] = make_float2(A.x + Bv.y, A.y - Bv.x);
+    }
+  }
+}
+
 template <bool INV> struct Dft<3, INV> : DftOdd<3, INV> {};
 template <bool INV> struct Dft<5, INV> : DftOdd<5, INV> {};
 template <bool INV> struct Dft<7, INV> : DftOdd<7, INV> {};

@@ -42,11 +42,54 @@ def release_workspace():
     _ws_cache.clear()
 
 
-def converse2d_fused(x, weight, bias, scale=1, padding=2, padding_mode="circular", eps=1e-5, act=None):
+class TableCache:
+    """LRU cache of transfer tables keyed on (psf, bias) identity and version counters plus the
+    geometry, mirroring the reference's OTF cache (converse2d.cpp:52-102).  Entries hold strong
+    references to psf and bias, so a cached address cannot be reused by another tensor while the
+    entry lives, and an in-place update (optimizer step, load_state_dict) bumps the version and
+    misses.  Bounded by entry count and bytes."""
+
+    def __init__(self, max_entries=128, max_bytes=8 << 30):
+        from collections import OrderedDict
+
+        self.entries = OrderedDict()
+        self.max_entries = max_entries
+        self.max_bytes = max_bytes
+        self.bytes = 0
+        self.hits = 0
+        self.misses = 0
+
+    def get(self, key):
+        e = self.entries.get(key)
+        if e is None:
+            self.misses += 1
+            return None
+        self.entries.move_to_end(key)
+        self.hits += 1
+        return e[0]
+
+    def put(self, key, table, refs):
+        self.entries[key] = (table, refs)
+        self.bytes += table.numel()
+        while self.entries and (len(self.entries) > self.max_entries or self.bytes > self.max_bytes):
+            _, (t, _) = self.entries.popitem(last=False)
+            self.bytes -= t.numel()
+
+    def clear(self):
+        self.entries.clear()
+        self.bytes = 0
+
+
+table_cache = TableCache()
+
+
+def converse2d_fused(x, weight, bias, scale=1, padding=2, padding_mode="circular", eps=1e-5, act=None,
+                     cache=True):
     """Converse2D.forward (util_converse.py:142-192) in one library call: pad, solve, crop.
 
     x (B,C,H,W); weight (1,C,kh,kw) or (B,C,kh,kw) (per-sample psf, as ConvReverseDataNet);
-    bias (1,C,1,1) or (C,).  act='gelu' applies exact GELU to the output on store."""
+    bias (1,C,1,1) or (C,).  act='gelu' applies exact GELU to the output on store.  cache=True keeps
+    the transfer table for reuse while weight and bias are unchanged (version-checked)."""
     lib = _lib.load()
     _need_hip(x, weight, bias)
     if x.dim() != 4:
@@ -62,21 +105,39 @@ def converse2d_fused(x, weight, bias, scale=1, padding=2, padding_mode="circular
     if s < 1:
         raise RuntimeError("scale must be >= 1")
     kh, kw = int(weight.shape[2]), int(weight.shape[3])
+    pb = int(weight.shape[0])
     x = x.contiguous()
-    weight = weight.contiguous()
-    bias = bias.contiguous()
+    if x.data_ptr() % 16:
+        x = x.clone()
     dev = x.device
     out = torch.empty((B, C, H * s, W * s), dtype=torch.float32, device=dev)
     if B == 0:
         return out
-    nbytes = lib.cvn_converse2d_fwd_workspace(B, C, H, W, weight.shape[0], kh, kw, s, int(padding))
-    if nbytes == 0:
+    p = int(padding)
+    geo = (B if pb > 1 else 0, C, H, W, pb, kh, kw, s, p)
+    tb = lib.cvn_converse2d_table_bytes(B, C, H, W, pb, kh, kw, s, p)
+    sb = lib.cvn_converse2d_scratch_bytes(B, C, H, W, pb, kh, kw, s, p)
+    if tb == 0:
         _lib.check(_lib.CVN_ERR_ARG, "converse2d_fused")
-    ws = _workspace(dev, nbytes)
-    rc = lib.cvn_converse2d_fwd_f32(
-        x.data_ptr(), B, C, H, W, weight.data_ptr(), weight.shape[0], kh, kw, bias.data_ptr(), float(eps), s,
-        int(padding), _lib.PAD_MODES[padding_mode], _lib.ACT_GELU if act == "gelu" else _lib.ACT_NONE,
-        out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev))
+    st = _stream(dev)
+    key = None
+    table = None
+    if cache:
+        key = (weight.data_ptr(), weight._version, bias.data_ptr(), bias._version, float(eps), geo, dev.index)
+        table = table_cache.get(key)
+    if table is None:
+        wc = weight.contiguous()
+        bc = bias.contiguous()
+        table = torch.empty(tb, dtype=torch.uint8, device=dev)
+        _lib.check(lib.cvn_converse2d_table_f32(wc.data_ptr(), pb, kh, kw, bc.data_ptr(), float(eps), B, C, H, W,
+                                                s, p, table.data_ptr(), tb, st), "converse2d transfer table")
+        if cache:
+            table_cache.put(key, table, (weight, bias))
+    scratch = _workspace(dev, sb) if sb > 0 else None
+    rc = lib.cvn_converse2d_apply_f32(
+        x.data_ptr(), B, C, H, W, pb, kh, kw, s, p, _lib.PAD_MODES[padding_mode],
+        _lib.ACT_GELU if act == "gelu" else _lib.ACT_NONE, table.data_ptr(),
+        scratch.data_ptr() if scratch is not None else None, sb, out.data_ptr(), st)
     _lib.check(rc, "converse2d_fused")
     return out
 

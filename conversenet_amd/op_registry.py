@@ -47,8 +47,9 @@ def _forward_fused(x, weight, bias, scale, padding, padding_mode, eps=1e-5, act=
 
 
 def _clear_cache():
-    if _lib.available():
-        _lib.load().cvn_clear_cache()
+    """Drops the cached transfer tables (the reference clears its OTF cache, converse2d.cpp:211-216)."""
+    functional.table_cache.clear()
+    functional.release_workspace()
 
 
 def register():

@@ -63,6 +63,24 @@ int cvn_converse2d_fwd_f32(const float* x, int64_t B, int64_t C, int64_t H, int6
                            float eps, int scale, int pad, int pad_mode, int act, float* out,
                            void* workspace, size_t workspace_bytes, cvn_stream_t stream);
 
+/* The same forward in two steps, so that the transfer table (the psf's optical transfer function
+ * combined with lambda into the closed-form solve, in the kernels' layout) can be cached across calls
+ * while weight and bias are unchanged, as the reference caches its OTF (converse2d.cpp:52-102).
+ * cvn_converse2d_table_f32 writes the table; cvn_converse2d_apply_f32 runs the solve with it.  The
+ * table depends on (psf, psf_batch, bias, eps, C, H, W, scale, pad) and, for psf_batch = B, on B.
+ * cvn_converse2d_fwd_f32 == table into workspace[0, align256(table_bytes)) + apply with the rest. */
+size_t cvn_converse2d_table_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch,
+                                  int kh, int kw, int scale, int pad);
+size_t cvn_converse2d_scratch_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch,
+                                    int kh, int kw, int scale, int pad);
+int cvn_converse2d_table_f32(const float* psf, int64_t psf_batch, int kh, int kw, const float* bias,
+                             float eps, int64_t B, int64_t C, int64_t H, int64_t W, int scale, int pad,
+                             void* table, size_t table_bytes, cvn_stream_t stream);
+int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
+                             int64_t psf_batch, int kh, int kw, int scale, int pad, int pad_mode,
+                             int act, const void* table, void* scratch, size_t scratch_bytes,
+                             float* out, cvn_stream_t stream);
+
 /* Op-level forward with the reference op's semantics: x (B,C,h,w) is the already padded input,
  * x0 (B,C,h*scale,w*scale) is arbitrary, psf (1,C,kh,kw), bias (C).  out: (B,C,h*scale,w*scale),
  * uncropped. */

@@ -92,3 +92,83 @@ def test_op_level_arbitrary_x0(s):
     dev = torch.device("cuda")
     got = Fh.converse2d_op(*(torch.from_numpy(a).to(dev) for a in (x, x0, wt, b)), s, 1e-5).cpu().numpy()
     assert np.abs(got - ref).max() <= TOL
+
+
+# ---------------------------------------------------------------------------------------------
+# fused single-kernel path (scale 1, padded planes with an instantiated plan: 260x260, 132x132)
+# ---------------------------------------------------------------------------------------------
+FUSED_CASES = [
+    # (B, C, H, W, k, p, mode)
+    (2, 3, 256, 256, 5, 2, "circular"),
+    (1, 2, 256, 256, 5, 2, "reflect"),
+    (1, 2, 256, 256, 3, 2, "replicate"),
+    (1, 2, 254, 254, 7, 3, "constant"),
+    (1, 2, 248, 248, 9, 6, "circular"),
+    (2, 3, 128, 128, 5, 2, "circular"),
+    (1, 2, 130, 130, 3, 1, "reflect"),
+    (1, 3, 124, 124, 4, 4, "replicate"),
+]
+
+
+@pytest.mark.parametrize("B,C,H,W,k,p,mode", FUSED_CASES)
+def test_fused_path_vs_oracle(B, C, H, W, k, p, mode):
+    rng = seeded("fused", B, C, H, W, k, p, mode)
+    x = rng.standard_normal((B, C, H, W)).astype(np.float32)
+    w = softmax_psf(rng, C, k)
+    b = (0.4 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    ref = O.converse2d_module(x, w, b, 1, p, mode, 1e-5)
+    got = _run_fused(x, w, b, 1, p, mode, 1e-5)
+    err = np.abs(got - ref).max()
+    print(f"fused {H + 2 * p}^2 {mode} k{k}: max-abs {err:.3e}")
+    assert err <= TOL, err
+
+
+def test_fused_per_sample_psf_and_gelu():
+    from conversenet_amd import functional as Fh
+    rng = seeded("fused-ps")
+    B, C, H, W, k = 2, 3, 256, 256, 5
+    x = rng.standard_normal((B, C, H, W)).astype(np.float32)
+    w = softmax_psf(rng, C, k, batch=B)
+    b = (0.4 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    ref = O.gelu(O.converse2d_module(x, w, b, 1, 2, "circular", 1e-3))
+    dev = torch.device("cuda")
+    got = Fh.converse2d_fused(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev),
+                              torch.from_numpy(b).reshape(-1).to(dev), 1, 2, "circular", 1e-3, act="gelu")
+    assert np.abs(got.cpu().numpy() - ref).max() <= TOL
+
+
+def test_transfer_table_cache_follows_in_place_updates():
+    """A cached table must not survive an in-place weight update (the reference's data_ptr-keyed
+    OTF cache, converse2d.cpp:62-66, returns a stale OTF in that case)."""
+    from conversenet_amd import functional as Fh
+    dev = torch.device("cuda")
+    rng = seeded("cache")
+    x = torch.from_numpy(rng.standard_normal((1, 2, 128, 128)).astype(np.float32)).to(dev)
+    w = torch.from_numpy(softmax_psf(rng, 2, 5)).to(dev)
+    b = torch.zeros(2, device=dev)
+    y1 = Fh.converse2d_fused(x, w, b, 1, 2, "circular", 1e-5)
+    y1b = Fh.converse2d_fused(x, w, b, 1, 2, "circular", 1e-5)
+    assert torch.equal(y1, y1b)
+    with torch.no_grad():
+        w.copy_(torch.from_numpy(softmax_psf(rng, 2, 5)).to(dev))  # same storage, new values
+    y2 = Fh.converse2d_fused(x, w, b, 1, 2, "circular", 1e-5)
+    ref = O.converse2d_module(x.cpu().numpy(), w.cpu().numpy(), b.reshape(1, 2, 1, 1).cpu().numpy(), 1, 2,
+                              "circular", 1e-5)
+    assert np.abs(y2.cpu().numpy() - ref).max() <= TOL
+    torch.ops.converse2d.clear_cache()
+    assert len(Fh.table_cache.entries) == 0
+
+
+@pytest.mark.parametrize("H,p", [(256, 2), (128, 2)])
+def test_fused_matches_generic_path(H, p, monkeypatch):
+    """The fused single-kernel path and the generic multi-pass path agree (both vs the oracle)."""
+    rng = seeded("fvg", H, p)
+    x = rng.standard_normal((2, 4, H, H)).astype(np.float32)
+    w = softmax_psf(rng, 4, 5)
+    b = (0.3 * rng.standard_normal((1, 4, 1, 1))).astype(np.float32)
+    fused = _run_fused(x, w, b, 1, p, "circular", 1e-5)
+    monkeypatch.setenv("CVN_DISABLE_FUSED", "1")
+    generic = _run_fused(x, w, b, 1, p, "circular", 1e-5)
+    ref = O.converse2d_module(x, w, b, 1, p, "circular", 1e-5)
+    assert np.abs(fused - ref).max() <= TOL and np.abs(generic - ref).max() <= TOL
+    assert np.abs(fused - generic).max() <= TOL
