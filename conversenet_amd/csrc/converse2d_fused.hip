@@ -29,6 +29,31 @@
 namespace cvn {
 
 constexpr int kFT = 1024;  // threads per fused workgroup
+typedef unsigned int v4u32_t __attribute__((ext_vector_type(4)));
+
+// Workgroup barrier that orders LDS traffic only: global loads and stores issued before it stay in
+// flight (every value a thread loads from global memory is consumed by that same thread, so no
+// cross-wave ordering of global memory is needed inside the kernel).
+// Raw buffer access: one SGPR resource per array, a per-lane VGPR byte offset and a wave-uniform
+// SGPR byte offset, so unrolled loops need no per-iteration 64-bit address registers.  Accesses
+// past num_records return zero (loads) or are dropped (stores).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ float2 bload2(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
+__device__ __forceinline__ void bstore4(float4 v, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, v), r, voff, soff, 0);
+}
+
+__device__ __forceinline__ void lds_barrier() {
+  // the "memory" clobber keeps the compiler from moving LDS accesses across the barrier
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 constexpr int mod_inv(int a, int m) {
   if (m <= 1) return 0;
@@ -47,10 +72,15 @@ struct FusedPlan {
   static constexpr int NQ = M / 2 + 1;    // half-spectrum columns
   static constexpr int ST1 = R2 * R3, ST2 = R3;  // row-axis strides (positions)
   static constexpr int CS1 = 2 * Q2, CS2 = 2;    // column-axis strides (row positions)
-  static constexpr int PARK = (SLOTS + kFT - 1) / kFT;
+  static constexpr int PARK = (SLOTS + kFT - 1) / kFT;  // rounds of kFT slots parked per thread
+  static constexpr int SLOTS_PAD = PARK * kFT;           // group buffer padded to whole rounds
+  // the first PARK_LDS rounds are parked in the LDS space left over next to the group buffer
+  static constexpr int TAB_BYTES = (2 * NQ + 2 * M) * 2;  // int16 tables pa, pb, pos, colsrc
+  static constexpr int PARK_LDS_MAX = (163840 - SLOTS_PAD * 8 - TAB_BYTES - 64) / (kFT * 8);
+  static constexpr int PARK_LDS = PARK_LDS_MAX < PARK ? PARK_LDS_MAX : PARK;
   static_assert(R1 * R2 * R3 == M && M % 2 == 0 && NP % 2 == 1, "plan");
-  // LDS: slots + int tables pa, pb (NQ each), pos (M), colsrc (M), rowsrc (2 NH)
-  static constexpr size_t LDS_BYTES = (size_t)SLOTS * 8 + (size_t)(2 * NQ + 2 * M + 2 * NH) * 4;
+  // LDS: group slots, parked rounds, int16 tables pa, pb (NQ each), pos (M), colsrc (M)
+  static constexpr size_t LDS_BYTES = (size_t)SLOTS_PAD * 8 + (size_t)PARK_LDS * kFT * 8 + TAB_BYTES;
 
   // position of natural sample n inside a row (Ruritanian coordinates, 3-D natural order)
   static __host__ __device__ constexpr int pos_in(int n) {
@@ -113,7 +143,7 @@ __device__ __forceinline__ void row_pass_b(float2* buf, int tid) {
 // radix-Q1 axis (row-pair stride Q2) in registers.  Work item (q, g2); q = 0 also carries the
 // Nyquist column M/2.
 template <class P>
-__device__ __forceinline__ void col_pass_a_fwd(float2* buf, const int* pa, const int* pb, int tid) {
+__device__ __forceinline__ void col_pass_a_fwd(float2* buf, const short* pa, const short* pb, int tid) {
   constexpr int Q1 = P::Q1, HQ = P::M / 2;
 #pragma unroll 1
   for (int w = tid; w < HQ * P::Q2; w += kFT) {
@@ -138,27 +168,26 @@ __device__ __forceinline__ void col_pass_a_fwd(float2* buf, const int* pa, const
         b[m * P::Q2 * P::RS + sb] = u1[m];
       }
     } else {
-      const int sn = pa[HQ];
-      float2 d0[Q1], d1[Q1], n0[Q1], n1[Q1];
+      // DC (slots 0 / M) and Nyquist (slots pa[M/2] / M + 1) columns, one after the other
 #pragma unroll
-      for (int m = 0; m < Q1; ++m) {
-        const float2 z0 = b[m * P::Q2 * P::RS], zn = b[m * P::Q2 * P::RS + sn];
-        d0[m] = make_float2(z0.x + z0.y, 0.f);
-        d1[m] = make_float2(z0.x - z0.y, 0.f);
-        n0[m] = make_float2(zn.x + zn.y, 0.f);
-        n1[m] = make_float2(zn.x - zn.y, 0.f);
-      }
-      Dft<Q1, false>::run(d0);
-      Dft<Q1, false>::run(d1);
-      Dft<Q1, false>::run(n0);
-      Dft<Q1, false>::run(n1);
+      for (int half = 0; half < 2; ++half) {
+        const int src = half ? pa[HQ] : 0;
+        const int da = half ? pa[HQ] : 0, db = half ? P::M + 1 : P::M;
+        float2 d0[Q1], d1[Q1];
 #pragma unroll
-      for (int m = 0; m < Q1; ++m) {
-        float2* r = b + m * P::Q2 * P::RS;
-        r[0] = d0[m];
-        r[P::M] = d1[m];
-        r[sn] = n0[m];
-        r[P::M + 1] = n1[m];
+        for (int m = 0; m < Q1; ++m) {
+          const float2 z = b[m * P::Q2 * P::RS + src];
+          d0[m] = make_float2(z.x + z.y, 0.f);
+          d1[m] = make_float2(z.x - z.y, 0.f);
+        }
+        Dft<Q1, false>::run(d0);
+        Dft<Q1, false>::run(d1);
+#pragma unroll
+        for (int m = 0; m < Q1; ++m) {
+          float2* r = b + m * P::Q2 * P::RS;
+          r[da] = d0[m];
+          r[db] = d1[m];
+        }
       }
     }
   }
@@ -166,7 +195,7 @@ __device__ __forceinline__ void col_pass_a_fwd(float2* buf, const int* pa, const
 
 // Column pass A (inverse): radix-Q1, inverse radix-2 pair axis, repack into complex row pairs.
 template <class P>
-__device__ __forceinline__ void col_pass_a_inv(float2* buf, const int* pa, const int* pb, int tid) {
+__device__ __forceinline__ void col_pass_a_inv(float2* buf, const short* pa, const short* pb, int tid) {
   constexpr int Q1 = P::Q1, HQ = P::M / 2;
 #pragma unroll 1
   for (int w = tid; w < HQ * P::Q2; w += kFT) {
@@ -189,25 +218,21 @@ __device__ __forceinline__ void col_pass_a_inv(float2* buf, const int* pa, const
         b[m * P::Q2 * P::RS + sb] = make_float2(A.x + B.y, B.x - A.y);  // conj(A) + i conj(B)
       }
     } else {
-      const int sn = pa[HQ];
-      float2 d0[Q1], d1[Q1], n0[Q1], n1[Q1];
+      // DC (slots 0 / M -> 0) and Nyquist (slots pa[M/2] / M + 1 -> pa[M/2]) columns in turn
 #pragma unroll
-      for (int m = 0; m < Q1; ++m) {
-        const float2* r = b + m * P::Q2 * P::RS;
-        d0[m] = r[0];
-        d1[m] = r[P::M];
-        n0[m] = r[sn];
-        n1[m] = r[P::M + 1];
-      }
-      Dft<Q1, true>::run(d0);
-      Dft<Q1, true>::run(d1);
-      Dft<Q1, true>::run(n0);
-      Dft<Q1, true>::run(n1);
+      for (int half = 0; half < 2; ++half) {
+        const int sa = half ? pa[HQ] : 0, sb = half ? P::M + 1 : P::M;
+        float2 d0[Q1], d1[Q1];
 #pragma unroll
-      for (int m = 0; m < Q1; ++m) {
-        float2* r = b + m * P::Q2 * P::RS;
-        r[0] = make_float2(d0[m].x + d1[m].x, d0[m].x - d1[m].x);
-        r[sn] = make_float2(n0[m].x + n1[m].x, n0[m].x - n1[m].x);
+        for (int m = 0; m < Q1; ++m) {
+          const float2* r = b + m * P::Q2 * P::RS;
+          d0[m] = r[sa];
+          d1[m] = r[sb];
+        }
+        Dft<Q1, true>::run(d0);
+        Dft<Q1, true>::run(d1);
+#pragma unroll
+        for (int m = 0; m < Q1; ++m) b[m * P::Q2 * P::RS + sa] = make_float2(d0[m].x + d1[m].x, d0[m].x - d1[m].x);
       }
     }
   }
@@ -215,7 +240,7 @@ __device__ __forceinline__ void col_pass_a_inv(float2* buf, const int* pa, const
 
 // Column pass B: radix Q2 along row pairs (stride 1 row pair); work item (q, g1, g3), q fastest.
 template <class P, bool INV>
-__device__ __forceinline__ void col_pass_b(float2* buf, const int* pa, const int* pb, int tid) {
+__device__ __forceinline__ void col_pass_b(float2* buf, const short* pa, const short* pb, int tid) {
   constexpr int Q = P::Q2;
 #pragma unroll 1
   for (int w = tid; w < P::NQ * P::Q1 * 2; w += kFT) {
@@ -255,16 +280,25 @@ struct RowIO {
   static constexpr int RPW = (P::NH + NW - 1) / NW;
 };
 
+// plane row of row position rp of group G (scalar: rp is wave-uniform)
 template <class P>
-__device__ __forceinline__ void group_prefetch(float4 (&v)[RowIO<P>::RPW], const int* srow, const float* xp,
-                                               int W, int wave, int lane) {
+__device__ __forceinline__ int plane_row(int rp, int G) {
+  const int g1 = rp / P::CS1, r1 = rp - g1 * P::CS1;
+  const int g2 = r1 >> 1, g3 = r1 & 1;
+  const int g = (g1 * (P::NH / P::Q1) + g2 * (P::NH / P::Q2) + g3 * (P::NH / 2)) % P::NH;
+  return 2 * g + G;
+}
+
+template <class P>
+__device__ __forceinline__ void group_prefetch(float4 (&v)[RowIO<P>::RPW], __amdgpu_buffer_rsrc_t xr, const FusedArgs& a,
+                                               int G, int wave, int lane) {
 #pragma unroll
   for (int i = 0; i < RowIO<P>::RPW; ++i) {
     const int rp = wave + i * RowIO<P>::NW;
     v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (rp < P::NH && 4 * lane < W) {
-      const int sr = srow[rp];
-      if (sr >= 0) v[i] = *(const float4*)(xp + sr * W + 4 * lane);
+    if (rp < P::NH) {
+      const int sr = fpad_src(plane_row<P>(rp, G), a.H, a.pad, a.mode);
+      if (sr >= 0) v[i] = bload4(xr, 16u * lane, (uint32_t)(sr * a.W) * 4u);
     }
   }
 }
@@ -288,7 +322,7 @@ __device__ __forceinline__ void group_deposit(float2* buf, const float4 (&v)[Row
 
 // Padding columns copied inside LDS from the interior column they replicate (or zeroed).
 template <class P>
-__device__ __forceinline__ void group_pad_cols(float2* buf, const int* pos, const int* colsrc, int pad, int tid) {
+__device__ __forceinline__ void group_pad_cols(float2* buf, const short* pos, const short* colsrc, int pad, int tid) {
   if (pad == 0) return;
   const int npc = 2 * pad;
 #pragma unroll 1
@@ -303,62 +337,66 @@ __device__ __forceinline__ void group_pad_cols(float2* buf, const int* pos, cons
 
 // forward passes up to (not including) the last column pass
 template <class P>
-__device__ __forceinline__ void group_forward_passes(float2* buf, const int* pa, const int* pb, int tid) {
+__device__ __forceinline__ void group_forward_passes(float2* buf, const short* pa, const short* pb, int tid) {
   row_pass_a<P, false>(buf, tid);
-  __syncthreads();
+  lds_barrier();
   row_pass_b<P, false>(buf, tid);
-  __syncthreads();
+  lds_barrier();
   col_pass_a_fwd<P>(buf, pa, pb, tid);
-  __syncthreads();
+  lds_barrier();
 }
 
 template <class P>
-__device__ __forceinline__ void group_inverse_store(float2* buf, const int* pa, const int* pb, const int (&lp)[4],
-                                                    const int* orow, float* op, const FusedArgs& a, int wave,
-                                                    int lane, int tid) {
+__device__ __forceinline__ void group_inverse_store(float2* buf, const short* pa, const short* pb, const int (&lp)[4],
+                                                    __amdgpu_buffer_rsrc_t orsrc, const FusedArgs& a, int G,
+                                                    int wave, int lane, int tid) {
   col_pass_b<P, true>(buf, pa, pb, tid);
-  __syncthreads();
+  lds_barrier();
   col_pass_a_inv<P>(buf, pa, pb, tid);
-  __syncthreads();
+  lds_barrier();
   row_pass_b<P, true>(buf, tid);
-  __syncthreads();
+  lds_barrier();
   row_pass_a<P, true>(buf, tid);
-  __syncthreads();
+  lds_barrier();
   const float* fb = (const float*)buf;
-#pragma unroll
+#pragma unroll 1
   for (int i = 0; i < RowIO<P>::RPW; ++i) {
     const int rp = wave + i * RowIO<P>::NW;
-    if (rp < P::NH && 4 * lane < a.W) {
-      const int orr = orow[rp];
-      if (orr >= 0 && orr < a.H) {
+    if (rp < P::NH) {
+      const int orr = plane_row<P>(rp, G) - a.pad;
+      if (orr >= 0 && orr < a.H && 4 * lane < a.W) {
         const float* r = fb + 2 * ((rp >> 1) * P::RS) + (rp & 1);
         float4 v = make_float4(r[2 * lp[0]], r[2 * lp[1]], r[2 * lp[2]], r[2 * lp[3]]);
         if (a.act == CVN_ACT_GELU) {
           v.x = fgelu(v.x); v.y = fgelu(v.y); v.z = fgelu(v.z); v.w = fgelu(v.w);
         }
-        *(float4*)(op + orr * a.W + 4 * lane) = v;
+        bstore4(v, orsrc, 16u * lane, (uint32_t)(orr * a.W) * 4u);
       }
     }
   }
 }
 
-// Table entries of one slot, loaded DEPTH slots ahead of their use in the combine step.
-constexpr int kTabDepth = 4;
+// Table entries of the combine step are loaded kTabBatch slots at a time.
+constexpr int kTabBatch = 4;
 
 template <class P>
 __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
   extern __shared__ float2 smem[];
   float2* buf = smem;
-  int* pa = (int*)(smem + P::SLOTS);
-  int* pb = pa + P::NQ;
-  int* pos = pb + P::NQ;
-  int* colsrc = pos + P::M;
-  int* rtab = colsrc + P::M;  // 2 NH: source rows by row position (G0, G1), later output rows
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float2* parkl = smem + P::SLOTS_PAD;  // PARK_LDS rounds of parked slots
+  short* pa = (short*)(parkl + P::PARK_LDS * kFT);
+  short* pb = pa + P::NQ;
+  short* pos = pb + P::NQ;
+  short* colsrc = pos + P::M;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t plane = blockIdx.x;
   const int64_t cp = (a.psf_batch == 1) ? (plane % a.C) : plane;
-  const float* xp = a.x + plane * (int64_t)a.H * a.W;
-  float* op = a.out + plane * (int64_t)a.H * a.W;
+  const uint32_t plane_bytes = (uint32_t)(a.H * a.W) * 4u;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + plane * (int64_t)a.H * a.W, plane_bytes);
+  const __amdgpu_buffer_rsrc_t orsrc = make_rsrc(a.out + plane * (int64_t)a.H * a.W, plane_bytes);
+  const __amdgpu_buffer_rsrc_t t4r = make_rsrc(a.tab4 + cp * P::SLOTS, P::SLOTS * 16u);
+  const __amdgpu_buffer_rsrc_t t2r = make_rsrc(a.tab2 + cp * P::SLOTS, P::SLOTS * 8u);
   for (int q = tid; q < P::NQ; q += kFT) {
     pa[q] = P::pa(q);
     pb[q] = P::pb(q);
@@ -367,83 +405,79 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
     pos[j] = P::pos_in(j);
     colsrc[j] = fpad_src(j, a.W, a.pad, a.mode);
   }
-  for (int g = tid; g < P::NH; g += kFT) {
-    const int rp = P::rpos_in(g);
-    rtab[rp] = fpad_src(2 * g, a.H, a.pad, a.mode);
-    rtab[P::NH + rp] = fpad_src(2 * g + 1, a.H, a.pad, a.mode);
-  }
   int lp[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) lp[c] = P::pos_in(min(a.pad + 4 * lane + c, P::M - 1));
-  __syncthreads();
   float4 pre[RowIO<P>::RPW];
-  group_prefetch<P>(pre, rtab, xp, a.W, wave, lane);
+  group_prefetch<P>(pre, xr, a, 0, wave, lane);
+  lds_barrier();
   group_deposit<P>(buf, pre, lp, a.W, wave, lane);
-  __syncthreads();
+  group_prefetch<P>(pre, xr, a, 1, wave, lane);  // G1 rows arrive during G0's passes
+  lds_barrier();
   group_pad_cols<P>(buf, pos, colsrc, a.pad, tid);
-  __syncthreads();
-  group_forward_passes<P>(buf, pa, pb, tid);
-  group_prefetch<P>(pre, rtab + P::NH, xp, a.W, wave, lane);  // G1 rows arrive during G0's last pass
-  col_pass_b<P, false>(buf, pa, pb, tid);
-  __syncthreads();
-  float2 park[P::PARK];
-#pragma unroll
-  for (int i = 0; i < P::PARK; ++i) {
-    const int s = tid + i * kFT;
-    park[i] = (s < P::SLOTS) ? buf[s] : make_float2(0.f, 0.f);
-  }
-  __syncthreads();
-  group_deposit<P>(buf, pre, lp, a.W, wave, lane);
-  __syncthreads();
-  group_pad_cols<P>(buf, pos, colsrc, a.pad, tid);
-  __syncthreads();
+  lds_barrier();
   group_forward_passes<P>(buf, pa, pb, tid);
   col_pass_b<P, false>(buf, pa, pb, tid);
-  __syncthreads();
-  // radix-2 across the groups, transfer function, inverse radix-2 (table loads run kTabDepth ahead)
-  const float4* t4 = a.tab4 + cp * P::SLOTS;
-  const float2* t2 = a.tab2 + cp * P::SLOTS;
-  float4 f4[kTabDepth];
-  float2 f2[kTabDepth];
-#pragma unroll
-  for (int i = 0; i < kTabDepth; ++i) {
-    const int s = min(tid + i * kFT, P::SLOTS - 1);
-    f4[i] = t4[s];
-    f2[i] = t2[s];
-  }
+  lds_barrier();
+  constexpr int PL = P::PARK_LDS, PR = P::PARK - P::PARK_LDS;
+  float2 park[PR > 0 ? PR : 1];
 #pragma unroll
   for (int i = 0; i < P::PARK; ++i) {
-    const int s = tid + i * kFT;
-    const float4 ab = f4[i % kTabDepth];
-    const float2 bi = f2[i % kTabDepth];
-    if (i + kTabDepth < P::PARK) {
-      const int sn = min(tid + (i + kTabDepth) * kFT, P::SLOTS - 1);
-      f4[i % kTabDepth] = t4[sn];
-      f2[i % kTabDepth] = t2[sn];
-    }
-    if (s < P::SLOTS) {
-      const float2 e = park[i], o = buf[s];
-      const float2 av = make_float2(ab.x, ab.y), bw = make_float2(ab.z, ab.w);
-      park[i] = cadd(cmul(av, e), cmul(bw, o));
-      buf[s] = cadd(cmul(bi, e), cmul(av, o));
-    }
+    const float2 v = buf[tid + i * kFT];  // slots past SLOTS are padding (never read back)
+    if (i < PL) parkl[i * kFT + tid] = v;
+    else park[i - PL] = v;
   }
-  __syncthreads();
-  for (int g = tid; g < P::NH; g += kFT) {  // output rows (plane row - pad) by row position
-    const int rp = P::rpos_in(g);
-    rtab[rp] = 2 * g - a.pad;
-    rtab[P::NH + rp] = 2 * g + 1 - a.pad;
-  }
-  __syncthreads();
-  group_inverse_store<P>(buf, pa, pb, lp, rtab + P::NH, op, a, wave, lane, tid);
-  __syncthreads();
+  lds_barrier();
+  group_deposit<P>(buf, pre, lp, a.W, wave, lane);
+  lds_barrier();
+  group_pad_cols<P>(buf, pos, colsrc, a.pad, tid);
+  lds_barrier();
+  group_forward_passes<P>(buf, pa, pb, tid);
+  // radix-2 across the groups, transfer function, inverse radix-2.  Table entries come in batches
+  // of kTabBatch slots; the first batch is requested before G1's last pass.
+  float4 f4[kTabBatch];
+  float2 f2[kTabBatch];
 #pragma unroll
-  for (int i = 0; i < P::PARK; ++i) {
-    const int s = tid + i * kFT;
-    if (s < P::SLOTS) buf[s] = park[i];
+  for (int i = 0; i < kTabBatch; ++i) {
+    f4[i] = bload4(t4r, 16u * tid, 16u * i * kFT);
+    f2[i] = bload2(t2r, 8u * tid, 8u * i * kFT);
   }
-  __syncthreads();
-  group_inverse_store<P>(buf, pa, pb, lp, rtab, op, a, wave, lane, tid);
+  col_pass_b<P, false>(buf, pa, pb, tid);
+  lds_barrier();
+#pragma unroll
+  for (int i0 = 0; i0 < P::PARK; i0 += kTabBatch) {
+    if (i0 > 0) {
+#pragma unroll
+      for (int i = 0; i < kTabBatch; ++i) {
+        f4[i] = bload4(t4r, 16u * tid, 16u * (i0 + i) * kFT);
+        f2[i] = bload2(t2r, 8u * tid, 8u * (i0 + i) * kFT);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kTabBatch; ++i) {
+      const int ii = i0 + i;
+      if (ii < P::PARK) {
+        const int s = tid + ii * kFT;
+        const float2 e = ii < PL ? parkl[ii * kFT + tid] : park[ii < PL ? 0 : ii - PL], o = buf[s];
+        const float2 av = make_float2(f4[i].x, f4[i].y), bw = make_float2(f4[i].z, f4[i].w);
+        float2 ne = cadd(cmul(av, e), cmul(bw, o));
+        // materialise E' here: otherwise the compiler sinks its arithmetic to the unpark and keeps
+        // e, o, a and bW (8 values per slot instead of 2) alive across the G1 inverse
+        asm volatile("" : "+v"(ne.x), "+v"(ne.y));
+        if (ii < PL) parkl[ii * kFT + tid] = ne;
+        else park[ii < PL ? 0 : ii - PL] = ne;
+        buf[s] = cadd(cmul(f2[i], e), cmul(av, o));
+      }
+    }
+    asm volatile("" ::: "memory");  // the next batch's loads may not be hoisted above this one
+  }
+  lds_barrier();
+  group_inverse_store<P>(buf, pa, pb, lp, orsrc, a, 1, wave, lane, tid);
+  lds_barrier();
+#pragma unroll
+  for (int i = 0; i < P::PARK; ++i) buf[tid + i * kFT] = i < PL ? parkl[i * kFT + tid] : park[i < PL ? 0 : i - PL];
+  lds_barrier();
+  group_inverse_store<P>(buf, pa, pb, lp, orsrc, a, 0, wave, lane, tid);
 }
 
 // ----------------------------------------------------------------------------------------------
