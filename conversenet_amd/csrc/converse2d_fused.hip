@@ -255,9 +255,20 @@ struct FusedArgs {
   const float4* tab4;    // (Cp, SLOTS): (a, bW)
   const float2* tab2;    // (Cp, SLOTS): bWi
   float* out;            // (P, H, W)
-  int64_t C, psf_batch;
+  int64_t B, C, psf_batch;
   int H, W, pad, mode, act;
 };
+
+// Plane handled by workgroup `blk`.  With one table per channel (psf_batch 1), planes are taken
+// channel-major, and the dispatcher's round-robin over the 8 XCDs (workgroup i runs on XCD i % 8)
+// is undone, so each XCD walks a contiguous run of channels: the planes that run together on one
+// XCD share a few transfer tables, which then stay in that XCD's L2.
+__device__ __forceinline__ int64_t fused_plane(int64_t blk, const FusedArgs& a) {
+  if (a.psf_batch != 1) return blk;
+  const int64_t P = a.B * a.C;
+  const int64_t k = (P % 8 == 0) ? (blk & 7) * (P >> 3) + (blk >> 3) : blk;
+  return (k % a.B) * a.C + k / a.B;
+}
 
 __device__ __forceinline__ int fpad_src(int i, int n, int p, int mode) {
   int j = i - p;
@@ -390,7 +401,7 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
   short* colsrc = pos + P::M;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t plane = blockIdx.x;
+  const int64_t plane = fused_plane(blockIdx.x, a);
   const int64_t cp = (a.psf_batch == 1) ? (plane % a.C) : plane;
   const uint32_t plane_bytes = (uint32_t)(a.H * a.W) * 4u;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + plane * (int64_t)a.H * a.W, plane_bytes);
@@ -592,7 +603,7 @@ int fused_apply_run(const float* x, int64_t B, int64_t C, int H, int W, int64_t 
   const int64_t Cp = psf_batch * C;
   const float4* t4 = (const float4*)table;
   const float2* t2 = (const float2*)((const char*)table + align_up((size_t)Cp * P::SLOTS * sizeof(float4)));
-  FusedArgs fa{x, t4, t2, out, C, psf_batch, H, W, pad, mode, act};
+  FusedArgs fa{x, t4, t2, out, B, C, psf_batch, H, W, pad, mode, act};
   hipLaunchKernelGGL(k_converse2d_fused<P>, dim3((unsigned)(B * C)), dim3(kFT), P::LDS_BYTES, st, fa);
   return check_launch("fused converse2d");
 }

@@ -1,0 +1,259 @@
+"""HIP LayerNorm / 1x1 (MFMA) / fused LN-MLP kernels, ConverseBlock, the two models, and full-size
+properties of the Converse2D path, all through the library's C ABI, against the fp64 oracle."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import converse_oracle as O
+from tests.conftest import seeded, softmax_psf
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+TOL = 1e-4
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _n(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def psnr(a, ref):
+    """utils_image.py:626-641 with peak = dynamic range of the reference output."""
+    mse = float(np.mean((a.astype(np.float64) - ref) ** 2))
+    return 10 * np.log10((ref.max() - ref.min()) ** 2 / mse) if mse > 0 else np.inf
+
+
+# ------------------------------------------------------------------------------------------------
+# a13 LayerNorm (channels first)
+# ------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("B,C,H,W,eps", [(2, 64, 32, 40, 1e-6), (1, 128, 16, 18, 1e-5), (3, 5, 7, 9, 1e-5),
+                                         (2, 16, 33, 31, 1e-6), (1, 1, 4, 4, 1e-6)])
+def test_layernorm_cf(B, C, H, W, eps):
+    from conversenet_amd import functional as Fh
+    rng = seeded("ln", B, C, H, W)
+    x = (3 * rng.standard_normal((B, C, H, W)) + 1).astype(np.float32)
+    w = rng.standard_normal(C).astype(np.float32)
+    b = rng.standard_normal(C).astype(np.float32)
+    got = _n(Fh.layernorm_cf(_t(x), _t(w), _t(b), eps))
+    ref = O.layernorm_cf(x, w, b, eps)
+    assert np.abs(got - ref).max() <= TOL
+
+
+# ------------------------------------------------------------------------------------------------
+# a14 1x1 conv (+ GELU, + residual, + LN prologue) on MFMA, and the generic fallback shapes
+# ------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("cin,cout", [(64, 64), (64, 128), (128, 64), (128, 128), (32, 64), (16, 64), (64, 16),
+                                      (3, 64), (64, 3), (1, 64), (64, 1)])
+@pytest.mark.parametrize("act", [None, "gelu"])
+def test_conv1x1(cin, cout, act):
+    from conversenet_amd import functional as Fh
+    rng = seeded("c11", cin, cout, act)
+    B, H, W = 2, 24, 20
+    x = rng.standard_normal((B, cin, H, W)).astype(np.float32)
+    w = (rng.standard_normal((cout, cin, 1, 1)) / np.sqrt(cin)).astype(np.float32)
+    b = rng.standard_normal(cout).astype(np.float32)
+    got = _n(Fh.conv1x1(_t(x), _t(w), _t(b), act=act))
+    ref = O.conv1x1(x, w, b)
+    if act == "gelu":
+        ref = O.gelu(ref)
+    assert np.abs(got - ref).max() <= TOL
+
+
+@pytest.mark.parametrize("HW", [(16, 16), (15, 17)])  # vector (HW % 4 == 0) and scalar paths
+def test_conv1x1_residual_scale_and_ln_prologue(HW):
+    from conversenet_amd import functional as Fh
+    rng = seeded("c11r", HW)
+    B, C = 2, 64
+    H, W = HW
+    x = rng.standard_normal((B, C, H, W)).astype(np.float32)
+    r = rng.standard_normal((B, C, H, W)).astype(np.float32)
+    w = (rng.standard_normal((C, C, 1, 1)) / 8).astype(np.float32)
+    b = rng.standard_normal(C).astype(np.float32)
+    a = rng.standard_normal(C).astype(np.float32)
+    lw, lb = rng.standard_normal(C).astype(np.float32), rng.standard_normal(C).astype(np.float32)
+    got = _n(Fh.conv1x1(_t(x), _t(w), _t(b), residual=_t(r), res_scale=_t(a)))
+    ref = a[None, :, None, None] * O.conv1x1(x, w, b) + r
+    assert np.abs(got - ref).max() <= TOL
+    if (H * W) % 4 == 0:
+        got = _n(Fh.conv1x1(_t(x), _t(w), _t(b), act="gelu", ln=(_t(lw), _t(lb), 1e-5)))
+        ref = O.gelu(O.conv1x1(O.layernorm_cf(x, lw, lb, 1e-5), w, b))
+        assert np.abs(got - ref).max() <= TOL
+
+
+@pytest.mark.parametrize("C,mid", [(64, 128), (32, 64)])
+@pytest.mark.parametrize("alpha", [False, True])
+def test_ln_mlp_residual(C, mid, alpha):
+    """ConverseBlock.conv2 plus its residual in one kernel (util_converse.py:285-292, :321-322)."""
+    from conversenet_amd import functional as Fh
+    rng = seeded("mlp", C, mid, alpha)
+    B, H, W = 2, 20, 24
+    x = rng.standard_normal((B, C, H, W)).astype(np.float32)
+    lw, lb = rng.standard_normal(C).astype(np.float32), rng.standard_normal(C).astype(np.float32)
+    w1 = (rng.standard_normal((mid, C, 1, 1)) / np.sqrt(C)).astype(np.float32)
+    b1 = rng.standard_normal(mid).astype(np.float32)
+    w2 = (rng.standard_normal((C, mid, 1, 1)) / np.sqrt(mid)).astype(np.float32)
+    b2 = rng.standard_normal(C).astype(np.float32)
+    a = rng.standard_normal(C).astype(np.float32) if alpha else None
+    got = _n(Fh.ln_mlp_residual(_t(x), _t(lw), _t(lb), 1e-5, _t(w1), _t(b1), _t(w2), _t(b2),
+                                res_scale=_t(a) if alpha else None))
+    t = O.conv1x1(O.gelu(O.conv1x1(O.layernorm_cf(x, lw, lb, 1e-5), w1, b1)), w2, b2)
+    ref = (a[None, :, None, None] * t if alpha else t) + x
+    assert np.abs(got - ref).max() <= TOL
+
+
+# ------------------------------------------------------------------------------------------------
+# a15 ConverseBlock / ConverseBlockAlphaVariant (fused block path on the GPU)
+# ------------------------------------------------------------------------------------------------
+def _sd(m):
+    return {k: v.detach().double().cpu().numpy() for k, v in m.state_dict().items()}
+
+
+@pytest.mark.parametrize("alpha", [False, True])
+@pytest.mark.parametrize("C,k,p,mode", [(64, 3, 2, "circular"), (32, 5, 2, "replicate"), (64, 7, 6, "circular")])
+def test_converse_block(alpha, C, k, p, mode):
+    from conversenet_amd import util_converse as U
+    torch.manual_seed(11)
+    cls = U.ConverseBlockAlphaVariant if alpha else U.ConverseBlock
+    blk = cls(C, C, kernel_size=k, padding=p, padding_mode=mode)
+    if alpha:
+        with torch.no_grad():
+            blk.alpha1.normal_(0, 0.5)
+            blk.alpha2.normal_(0, 0.5)
+    rng = seeded("blk", alpha, C, k, p, mode)
+    x = rng.standard_normal((2, C, 36, 40)).astype(np.float32)
+    ref = O.converse_block(x, _sd(blk), "", k, 1, p, mode, 1e-5, alpha)
+    blk = blk.to(DEV).eval()
+    with torch.no_grad():
+        got = _n(blk(_t(x)))
+    err = np.abs(got - ref).max()
+    print(f"block C{C} k{k} {mode} alpha={alpha}: max-abs {err:.3e} psnr {psnr(got, ref):.1f}")
+    assert err <= 1e-3 and psnr(got, ref) >= 60
+
+
+# ------------------------------------------------------------------------------------------------
+# a16 / a17 models (reduced spatial size; same layer shapes and channel counts as cfg4 / cfg5)
+# ------------------------------------------------------------------------------------------------
+def test_converse_dncnn():
+    from conversenet_amd.converse_dncnn import ConverseDnCNN
+    torch.manual_seed(4)
+    m = ConverseDnCNN().eval()
+    rng = seeded("dncnn")
+    x = (rng.random((2, 1, 48, 56)) + 0.1 * rng.standard_normal((2, 1, 48, 56))).astype(np.float32)
+    ref = O.converse_dncnn(x, _sd(m))
+    with torch.no_grad():
+        got = _n(m.to(DEV)(_t(x)))
+    print(f"ConverseDnCNN psnr {psnr(got, ref):.1f} dB")
+    assert psnr(got, ref) >= 60
+
+
+def test_converse_usrnet():
+    from conversenet_amd.converse_usrnet import ConverseUSRNet
+    torch.manual_seed(5)
+    m = ConverseUSRNet().eval()
+    with torch.no_grad():
+        for p in (m.d.alpha, *[b.alpha1 for b in m.p.m_body], *[b.alpha2 for b in m.p.m_body]):
+            p.normal_(0, 0.1)
+    rng = seeded("usrnet")
+    x = rng.random((2, 3, 12, 12)).astype(np.float32)
+    k = rng.random((2, 1, 7, 7)).astype(np.float32)
+    k /= k.sum(axis=(2, 3), keepdims=True)
+    ref = O.converse_usrnet(x, k, 4, _sd(m), 7)
+    with torch.no_grad():
+        got = _n(m.to(DEV)(_t(x), _t(k), 4))
+    print(f"ConverseUSRNet psnr {psnr(got, ref):.1f} dB")
+    assert psnr(got, ref) >= 60
+
+
+# ------------------------------------------------------------------------------------------------
+# Full cfg3 size (B16 C64 256^2 k5 p2 circular): oracle on a plane sample, plus size-free identities
+# ------------------------------------------------------------------------------------------------
+def _cfg3():
+    g0 = torch.Generator().manual_seed(0)
+    x = torch.randn(16, 64, 256, 256, generator=g0)
+    g1 = torch.Generator().manual_seed(1)
+    w = torch.softmax(torch.randn(1, 64, 25, generator=g1), dim=-1).reshape(1, 64, 5, 5)
+    return x, w
+
+
+def test_cfg3_full_size_planes_vs_oracle():
+    from conversenet_amd import functional as Fh
+    x, w = _cfg3()
+    b = torch.zeros(64)
+    got = Fh.converse2d_fused(x.to(DEV), w.to(DEV), b.to(DEV), 1, 2, "circular", 1e-5)
+    torch.cuda.synchronize()
+    # one plane per channel, batch index cycling, so every channel's table and every batch slot is hit
+    idx = [(c % 16, c) for c in range(64)]
+    xs = np.stack([x[bb, c].numpy() for bb, c in idx])[None]          # (1, 64, 256, 256)
+    ws = np.stack([w[0, c].numpy() for _, c in idx])[None]
+    ref = O.converse2d_module(xs, ws, np.zeros((1, 64, 1, 1), np.float32), 1, 2, "circular", 1e-5)
+    g = np.stack([got[bb, c].cpu().numpy() for bb, c in idx])[None]
+    err = np.abs(g - ref).max()
+    print(f"cfg3 64-plane sample: max-abs {err:.3e}")
+    assert err <= TOL
+
+
+def test_cfg3_full_size_linearity_and_identity():
+    """The solve is linear in x for fixed psf and bias; a centred delta psf makes it the identity
+    (K = 1, so (conj K + lambda) / (|K|^2 + lambda) = 1)."""
+    from conversenet_amd import functional as Fh
+    x, w = _cfg3()
+    b = torch.zeros(64, device=DEV)
+    x1 = x.to(DEV)
+    x2 = torch.roll(x1, shifts=(3, 5), dims=(2, 3)).flip(0)
+    w = w.to(DEV)
+    f = lambda t: Fh.converse2d_fused(t, w, b, 1, 2, "circular", 1e-5)
+    lhs = f(0.75 * x1 - 1.5 * x2)
+    rhs = 0.75 * f(x1) - 1.5 * f(x2)
+    # each of the three evaluations is within 1e-4 of its exact value: 1e-4 (1 + 0.75 + 1.5) bounds the gap
+    assert float((lhs - rhs).abs().max()) <= 3.25e-4
+    delta = torch.zeros(1, 64, 5, 5, device=DEV)
+    delta[..., 2, 2] = 1.0
+    y = Fh.converse2d_fused(x1, delta, b, 1, 2, "circular", 1e-5)
+    assert float((y - x1).abs().max()) <= 5e-5
+
+
+# ------------------------------------------------------------------------------------------------
+# Edge cases: empty batch, single channel, ragged shapes, a large plane, non-contiguous input
+# ------------------------------------------------------------------------------------------------
+def test_empty_batch():
+    from conversenet_amd import functional as Fh
+    x = torch.zeros(0, 4, 16, 16, device=DEV)
+    w = torch.full((1, 4, 3, 3), 1 / 9, device=DEV)
+    y = Fh.converse2d_fused(x, w, torch.zeros(4, device=DEV), 2, 1, "circular", 1e-5)
+    assert tuple(y.shape) == (0, 4, 32, 32)
+    y = torch.ops.converse2d.forward(x, torch.zeros(0, 4, 16, 16, device=DEV), w, torch.zeros(1, 4, 1, 1, device=DEV),
+                                     1, 1e-5)
+    assert tuple(y.shape) == (0, 4, 16, 16)
+
+
+@pytest.mark.parametrize("B,C,H,W,k,s,p,mode", [(1, 1, 1, 1, 1, 1, 0, "circular"),
+                                                 (1, 1, 3, 50, 3, 2, 1, "reflect"),
+                                                 (2, 3, 37, 1, 1, 3, 0, "replicate"),
+                                                 (1, 1, 1000, 1000, 5, 1, 2, "circular"),
+                                                 (1, 2, 61, 67, 6, 2, 3, "constant")])
+def test_ragged_and_large(B, C, H, W, k, s, p, mode):
+    from conversenet_amd import functional as Fh
+    rng = seeded("rag", B, C, H, W, k, s, p, mode)
+    x = rng.standard_normal((B, C, H, W)).astype(np.float32)
+    w = softmax_psf(rng, C, k)
+    b = (0.3 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    got = _n(Fh.converse2d_fused(_t(x), _t(w), _t(b).reshape(-1), s, p, mode, 1e-5))
+    ref = O.converse2d_module(x, w, b, s, p, mode, 1e-5)
+    assert np.abs(got - ref).max() <= TOL
+
+
+def test_module_non_contiguous_input():
+    from conversenet_amd.util_converse import Converse2D
+    torch.manual_seed(6)
+    m = Converse2D(8, 8, 5, scale=1, padding=2).to(DEV)
+    base = torch.randn(2, 16, 40, 36, device=DEV)
+    x = base[:, ::2]  # channel-strided view
+    with torch.no_grad():
+        got = _n(m(x))
+    ref = O.converse2d_module(x.cpu().numpy(), m.weight.detach().cpu().numpy(), m.bias.detach().cpu().numpy(), 1,
+                              2, "circular", 1e-5)
+    assert np.abs(got - ref).max() <= TOL
