@@ -148,9 +148,9 @@ def load_traffic(name):
         return None
 
 
-def bench_model(torch, dev, iters=3):
+def make_dncnn(torch, dev):
     """Converse-DnCNN (cfg4): default constructor (k7, p6, circular, 20 blocks, 796,353 params),
-    random init (seed 0), B=8 1x256x256 synthetic noisy input; images/s."""
+    random init (seed 0), B=8 1x256x256 synthetic noisy input."""
     sys.path.insert(0, ROOT)
     from conversenet_amd.converse_dncnn import ConverseDnCNN
 
@@ -158,6 +158,12 @@ def bench_model(torch, dev, iters=3):
     m = ConverseDnCNN().to(dev).eval()
     g = torch.Generator().manual_seed(0)
     x = (torch.rand(8, 1, 256, 256, generator=g) + torch.randn(8, 1, 256, 256, generator=g) * (25 / 255)).to(dev)
+    return m, x
+
+
+def bench_model(torch, dev, iters=3):
+    """Converse-DnCNN (cfg4) images/s."""
+    m, x = make_dncnn(torch, dev)
     with torch.no_grad():
         m(x)
         torch.cuda.synchronize()
@@ -182,6 +188,10 @@ def only_kernel(torch, Fh, args, dev, x, step):
         src = torch.randn(COPY_FLOATS, device=dev)
         dst = torch.empty_like(src)
         fn = lambda: Fh.copy_(dst, src)
+    elif args.only == "dncnn":
+        m, xin = make_dncnn(torch, dev)
+        torch.set_grad_enabled(False)
+        fn = lambda: m(xin)
     else:
         raise SystemExit(f"unknown --only {args.only}")
     for _ in range(args.warmup):
@@ -205,7 +215,7 @@ def main():
     ap.add_argument("--cpu-worker", action="store_true")
     ap.add_argument("--cpu-iters", type=int, default=3)
     ap.add_argument("--cpu-threads", type=int, default=16)
-    ap.add_argument("--only", choices=["converse2d", "layernorm", "conv1x1", "copy"],
+    ap.add_argument("--only", choices=["converse2d", "layernorm", "conv1x1", "copy", "dncnn"],
                     help="run one kernel family alone (for rocprofv3)")
     args = ap.parse_args()
 

@@ -27,7 +27,8 @@ def _hip_ok(*ts) -> bool:
         return False
     if torch.is_grad_enabled() and any(t.requires_grad for t in ts):
         return False
-    return _lib.available()
+    _lib.load()  # HIP tensors need the library: ImportError rather than a silent fallback
+    return True
 
 
 def _forward(x, x0, weight, bias, scale, eps=1e-5):

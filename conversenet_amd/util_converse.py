@@ -5,7 +5,8 @@ Same public names, constructor signatures, parameter shapes and state-dict keys 
 ConverseBlock (:253-293), ConverseBlockAlphaVariant (:296-323), ResidualBlock (:328-342).
 
 Dispatch (mirrors the reference's backend selection, util_converse.py:150-169):
-  * backend "auto": fp32 HIP tensors without a pending gradient run the fused HIP kernels;
+  * backend "auto": fp32 HIP tensors without a pending gradient run the fused HIP kernels (an
+    ImportError if the library is not built: there is no silent fallback for HIP tensors);
     anything else runs the PyTorch composition (the reference's own pure-PyTorch path).
   * backend "cuda": requires the HIP library and a HIP tensor (RuntimeError otherwise, as :156-158).
   * backend "pytorch": always the PyTorch composition.
@@ -38,9 +39,8 @@ def _backend(default: str) -> str:
 
 
 def _hip_eligible(*ts) -> bool:
-    """True when the forward-only fp32 HIP kernels may run on these tensors."""
-    if not _HAS_CONVERSE2D_EXT:
-        return False
+    """True when the forward-only fp32 HIP kernels serve these tensors.  HIP tensors never fall back
+    to the PyTorch composition because the library is missing: that raises instead."""
     for t in ts:
         if t is None:
             continue
@@ -48,6 +48,7 @@ def _hip_eligible(*ts) -> bool:
             return False
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts):
         return False
+    _lib.load()  # ImportError when libcvn_hip.so is not built
     return True
 
 
