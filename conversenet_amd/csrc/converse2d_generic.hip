@@ -204,6 +204,7 @@ struct RowFwdArgs {
   int NC;          // w / 2 + 1
   int rpb;         // rows per block (even)
   FftPlan plan;    // length w
+  int rad_off;     // byte offset of the plan's Rader tables in LDS
   float2* S;       // (P, NC, h)
 };
 
@@ -217,6 +218,8 @@ __global__ void __launch_bounds__(256) k_rows_fwd(RowFwdArgs a) {
   const int r0 = blockIdx.x * a.rpb;
   const int tid = threadIdx.x, nth = blockDim.x;
   build_twiddles(tw, L, tid, nth);
+  char* rad = (char*)sm + a.rad_off;
+  build_rader(a.plan, rad, tid, nth);
   const float* xp = a.x + plane * (int64_t)a.Hin * a.Win;
   for (int idx = tid; idx < ntr * L; idx += nth) {
     const int t = idx / L, c = idx - t * L;
@@ -236,7 +239,7 @@ __global__ void __launch_bounds__(256) k_rows_fwd(RowFwdArgs a) {
     A[t * L + c] = make_float2(va, vb);
   }
   __syncthreads();
-  const float2* Z = fft_lds<false>(a.plan, A, Bf, ntr, tw, tid, nth);
+  const float2* Z = fft_lds<false>(a.plan, A, Bf, ntr, tw, tid, nth, rad);
   // unpack two real rows: Ya = (Z[c] + conj Z[-c]) / 2, Yb = (Z[c] - conj Z[-c]) / (2i)
   float2* Sp = a.S + plane * (int64_t)a.NC * a.h;
   for (int idx = tid; idx < a.NC * a.rpb; idx += nth) {
@@ -265,6 +268,7 @@ struct ColModArgs {
   int64_t C, psf_batch;
   int h, w, Hs, Ws, NC, NCs, cpb;
   FftPlan plan_h, plan_H;
+  int rad_off;        // byte offset of plan_h's Rader tables in LDS (plan_H's follow)
 };
 
 __global__ void __launch_bounds__(256) k_cols_module(ColModArgs a) {
@@ -281,6 +285,10 @@ __global__ void __launch_bounds__(256) k_cols_module(ColModArgs a) {
   build_twiddles(twh, a.h, tid, nth);
   if (a.Hs != a.h) build_twiddles(twH, a.Hs, tid, nth);
   const float2* tH = (a.Hs != a.h) ? twH : twh;
+  char* radh = (char*)sm + a.rad_off;
+  char* radH = radh + rader_lds_bytes(a.plan_h);
+  build_rader(a.plan_h, radh, tid, nth);
+  build_rader(a.plan_H, radH, tid, nth);
   const float2* Sp = a.S + plane * (int64_t)a.NC * a.h;
   for (int idx = tid; idx < a.cpb * a.h; idx += nth) {
     const int cl = idx / a.h, u = idx - cl * a.h;
@@ -293,7 +301,7 @@ __global__ void __launch_bounds__(256) k_cols_module(ColModArgs a) {
     A[cl * a.h + u] = val;
   }
   __syncthreads();
-  float2* Y = fft_lds<false>(a.plan_h, A, Bf, a.cpb, twh, tid, nth);
+  float2* Y = fft_lds<false>(a.plan_h, A, Bf, a.cpb, twh, tid, nth, radh);
   float2* X = (Y == A) ? Bf : A;
   const float2* ph = a.phi + cp * (int64_t)a.NCs * a.Hs;
   for (int idx = tid; idx < a.cpb * a.Hs; idx += nth) {
@@ -303,7 +311,7 @@ __global__ void __launch_bounds__(256) k_cols_module(ColModArgs a) {
     X[cl * a.Hs + u] = val;
   }
   __syncthreads();
-  const float2* R = fft_lds<true>(a.plan_H, X, (X == A) ? Bf : A, a.cpb, tH, tid, nth);
+  const float2* R = fft_lds<true>(a.plan_H, X, (X == A) ? Bf : A, a.cpb, tH, tid, nth, radH);
   float2* SHp = a.SH + plane * (int64_t)a.NCs * a.Hs;
   for (int idx = tid; idx < ncol * a.Hs; idx += nth) {
     const int cl = idx / a.Hs, u = idx - cl * a.Hs;
@@ -323,6 +331,7 @@ struct ColOpArgs {
   int64_t C;
   int h, w, s, Hs, Ws, NC, NCs;
   FftPlan plan_h, plan_H;
+  int rad_off;        // byte offset of plan_h's Rader tables in LDS (plan_H's follow)
 };
 
 __global__ void __launch_bounds__(256) k_cols_op(ColOpArgs a) {
@@ -341,6 +350,10 @@ __global__ void __launch_bounds__(256) k_cols_op(ColOpArgs a) {
   if (v0 > a.Ws / 2) return;  // member b = 0 is the smallest
   build_twiddles(twh, a.h, tid, nth);
   build_twiddles(twH, a.Hs, tid, nth);
+  char* radh = (char*)sm + a.rad_off;
+  char* radH = radh + rader_lds_bytes(a.plan_h);
+  build_rader(a.plan_h, radh, tid, nth);
+  build_rader(a.plan_H, radH, tid, nth);
   const float2* Sp = a.S + plane * (int64_t)a.NC * a.h;
   const float2* S0p = a.S0 + plane * (int64_t)a.NCs * a.Hs;
   for (int u = tid; u < a.h; u += nth) {
@@ -353,8 +366,8 @@ __global__ void __launch_bounds__(256) k_cols_op(ColOpArgs a) {
                                       : cconj(S0p[(int64_t)(a.Ws - vb) * a.Hs + u]);
   }
   __syncthreads();
-  const float2* Y = fft_lds<false>(a.plan_h, Ya, Yb, 1, twh, tid, nth);
-  float2* X0 = fft_lds<false>(a.plan_H, Xa, Xb, a.s, twH, tid, nth);
+  const float2* Y = fft_lds<false>(a.plan_h, Ya, Yb, 1, twh, tid, nth, radh);
+  float2* X0 = fft_lds<false>(a.plan_H, Xa, Xb, a.s, twH, tid, nth, radH);
   float2* Xo = (X0 == Xa) ? Xb : Xa;
   const float2* kf = a.kf + c * (int64_t)a.Ws * a.Hs;
   const float2* Am = a.A + c * (int64_t)a.Ws * a.Hs;
@@ -379,7 +392,7 @@ __global__ void __launch_bounds__(256) k_cols_op(ColOpArgs a) {
       }
   }
   __syncthreads();
-  const float2* R = fft_lds<true>(a.plan_H, Xo, (Xo == Xa) ? Xb : Xa, a.s, twH, tid, nth);
+  const float2* R = fft_lds<true>(a.plan_H, Xo, (Xo == Xa) ? Xb : Xa, a.s, twH, tid, nth, radH);
   float2* SHp = a.SH + plane * (int64_t)a.NCs * a.Hs;
   for (int idx = tid; idx < a.s * a.Hs; idx += nth) {
     const int b = idx / a.Hs, u = idx - b * a.Hs;
@@ -398,6 +411,7 @@ struct RowInvArgs {
   int row0, nrows, col0, ncols;  // crop window
   int rpb, act;
   FftPlan plan;      // length Ws
+  int rad_off;       // byte offset of the plan's Rader tables in LDS
 };
 
 __global__ void __launch_bounds__(256) k_rows_inv(RowInvArgs a) {
@@ -410,6 +424,8 @@ __global__ void __launch_bounds__(256) k_rows_inv(RowInvArgs a) {
   const int64_t plane = blockIdx.y;
   const int r0 = blockIdx.x * a.rpb;  // local output row
   build_twiddles(tw, L, tid, nth);
+  char* rad = (char*)sm + a.rad_off;
+  build_rader(a.plan, rad, tid, nth);
   const float2* SHp = a.SH + plane * (int64_t)a.NCs * a.Hs;
   // stage the half spectra: Bf[rl * NCs + v]
   for (int idx = tid; idx < a.NCs * a.rpb; idx += nth) {
@@ -430,7 +446,7 @@ __global__ void __launch_bounds__(256) k_rows_inv(RowInvArgs a) {
     A[t * L + v] = make_float2(ha.x - hb.y, ha.y + hb.x);
   }
   __syncthreads();
-  const float2* Z = fft_lds<true>(a.plan, A, Bf, ntr, tw, tid, nth);
+  const float2* Z = fft_lds<true>(a.plan, A, Bf, ntr, tw, tid, nth, rad);
   float* op = a.out + plane * (int64_t)a.nrows * a.ncols;
   for (int idx = tid; idx < a.rpb * a.ncols; idx += nth) {
     const int rl = idx / a.ncols, cc = idx - rl * a.ncols;
@@ -546,9 +562,10 @@ int launch_rows_fwd(const float* x, int64_t P, int Hin, int Win, int pad, int mo
   a.NC = w / 2 + 1;
   a.rpb = rows_per_block(w, h);
   if (!make_plan(w, &a.plan)) return fail(CVN_ERR_UNSUPPORTED, "no plan for length %d", w);
+  a.rad_off = (int)align_up(rows_lds(w, a.rpb), 16);
   a.S = S;
   dim3 grid((h + a.rpb - 1) / a.rpb, (unsigned)P);
-  hipLaunchKernelGGL(k_rows_fwd, grid, dim3(kThreads), rows_lds(w, a.rpb), st, a);
+  hipLaunchKernelGGL(k_rows_fwd, grid, dim3(kThreads), a.rad_off + rader_lds_bytes(a.plan), st, a);
   return check_launch("row forward pass");
 }
 
@@ -559,8 +576,9 @@ int launch_rows_inv(const float2* SH, const Geo& g, int row0, int nrows, int col
   a.row0 = row0; a.nrows = nrows; a.col0 = col0; a.ncols = ncols; a.act = act;
   a.rpb = rows_per_block(g.Ws, nrows);
   if (!make_plan(g.Ws, &a.plan)) return fail(CVN_ERR_UNSUPPORTED, "no plan for length %d", g.Ws);
+  a.rad_off = (int)align_up(rows_lds(g.Ws, a.rpb), 16);
   dim3 grid((nrows + a.rpb - 1) / a.rpb, (unsigned)g.P);
-  hipLaunchKernelGGL(k_rows_inv, grid, dim3(kThreads), rows_lds(g.Ws, a.rpb), st, a);
+  hipLaunchKernelGGL(k_rows_inv, grid, dim3(kThreads), a.rad_off + rader_lds_bytes(a.plan), st, a);
   return check_launch("row inverse pass");
 }
 
@@ -688,8 +706,9 @@ extern "C" int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, in
   ca.cpb = cols_per_block(g.h, g.Hs);
   if (!make_plan(g.h, &ca.plan_h) || !make_plan(g.Hs, &ca.plan_H))
     return fail(CVN_ERR_UNSUPPORTED, "no plan for column length");
+  ca.rad_off = (int)align_up(cols_lds(g.h, g.Hs, ca.cpb), 16);
   hipLaunchKernelGGL(k_cols_module, dim3((g.NCs + ca.cpb - 1) / ca.cpb, (unsigned)g.P), dim3(kThreads),
-                     cols_lds(g.h, g.Hs, ca.cpb), st, ca);
+                     ca.rad_off + rader_lds_bytes(ca.plan_h) + rader_lds_bytes(ca.plan_H), st, ca);
   if ((rc = check_launch("column pass")) != CVN_OK) return rc;
   const int ps = g.pad * g.s;
   return launch_rows_inv(SH, g, ps, g.H * g.s, ps, g.W * g.s, act, out, st);
@@ -760,7 +779,8 @@ extern "C" int cvn_converse2d_op_f32(const float* x, const float* x0, int64_t B,
   ca.h = g.h; ca.w = g.w; ca.s = g.s; ca.Hs = g.Hs; ca.Ws = g.Ws; ca.NC = g.NC; ca.NCs = g.NCs;
   if (!make_plan(g.h, &ca.plan_h) || !make_plan(g.Hs, &ca.plan_H))
     return fail(CVN_ERR_UNSUPPORTED, "no plan for column length");
-  const size_t lds = (size_t)(2 * g.h + g.Hs + 2 * g.h + 2 * g.s * g.Hs) * sizeof(float2);
+  ca.rad_off = (int)align_up((size_t)(3 * g.h + g.Hs + 2 * g.s * g.Hs) * sizeof(float2), 16);
+  const size_t lds = ca.rad_off + rader_lds_bytes(ca.plan_h) + rader_lds_bytes(ca.plan_H);
   if (lds > kLdsLimit) return fail(CVN_ERR_UNSUPPORTED, "column class does not fit in LDS");
   hipLaunchKernelGGL(k_cols_op, dim3(g.w, (unsigned)g.P), dim3(kThreads), lds, st, ca);
   if ((rc = check_launch("op column pass")) != CVN_OK) return rc;

@@ -36,16 +36,13 @@ inline size_t align_up(size_t n, size_t a = 256) { return (n + a - 1) / a * a; }
 // Largest transform length any generic-path kernel accepts (LDS capacity).
 constexpr int kMaxFftLen = 4096;
 
-// Decompose L into Stockham radices: 8s, then 4/2 for the rest of the power of two, then the odd
-// radices with fixed butterflies, then any remaining prime factors (generic O(R^2) pass).
-inline bool make_plan(int L, FftPlan* plan) {
-  if (L < 1 || L > kMaxFftLen) return false;
-  plan->L = L;
-  plan->nst = 0;
-  int n = L;
+// Fixed-radix decomposition (8s, then 4 / 2 for the rest of the power of two, then 3, 5, 7, 11,
+// 13); false if a factor is left over or the stage list overflows.
+inline bool fixed_radices(int n, int* radix, int* nst, int cap) {
+  *nst = 0;
   auto push = [&](int r) {
-    if (plan->nst >= kMaxStages) return false;
-    plan->radix[plan->nst++] = r;
+    if (*nst >= cap) return false;
+    radix[(*nst)++] = r;
     return true;
   };
   while (n % 8 == 0) { if (!push(8)) return false; n /= 8; }
@@ -54,9 +51,82 @@ inline bool make_plan(int L, FftPlan* plan) {
   const int odd[] = {3, 5, 7, 11, 13};
   for (int r : odd)
     while (n % r == 0) { if (!push(r)) return false; n /= r; }
-  for (int f = 17; n > 1 && (int64_t)f * f <= n; f += 2)
-    while (n % f == 0) { if (!push(f)) return false; n /= f; }
-  if (n > 1 && !push(n)) return false;
+  return n == 1;
+}
+
+inline int powmod_host(int64_t g, int64_t e, int64_t m) {
+  int64_t r = 1 % m, b = g % m;
+  while (e > 0) {
+    if (e & 1) r = r * b % m;
+    b = b * b % m;
+    e >>= 1;
+  }
+  return (int)r;
+}
+
+// Rader setup for prime R: a primitive root g, its inverse, and the fixed-radix plan of R - 1.
+inline bool make_rader(int R, RaderPlan* rp) {
+  if (R - 1 > kMaxRaderLen) return false;
+  for (int d = 2; d * d <= R; ++d)
+    if (R % d == 0) return false;  // not prime
+  if (!fixed_radices(R - 1, rp->radix, &rp->nst, kMaxInnerStages)) return false;
+  int qs[16], nq = 0;
+  for (int n = R - 1, d = 2; n > 1; ++d)
+    if (n % d == 0) {
+      qs[nq++] = d;
+      while (n % d == 0) n /= d;
+    }
+  for (int g = 2; g < R; ++g) {
+    bool prim = true;
+    for (int i = 0; i < nq && prim; ++i) prim = powmod_host(g, (R - 1) / qs[i], R) != 1;
+    if (prim) {
+      rp->R = R;
+      rp->g = g;
+      rp->ginv = powmod_host(g, R - 2, R);
+      return true;
+    }
+  }
+  return false;
+}
+
+// Decompose L into Stockham radices: the fixed butterflies first, then the remaining prime factors,
+// each either a Rader stage (prime R with R - 1 made of fixed radices, R - 1 <= kMaxRaderLen) or
+// the generic O(R^2) pass.
+inline bool make_plan(int L, FftPlan* plan) {
+  if (L < 1 || L > kMaxFftLen) return false;
+  plan->L = L;
+  plan->nst = 0;
+  plan->nrad = 0;
+  int n = L;
+  auto push = [&](int r) {
+    if (plan->nst >= kMaxStages) return false;
+    plan->radix[plan->nst++] = r;
+    return true;
+  };
+  for (int r : {2, 3, 5, 7, 11, 13})
+    while (n % r == 0) n /= r;
+  int nfix = 0, fixr[kMaxStages];
+  if (!fixed_radices(L / n, fixr, &nfix, kMaxStages)) return false;
+  for (int i = 0; i < nfix; ++i)
+    if (!push(fixr[i])) return false;
+  size_t off = 0;
+  for (int f = 17; n > 1; f += 2) {
+    if ((int64_t)f * f > n) f = n;  // what is left is prime
+    while (n % f == 0) {
+      if (!push(f)) return false;
+      n /= f;
+      bool have = false;
+      for (int r = 0; r < plan->nrad; ++r) have = have || plan->rad[r].R == f;
+      if (!have && plan->nrad < kMaxRader) {
+        RaderPlan rp;
+        if (make_rader(f, &rp)) {
+          rp.off = (int)off;
+          off += rader_tab_bytes(f);
+          plan->rad[plan->nrad++] = rp;
+        }
+      }
+    }
+  }
   return true;
 }
 

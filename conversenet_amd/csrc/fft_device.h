@@ -206,11 +206,59 @@ template <bool INV> struct Dft<13, INV> : DftOdd<13, INV> {};
 // FFT plan: a length L = prod(radix[i]) decomposed into Stockham passes.
 // ----------------------------------------------------------------------------------------------
 constexpr int kMaxStages = 24;
+// Prime radices above 13 whose R - 1 factors into the fixed butterflies are computed with Rader's
+// algorithm (C. M. Rader, "Discrete Fourier transforms when the number of data samples is prime",
+// Proc. IEEE 56(6), 1968): with g a primitive root mod R, a_p = u_{g^p} and b_m = W^{g^-m},
+//   X_0 = u_0 + sum_p a_p,   X_{g^-q} = u_0 + (a (*) b)_q   (cyclic convolution of length R - 1),
+// and the convolution runs as FFT_{R-1}, a pointwise product with FFT_{R-1}(b) / (R - 1), and an
+// unnormalised inverse FFT_{R-1}.  That costs O(R log R) per butterfly instead of O(R^2).
+constexpr int kMaxRader = 2;        // distinct Rader primes per plan (three would exceed 4096)
+constexpr int kMaxRaderLen = 256;   // R - 1 limit (bounds the LDS tables)
+constexpr int kMaxInnerStages = 8;
+struct RaderPlan {
+  int R, g, ginv;                   // prime, primitive root mod R, its inverse mod R
+  int off;                          // byte offset of this prime's tables in the Rader LDS area
+  int nst;                          // inner plan of length R - 1 (fixed radices only)
+  int radix[kMaxInnerStages];
+};
 struct FftPlan {
   int L;
   int nst;
   int radix[kMaxStages];
+  int nrad;
+  RaderPlan rad[kMaxRader];
 };
+
+// LDS tables of one Rader prime (Rm = R - 1 entries each); wd / bd are fp64 scratch for building bf / bi.
+__host__ __device__ constexpr size_t rader_tab_bytes(int R) { return ((size_t)60 * (R - 1) + 15) / 16 * 16; }
+// Bytes of LDS a plan's Rader tables need (0 without Rader stages).
+__host__ __device__ inline size_t rader_lds_bytes(const FftPlan& plan) {
+  size_t b = 0;
+  for (int r = 0; r < plan.nrad; ++r) b += rader_tab_bytes(plan.rad[r].R);
+  return b;
+}
+struct RaderTab {
+  double2* wd;  // exp(-2 pi i m / Rm)
+  double2* bd;  // b_m = exp(-2 pi i g^-m / R)
+  float2* tw;   // twiddles of the inner length-Rm transforms
+  float2* bf;   // FFT_Rm(b) / Rm (forward direction)
+  float2* bi;   // FFT_Rm(conj b) / Rm (inverse direction)
+  short* gp;    // g^p mod R
+  short* gq;    // g^-q mod R
+};
+__device__ __forceinline__ RaderTab rader_tab(char* base, const RaderPlan& rp) {
+  const int Rm = rp.R - 1;
+  char* b = base + rp.off;
+  RaderTab t;
+  t.wd = (double2*)b;
+  t.bd = (double2*)(b + 16 * Rm);
+  t.tw = (float2*)(b + 32 * Rm);
+  t.bf = (float2*)(b + 40 * Rm);
+  t.bi = (float2*)(b + 48 * Rm);
+  t.gp = (short*)(b + 56 * Rm);
+  t.gq = (short*)(b + 58 * Rm);
+  return t;
+}
 
 // One radix-R Stockham pass over `ntr` transforms of length L stored back to back (src -> dst).
 // p is the product of the radices already applied.  Output position of butterfly i, leg j is
@@ -274,16 +322,152 @@ __device__ void stockham_pass_generic(const float2* __restrict__ src, float2* __
   }
 }
 
+// A fixed-radix-only plan (the inner transforms of a Rader stage) on `ntr` transforms in a / b.
+template <bool INV>
+__device__ float2* fft_fixed(const int* radix, int nst, int L, float2* a, float2* b, int ntr, const float2* tw,
+                             int tid, int nth) {
+  int p = 1;
+  float2* src = a;
+  float2* dst = b;
+  for (int st = 0; st < nst; ++st) {
+    const int R = radix[st];
+    switch (R) {
+      case 2: stockham_pass<2, INV>(src, dst, L, p, ntr, tw, tid, nth); break;
+      case 3: stockham_pass<3, INV>(src, dst, L, p, ntr, tw, tid, nth); break;
+      case 4: stockham_pass<4, INV>(src, dst, L, p, ntr, tw, tid, nth); break;
+      case 5: stockham_pass<5, INV>(src, dst, L, p, ntr, tw, tid, nth); break;
+      case 7: stockham_pass<7, INV>(src, dst, L, p, ntr, tw, tid, nth); break;
+      case 8: stockham_pass<8, INV>(src, dst, L, p, ntr, tw, tid, nth); break;
+      case 11: stockham_pass<11, INV>(src, dst, L, p, ntr, tw, tid, nth); break;
+      default: stockham_pass<13, INV>(src, dst, L, p, ntr, tw, tid, nth); break;
+    }
+    __syncthreads();
+    p *= R;
+    float2* t = src;
+    src = dst;
+    dst = t;
+  }
+  return src;
+}
+
+// One radix-R Stockham pass (same input / output placement as stockham_pass) by Rader's algorithm.
+// The NB = ntr L / R butterflies each gather their R - 1 non-zero-index legs in generator order
+// into dst[b (R-1) + p]; leg 0 goes to the tail dst[NB (R-1) + b].  The inner forward and inverse
+// transforms ping-pong between the first NB (R-1) slots of dst and src; with the same number of
+// passes each way the convolution always ends in dst, whose tail was never touched, so the
+// outputs are scattered into src.  Returns src (the pass does not swap buffers).
+template <bool INV>
+__device__ float2* rader_pass(float2* src, float2* dst, int L, int p, int ntr, const float2* tw,
+                              const RaderPlan& rp, const RaderTab& rt, int tid, int nth) {
+  const int R = rp.R, Rm = R - 1, T = L / R, NB = T * ntr;
+  const int twstep = L / (p * R);
+  float2* tail = dst + NB * Rm;
+  for (int idx = tid; idx < NB * Rm; idx += nth) {
+    const int b = idx / Rm, q = idx - b * Rm;
+    const int t = b / T, i = b - t * T;
+    const int j = rt.gp[q];
+    float2 v = src[t * L + i + j * T];
+    if (p > 1) v = cmul(v, twid<INV>(tw[j * (i % p) * twstep]));
+    dst[idx] = v;
+    if (q == 0) tail[b] = src[t * L + i];
+  }
+  __syncthreads();
+  float2* F = fft_fixed<false>(rp.radix, rp.nst, Rm, dst, src, NB, rt.tw, tid, nth);
+  const float2* bh = INV ? rt.bi : rt.bf;
+  for (int idx = tid; idx < NB * Rm; idx += nth) {
+    const int b = idx / Rm, m = idx - b * Rm;
+    const float2 v = F[idx];
+    float2 w = cmul(v, bh[m]);
+    if (m == 0) {  // X_0 = u_0 + sum_p a_p; adding u_0 to bin 0 adds it to every convolution output
+      const float2 u0 = tail[b];
+      tail[b] = cadd(u0, v);
+      w = cadd(w, u0);
+    }
+    F[idx] = w;
+  }
+  __syncthreads();
+  const float2* C = fft_fixed<true>(rp.radix, rp.nst, Rm, F, F == dst ? src : dst, NB, rt.tw, tid, nth);
+  for (int idx = tid; idx < NB * R; idx += nth) {
+    const int b = idx / R, r = idx - b * R;
+    const int t = b / T, i = b - t * T;
+    const int k = i % p;
+    const int n = r == 0 ? 0 : rt.gq[r - 1];
+    src[t * L + (i - k) * R + k + n * p] = r == 0 ? tail[b] : C[b * Rm + r - 1];
+  }
+  __syncthreads();
+  return src;
+}
+
+__device__ __forceinline__ int powmod_dev(int g, int e, int m) {
+  int r = 1 % m;
+  for (int i = 0; i < e; ++i) r = (r * g) % m;
+  return r;
+}
+
+// Fills the Rader tables of every Rader prime of `plan` into the LDS area `base`.  All threads of
+// the block call it; it synchronises.
+__device__ void build_rader(const FftPlan& plan, char* base, int tid, int nth) {
+  if (plan.nrad == 0) return;
+  for (int r = 0; r < plan.nrad; ++r) {
+    const RaderPlan& rp = plan.rad[r];
+    const RaderTab t = rader_tab(base, rp);
+    const int Rm = rp.R - 1;
+    for (int m = tid; m < Rm; m += nth) {
+      const int gq = powmod_dev(rp.ginv, m, rp.R);
+      t.gp[m] = (short)powmod_dev(rp.g, m, rp.R);
+      t.gq[m] = (short)gq;
+      double sn, cs;
+      sincospi(-2.0 * (double)m / (double)Rm, &sn, &cs);
+      t.wd[m] = make_double2(cs, sn);
+      t.tw[m] = make_float2((float)cs, (float)sn);
+      sincospi(-2.0 * (double)gq / (double)rp.R, &sn, &cs);
+      t.bd[m] = make_double2(cs, sn);
+    }
+  }
+  __syncthreads();
+  for (int r = 0; r < plan.nrad; ++r) {
+    const RaderPlan& rp = plan.rad[r];
+    const RaderTab t = rader_tab(base, rp);
+    const int Rm = rp.R - 1;
+    for (int m = tid; m < Rm; m += nth) {
+      double fr = 0.0, fi = 0.0, ir = 0.0, ii = 0.0;
+      int e = 0;  // (p m) mod Rm
+      for (int q = 0; q < Rm; ++q) {
+        const double2 b = t.bd[q], w = t.wd[e];
+        fr += b.x * w.x - b.y * w.y;
+        fi += b.x * w.y + b.y * w.x;
+        ir += b.x * w.x + b.y * w.y;   // conj(b) w
+        ii += b.x * w.y - b.y * w.x;
+        e += m;
+        if (e >= Rm) e -= Rm;
+      }
+      const double sc = 1.0 / (double)Rm;
+      t.bf[m] = make_float2((float)(fr * sc), (float)(fi * sc));
+      t.bi[m] = make_float2((float)(ir * sc), (float)(ii * sc));
+    }
+  }
+  __syncthreads();
+}
+
 // Runs the whole plan on `ntr` transforms held in buffer a (workspace b of equal size).  Returns
 // the buffer holding the result.  All threads of the block must call it; it synchronises.
+// `rader` is the plan's Rader LDS area (filled by build_rader), or null when plan.nrad == 0.
 template <bool INV>
 __device__ float2* fft_lds(const FftPlan& plan, float2* a, float2* b, int ntr, const float2* tw,
-                           int tid, int nth) {
+                           int tid, int nth, char* rader = nullptr) {
   int p = 1;
   float2* src = a;
   float2* dst = b;
   for (int st = 0; st < plan.nst; ++st) {
     const int R = plan.radix[st];
+    int ri = -1;
+    for (int r = 0; r < plan.nrad; ++r)
+      if (plan.rad[r].R == R) ri = r;
+    if (ri >= 0) {
+      rader_pass<INV>(src, dst, plan.L, p, ntr, tw, plan.rad[ri], rader_tab(rader, plan.rad[ri]), tid, nth);
+      p *= R;
+      continue;  // result stays in src
+    }
     switch (R) {
       case 2: stockham_pass<2, INV>(src, dst, plan.L, p, ntr, tw, tid, nth); break;
       case 3: stockham_pass<3, INV>(src, dst, plan.L, p, ntr, tw, tid, nth); break;

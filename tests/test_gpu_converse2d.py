@@ -172,3 +172,46 @@ def test_fused_matches_generic_path(H, p, monkeypatch):
     ref = O.converse2d_module(x, w, b, 1, p, "circular", 1e-5)
     assert np.abs(fused - ref).max() <= TOL and np.abs(generic - ref).max() <= TOL
     assert np.abs(fused - generic).max() <= TOL
+
+
+# ---------------------------------------------------------------------------------------------
+# prime factors above 13 (Rader stages): 268 = 4*67 (cfg4's layer plane), 67, 17*19 (two Rader
+# primes in one plan), 4*17*17 (a repeated Rader prime), 2*47 (generic O(R^2) stage), scale 2
+# ---------------------------------------------------------------------------------------------
+RADER_CASES = [
+    # (B, C, H, W, k, s, p, mode)
+    (1, 4, 256, 256, 7, 1, 6, "circular"),
+    (2, 2, 61, 65, 5, 1, 3, "reflect"),
+    (1, 2, 319, 315, 5, 1, 2, "circular"),
+    (1, 1, 1152, 20, 5, 1, 2, "replicate"),
+    (1, 2, 90, 40, 3, 1, 2, "constant"),
+    (2, 2, 15, 19, 3, 2, 2, "circular"),
+]
+
+
+@pytest.mark.parametrize("B,C,H,W,k,s,p,mode", RADER_CASES)
+def test_rader_prime_sizes(B, C, H, W, k, s, p, mode):
+    rng = seeded("rader", B, C, H, W, k, s, p, mode)
+    x = rng.standard_normal((B, C, H, W)).astype(np.float32)
+    w = softmax_psf(rng, C, k)
+    b = (0.3 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    ref = O.converse2d_module(x, w, b, s, p, mode, 1e-5)
+    got = _run_fused(x, w, b, s, p, mode, 1e-5)
+    err = np.abs(got - ref).max()
+    print(f"rader {H + 2 * p}x{W + 2 * p} s{s}: max-abs {err:.3e}")
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("s", [1, 2])
+def test_rader_op_level(s):
+    from conversenet_amd import functional as Fh
+    rng = seeded("rader-op", s)
+    B, C, h, w, k = 1, 2, 67, 38, 5
+    x = rng.standard_normal((B, C, h, w)).astype(np.float32)
+    x0 = rng.standard_normal((B, C, h * s, w * s)).astype(np.float32)
+    wt = softmax_psf(rng, C, k)
+    b = (0.3 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    ref = O.converse2d_op(x, x0, wt, b, s, 1e-5)
+    dev = torch.device("cuda")
+    got = Fh.converse2d_op(*(torch.from_numpy(a).to(dev) for a in (x, x0, wt, b)), s, 1e-5).cpu().numpy()
+    assert np.abs(got - ref).max() <= TOL
