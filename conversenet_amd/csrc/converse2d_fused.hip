@@ -62,11 +62,11 @@ constexpr int mod_inv(int a, int m) {
   return 0;
 }
 
-template <int M_, int R1_, int R2_, int R3_, int Q1_, int Q2_>
+template <int M_, int R1_, int R2_, int R3_, int Q1_, int Q2_, int RSX_ = 0>
 struct FusedPlan {
   static constexpr int M = M_, R1 = R1_, R2 = R2_, R3 = R3_;
   static constexpr int Q1 = Q1_, Q2 = Q2_, NH = 2 * Q1_ * Q2_, N = 2 * NH;
-  static constexpr int RS = M + 2;        // row-pair stride (M/2 + 1 bins per row, two rows)
+  static constexpr int RS = M + 2 + RSX_;  // row-pair stride (M/2 + 1 bins per row, two rows, RSX_ spare)
   static constexpr int NP = NH / 2;       // row pairs per group
   static constexpr int SLOTS = NP * RS;   // complex slots per group
   static constexpr int NQ = M / 2 + 1;    // half-spectrum columns
@@ -107,7 +107,7 @@ __device__ __forceinline__ void row_pass_a(float2* buf, int tid) {
   constexpr int R = P::R3, PER = P::M / R;
 #pragma unroll 1
   for (int w = tid; w < P::NP * PER; w += kFT) {
-    const int t = w / PER, i = w - t * PER;
+    const int i = w / P::NP, t = w - i * P::NP;  // row pair fastest across lanes (LDS bank spread)
     dft_odd_mem<R, 1, INV>(buf + t * P::RS + i * R);
   }
 }
@@ -118,7 +118,7 @@ __device__ __forceinline__ void row_pass_b(float2* buf, int tid) {
   constexpr int R1 = P::R1, R2 = P::R2, PER = P::R3;
 #pragma unroll 1
   for (int w = tid; w < P::NP * PER; w += kFT) {
-    const int t = w / PER, n3 = w - t * PER;
+    const int n3 = w / P::NP, t = w - n3 * P::NP;  // row pair fastest across lanes (LDS bank spread)
     float2* b = buf + t * P::RS + n3;
     float2 u[R1][R2];
 #pragma unroll
@@ -147,7 +147,8 @@ __device__ __forceinline__ void col_pass_a_fwd(float2* buf, const short* pa, con
   constexpr int Q1 = P::Q1, HQ = P::M / 2;
 #pragma unroll 1
   for (int w = tid; w < HQ * P::Q2; w += kFT) {
-    const int g2 = w / HQ, q = w - g2 * HQ;
+    // row-pair group fastest across lanes: spreads the lanes of a wave over LDS banks
+    const int q = w / P::Q2, g2 = w - q * P::Q2;
     float2* b = buf + g2 * P::RS;
     if (q != 0) {
       const int sa = pa[q], sb = pb[q];
@@ -199,7 +200,8 @@ __device__ __forceinline__ void col_pass_a_inv(float2* buf, const short* pa, con
   constexpr int Q1 = P::Q1, HQ = P::M / 2;
 #pragma unroll 1
   for (int w = tid; w < HQ * P::Q2; w += kFT) {
-    const int g2 = w / HQ, q = w - g2 * HQ;
+    // row-pair group fastest across lanes: spreads the lanes of a wave over LDS banks
+    const int q = w / P::Q2, g2 = w - q * P::Q2;
     float2* b = buf + g2 * P::RS;
     if (q != 0) {
       const int sa = pa[q], sb = pb[q];
@@ -241,12 +243,14 @@ __device__ __forceinline__ void col_pass_a_inv(float2* buf, const short* pa, con
 // Column pass B: radix Q2 along row pairs (stride 1 row pair); work item (q, g1, g3), q fastest.
 template <class P, bool INV>
 __device__ __forceinline__ void col_pass_b(float2* buf, const short* pa, const short* pb, int tid) {
-  constexpr int Q = P::Q2;
+  // The half-spectrum columns sit at positions pa[q] and pb[q], which together cover every
+  // position 0 .. M + 1 of a row pair exactly once, so the work items run over positions:
+  // neighbouring lanes then touch neighbouring LDS words (no bank conflicts, no table lookups).
+  constexpr int Q = P::Q2, NPOS = P::M + 2;
 #pragma unroll 1
-  for (int w = tid; w < P::NQ * P::Q1 * 2; w += kFT) {
-    const int i = w / P::NQ, q = w - i * P::NQ;
-    const int g1 = i >> 1, g3 = i & 1;
-    dft_odd_mem<Q, P::RS, INV>(buf + g1 * P::Q2 * P::RS + (g3 ? pb[q] : pa[q]));
+  for (int w = tid; w < NPOS * P::Q1; w += kFT) {
+    const int g1 = w / NPOS, p = w - g1 * NPOS;
+    dft_odd_mem<Q, P::RS, INV>(buf + g1 * P::Q2 * P::RS + p);
   }
 }
 
@@ -300,11 +304,11 @@ __device__ __forceinline__ int plane_row(int rp, int G) {
   return 2 * g + G;
 }
 
-template <class P>
+template <class P, int I0 = 0, int I1 = RowIO<P>::RPW>
 __device__ __forceinline__ void group_prefetch(float4 (&v)[RowIO<P>::RPW], __amdgpu_buffer_rsrc_t xr, const FusedArgs& a,
                                                int G, int wave, int lane) {
 #pragma unroll
-  for (int i = 0; i < RowIO<P>::RPW; ++i) {
+  for (int i = I0; i < I1; ++i) {
     const int rp = wave + i * RowIO<P>::NW;
     v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (rp < P::NH) {
@@ -355,6 +359,26 @@ __device__ __forceinline__ void group_forward_passes(float2* buf, const short* p
   lds_barrier();
   col_pass_a_fwd<P>(buf, pa, pb, tid);
   lds_barrier();
+}
+
+// The same passes with G1's row loads issued a few at a time between them, so the loads never
+// queue up behind each other at issue and their HBM traffic spreads over G0's compute.
+template <class P>
+__device__ __forceinline__ void group_forward_passes_loading(float2* buf, const short* pa, const short* pb, int tid,
+                                                             float4 (&pre)[RowIO<P>::RPW],
+                                                             __amdgpu_buffer_rsrc_t xr, const FusedArgs& a,
+                                                             int wave, int lane) {
+  constexpr int N = RowIO<P>::RPW, C1 = (N + 3) / 4, C2 = (2 * N + 3) / 4, C3 = (3 * N + 3) / 4;
+  group_prefetch<P, 0, C1>(pre, xr, a, 1, wave, lane);
+  row_pass_a<P, false>(buf, tid);
+  lds_barrier();
+  group_prefetch<P, C1, C2>(pre, xr, a, 1, wave, lane);
+  row_pass_b<P, false>(buf, tid);
+  lds_barrier();
+  group_prefetch<P, C2, C3>(pre, xr, a, 1, wave, lane);
+  col_pass_a_fwd<P>(buf, pa, pb, tid);
+  lds_barrier();
+  group_prefetch<P, C3, N>(pre, xr, a, 1, wave, lane);
 }
 
 template <class P>
@@ -423,11 +447,10 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
   group_prefetch<P>(pre, xr, a, 0, wave, lane);
   lds_barrier();
   group_deposit<P>(buf, pre, lp, a.W, wave, lane);
-  group_prefetch<P>(pre, xr, a, 1, wave, lane);  // G1 rows arrive during G0's passes
   lds_barrier();
   group_pad_cols<P>(buf, pos, colsrc, a.pad, tid);
   lds_barrier();
-  group_forward_passes<P>(buf, pa, pb, tid);
+  group_forward_passes_loading<P>(buf, pa, pb, tid, pre, xr, a, wave, lane);  // G1 rows arrive meanwhile
   col_pass_b<P, false>(buf, pa, pb, tid);
   lds_barrier();
   constexpr int PL = P::PARK_LDS, PR = P::PARK - P::PARK_LDS;
@@ -572,7 +595,7 @@ __global__ void __launch_bounds__(256) k_phi_fused(PhiFusedArgs a) {
 // ----------------------------------------------------------------------------------------------
 // host dispatch
 // ----------------------------------------------------------------------------------------------
-using Plan260 = FusedPlan<260, 4, 5, 13, 5, 13>;   // rows 260 = 4 5 13, columns 130 = 5 13 2
+using Plan260 = FusedPlan<260, 4, 5, 13, 5, 13, 5>;   // rows 260 = 4 5 13, columns 130 = 5 13 2
 using Plan132 = FusedPlan<132, 4, 3, 11, 3, 11>;   // rows 132 = 4 3 11, columns 66 = 3 11 2
 
 template <class P>
