@@ -75,7 +75,9 @@ struct FusedPlan {
   static constexpr int PARK = (SLOTS + kFT - 1) / kFT;  // rounds of kFT slots parked per thread
   static constexpr int SLOTS_PAD = PARK * kFT;           // group buffer padded to whole rounds
   // the first PARK_LDS rounds are parked in the LDS space left over next to the group buffer
-  static constexpr int TAB_BYTES = (2 * NQ + 2 * M) * 2;  // int16 tables pa, pb, pos, colsrc
+  // LDS tables: radix-2 twiddles by row position (NH + 2 float2), int16 pa, pb, pos, colsrc, and a
+  // byte per row-pair position saying whether it holds the odd row's bins
+  static constexpr int TAB_BYTES = (NH + 2) * 8 + (2 * NQ + 2 * M) * 2 + RS;
   static constexpr int PARK_LDS_MAX = (163840 - SLOTS_PAD * 8 - TAB_BYTES - 64) / (kFT * 8);
   static constexpr int PARK_LDS = PARK_LDS_MAX < PARK ? PARK_LDS_MAX : PARK;
   static_assert(R1 * R2 * R3 == M && M % 2 == 0 && NP % 2 == 1, "plan");
@@ -256,8 +258,7 @@ __device__ __forceinline__ void col_pass_b(float2* buf, const short* pa, const s
 
 struct FusedArgs {
   const float* x;        // (P, H, W)
-  const float4* tab4;    // (Cp, SLOTS): (a, bW)
-  const float2* tab2;    // (Cp, SLOTS): bWi
+  const float4* tab4;    // (Cp, SLOTS): (Phi at row frequency k, Phi at k + N/2)
   float* out;            // (P, H, W)
   int64_t B, C, psf_batch;
   int H, W, pad, mode, act;
@@ -419,10 +420,12 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
   extern __shared__ float2 smem[];
   float2* buf = smem;
   float2* parkl = smem + P::SLOTS_PAD;  // PARK_LDS rounds of parked slots
-  short* pa = (short*)(parkl + P::PARK_LDS * kFT);
+  float2* wtab = parkl + P::PARK_LDS * kFT;  // exp(-2 pi i k / N) at row position rfpos(k)
+  short* pa = (short*)(wtab + P::NH + 2);
   short* pb = pa + P::NQ;
   short* pos = pb + P::NQ;
   short* colsrc = pos + P::M;
+  unsigned char* isb = (unsigned char*)(colsrc + P::M);  // 1 where a position holds the odd row
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t plane = fused_plane(blockIdx.x, a);
@@ -431,10 +434,17 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + plane * (int64_t)a.H * a.W, plane_bytes);
   const __amdgpu_buffer_rsrc_t orsrc = make_rsrc(a.out + plane * (int64_t)a.H * a.W, plane_bytes);
   const __amdgpu_buffer_rsrc_t t4r = make_rsrc(a.tab4 + cp * P::SLOTS, P::SLOTS * 16u);
-  const __amdgpu_buffer_rsrc_t t2r = make_rsrc(a.tab2 + cp * P::SLOTS, P::SLOTS * 8u);
+  for (int p = tid; p < P::RS; p += kFT) isb[p] = 0;  // spare positions: any in-range value
+  for (int k = tid; k < P::NH + 2; k += kFT) {
+    double sn = 0.0, cs = 0.0;
+    if (k < P::NH) sincospi(-2.0 * (double)k / (double)P::N, &sn, &cs);
+    wtab[k < P::NH ? P::rfpos(k) : k] = make_float2((float)cs, (float)sn);
+  }
+  lds_barrier();
   for (int q = tid; q < P::NQ; q += kFT) {
     pa[q] = P::pa(q);
     pb[q] = P::pb(q);
+    isb[P::pb(q)] = 1;
   }
   for (int j = tid; j < P::M; j += kFT) {
     pos[j] = P::pos_in(j);
@@ -470,37 +480,34 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
   // radix-2 across the groups, transfer function, inverse radix-2.  Table entries come in batches
   // of kTabBatch slots; the first batch is requested before G1's last pass.
   float4 f4[kTabBatch];
-  float2 f2[kTabBatch];
 #pragma unroll
-  for (int i = 0; i < kTabBatch; ++i) {
-    f4[i] = bload4(t4r, 16u * tid, 16u * i * kFT);
-    f2[i] = bload2(t2r, 8u * tid, 8u * i * kFT);
-  }
+  for (int i = 0; i < kTabBatch; ++i) f4[i] = bload4(t4r, 16u * tid, 16u * i * kFT);
   col_pass_b<P, false>(buf, pa, pb, tid);
   lds_barrier();
 #pragma unroll
   for (int i0 = 0; i0 < P::PARK; i0 += kTabBatch) {
     if (i0 > 0) {
 #pragma unroll
-      for (int i = 0; i < kTabBatch; ++i) {
-        f4[i] = bload4(t4r, 16u * tid, 16u * (i0 + i) * kFT);
-        f2[i] = bload2(t2r, 8u * tid, 8u * (i0 + i) * kFT);
-      }
+      for (int i = 0; i < kTabBatch; ++i) f4[i] = bload4(t4r, 16u * tid, 16u * (i0 + i) * kFT);
     }
 #pragma unroll
     for (int i = 0; i < kTabBatch; ++i) {
       const int ii = i0 + i;
       if (ii < P::PARK) {
         const int s = tid + ii * kFT;
+        const int t = s / P::RS;
+        const float2 w = wtab[2 * t + isb[s - t * P::RS]];  // radix-2 twiddle of the slot's row frequency
         const float2 e = ii < PL ? parkl[ii * kFT + tid] : park[ii < PL ? 0 : ii - PL], o = buf[s];
-        const float2 av = make_float2(f4[i].x, f4[i].y), bw = make_float2(f4[i].z, f4[i].w);
-        float2 ne = cadd(cmul(av, e), cmul(bw, o));
+        const float2 wo = cmul(w, o);
+        const float2 y0 = cmul(make_float2(f4[i].x, f4[i].y), cadd(e, wo));
+        const float2 y1 = cmul(make_float2(f4[i].z, f4[i].w), csub(e, wo));
+        float2 ne = cadd(y0, y1);
         // materialise E' here: otherwise the compiler sinks its arithmetic to the unpark and keeps
-        // e, o, a and bW (8 values per slot instead of 2) alive across the G1 inverse
+        // e, o and the table entry alive across the G1 inverse
         asm volatile("" : "+v"(ne.x), "+v"(ne.y));
         if (ii < PL) parkl[ii * kFT + tid] = ne;
         else park[ii < PL ? 0 : ii - PL] = ne;
-        buf[s] = cadd(cmul(f2[i], e), cmul(av, o));
+        buf[s] = cmul(cconj(w), csub(y0, y1));
       }
     }
     asm volatile("" ::: "memory");  // the next batch's loads may not be hoisted above this one
@@ -527,7 +534,6 @@ struct PhiFusedArgs {
   int kh, kw;
   double eps;
   float4* tab4;
-  float2* tab2;
 };
 
 __device__ __forceinline__ double2 d_cmul(double2 a, double2 b) {
@@ -565,11 +571,9 @@ __global__ void __launch_bounds__(256) k_phi_fused(PhiFusedArgs a) {
   const double norm = 1.0 / ((double)P::N * (double)P::M);
   for (int k = threadIdx.x; k < P::NH; k += blockDim.x) {
     double2 ph[2];
-    double2 wk = make_double2(1.0, 0.0);
     for (int h = 0; h < 2; ++h) {
       const int u = k + h * P::NH;
       const double2 r = d_root(u, P::N);
-      if (h == 0) wk = r;
       double2 e = d_root(-(int64_t)u * (a.kh / 2), P::N);
       double2 K = make_double2(0.0, 0.0);
       for (int i = 0; i < a.kh; ++i) {
@@ -581,14 +585,10 @@ __global__ void __launch_bounds__(256) k_phi_fused(PhiFusedArgs a) {
       const double den = (K.x * K.x + K.y * K.y + lmb) / norm;
       ph[h] = make_double2((K.x + lmb) / den, -K.y / den);
     }
-    const double2 av = make_double2(ph[0].x + ph[1].x, ph[0].y + ph[1].y);
-    const double2 bv = make_double2(ph[0].x - ph[1].x, ph[0].y - ph[1].y);
-    const double2 bw = d_cmul(bv, wk);
-    const double2 bwi = d_cmul(bv, make_double2(wk.x, -wk.y));
     const int rp = P::rfpos(k);
     const int slot = (rp >> 1) * P::RS + ((rp & 1) ? P::pb(q) : P::pa(q));
-    a.tab4[cp * P::SLOTS + slot] = make_float4((float)av.x, (float)av.y, (float)bw.x, (float)bw.y);
-    a.tab2[cp * P::SLOTS + slot] = make_float2((float)bwi.x, (float)bwi.y);
+    a.tab4[cp * P::SLOTS + slot] =
+        make_float4((float)ph[0].x, (float)ph[0].y, (float)ph[1].x, (float)ph[1].y);
   }
 }
 
@@ -600,7 +600,7 @@ using Plan132 = FusedPlan<132, 4, 3, 11, 3, 11>;   // rows 132 = 4 3 11, columns
 
 template <class P>
 size_t fused_ws(int64_t Cp) {
-  return align_up((size_t)Cp * P::SLOTS * sizeof(float4)) + align_up((size_t)Cp * P::SLOTS * sizeof(float2));
+  return align_up((size_t)Cp * P::SLOTS * sizeof(float4));
 }
 
 template <class P>
@@ -608,8 +608,7 @@ int fused_table_run(const float* psf, const float* bias, float eps, int64_t C, i
                     void* table, hipStream_t st) {
   const int64_t Cp = psf_batch * C;
   float4* t4 = (float4*)table;
-  float2* t2 = (float2*)((char*)table + align_up((size_t)Cp * P::SLOTS * sizeof(float4)));
-  PhiFusedArgs pa{psf, bias, C, kh, kw, (double)eps, t4, t2};
+  PhiFusedArgs pa{psf, bias, C, kh, kw, (double)eps, t4};
   hipLaunchKernelGGL(k_phi_fused<P>, dim3((unsigned)(Cp * P::NQ)), dim3(256), 0, st, pa);
   return check_launch("fused transfer table");
 }
@@ -625,8 +624,7 @@ int fused_apply_run(const float* x, int64_t B, int64_t C, int H, int W, int64_t 
   }
   const int64_t Cp = psf_batch * C;
   const float4* t4 = (const float4*)table;
-  const float2* t2 = (const float2*)((const char*)table + align_up((size_t)Cp * P::SLOTS * sizeof(float4)));
-  FusedArgs fa{x, t4, t2, out, B, C, psf_batch, H, W, pad, mode, act};
+  FusedArgs fa{x, t4, out, B, C, psf_batch, H, W, pad, mode, act};
   hipLaunchKernelGGL(k_converse2d_fused<P>, dim3((unsigned)(B * C)), dim3(kFT), P::LDS_BYTES, st, fa);
   return check_launch("fused converse2d");
 }
