@@ -204,6 +204,7 @@ struct RowFwdArgs {
   int NC;          // w / 2 + 1
   int rpb;         // rows per block (even)
   FftPlan plan;    // length w
+  const char* tabs;  // the plan's tables (build_plan_tabs)
   int rad_off;     // byte offset of the plan's Rader tables in LDS
   float2* S;       // (P, NC, h)
 };
@@ -217,12 +218,12 @@ __global__ void __launch_bounds__(256) k_rows_fwd(RowFwdArgs a) {
   const int64_t plane = blockIdx.y;
   const int r0 = blockIdx.x * a.rpb;
   const int tid = threadIdx.x, nth = blockDim.x;
-  build_twiddles(tw, L, tid, nth);
   char* rad = (char*)sm + a.rad_off;
-  build_rader(a.plan, rad, tid, nth);
+  load_plan_tabs(a.plan, a.tabs, tw, rad, tid, nth);
   const float* xp = a.x + plane * (int64_t)a.Hin * a.Win;
+  const FastDiv fL = fast_div(L), frpb = fast_div(a.rpb);
   for (int idx = tid; idx < ntr * L; idx += nth) {
-    const int t = idx / L, c = idx - t * L;
+    const int t = idx / fL, c = idx - t * L;
     const int ra = r0 + 2 * t, rb = ra + 1;
     const int sc = pad_src(c, a.Win, a.pad, a.mode);
     float va = 0.f, vb = 0.f;
@@ -243,7 +244,7 @@ __global__ void __launch_bounds__(256) k_rows_fwd(RowFwdArgs a) {
   // unpack two real rows: Ya = (Z[c] + conj Z[-c]) / 2, Yb = (Z[c] - conj Z[-c]) / (2i)
   float2* Sp = a.S + plane * (int64_t)a.NC * a.h;
   for (int idx = tid; idx < a.NC * a.rpb; idx += nth) {
-    const int c = idx / a.rpb, rl = idx - c * a.rpb;
+    const int c = idx / frpb, rl = idx - c * a.rpb;
     const int r = r0 + rl;
     if (r >= a.h) continue;
     const int t = rl >> 1;
@@ -268,6 +269,7 @@ struct ColModArgs {
   int64_t C, psf_batch;
   int h, w, Hs, Ws, NC, NCs, cpb;
   FftPlan plan_h, plan_H;
+  const char *tabs_h, *tabs_H;  // the plans' tables (build_plan_tabs)
   int rad_off;        // byte offset of plan_h's Rader tables in LDS (plan_H's follow)
 };
 
@@ -282,16 +284,16 @@ __global__ void __launch_bounds__(256) k_cols_module(ColModArgs a) {
   const int v0 = blockIdx.x * a.cpb;
   const int ncol = min(a.cpb, a.NCs - v0);
   const int64_t cp = (a.psf_batch == 1) ? (plane % a.C) : plane;
-  build_twiddles(twh, a.h, tid, nth);
-  if (a.Hs != a.h) build_twiddles(twH, a.Hs, tid, nth);
   const float2* tH = (a.Hs != a.h) ? twH : twh;
   char* radh = (char*)sm + a.rad_off;
   char* radH = radh + rader_lds_bytes(a.plan_h);
-  build_rader(a.plan_h, radh, tid, nth);
-  build_rader(a.plan_H, radH, tid, nth);
+  load_plan_tabs(a.plan_h, a.tabs_h, twh, radh, tid, nth);
+  if (a.Hs != a.h) load_plan_tabs(a.plan_H, a.tabs_H, twH, radH, tid, nth);
+  else radH = radh;
   const float2* Sp = a.S + plane * (int64_t)a.NC * a.h;
+  const FastDiv fh = fast_div(a.h), fHs = fast_div(a.Hs);
   for (int idx = tid; idx < a.cpb * a.h; idx += nth) {
-    const int cl = idx / a.h, u = idx - cl * a.h;
+    const int cl = idx / fh, u = idx - cl * a.h;
     float2 val = make_float2(0.f, 0.f);
     if (cl < ncol) {
       const int vv = (v0 + cl) % a.w;
@@ -305,16 +307,16 @@ __global__ void __launch_bounds__(256) k_cols_module(ColModArgs a) {
   float2* X = (Y == A) ? Bf : A;
   const float2* ph = a.phi + cp * (int64_t)a.NCs * a.Hs;
   for (int idx = tid; idx < a.cpb * a.Hs; idx += nth) {
-    const int cl = idx / a.Hs, u = idx - cl * a.Hs;
+    const int cl = idx / fHs, u = idx - cl * a.Hs;
     float2 val = make_float2(0.f, 0.f);
-    if (cl < ncol) val = cmul(Y[cl * a.h + (u % a.h)], ph[(int64_t)(v0 + cl) * a.Hs + u]);
+    if (cl < ncol) val = cmul(Y[cl * a.h + (u - (u / fh) * a.h)], ph[(int64_t)(v0 + cl) * a.Hs + u]);
     X[cl * a.Hs + u] = val;
   }
   __syncthreads();
   const float2* R = fft_lds<true>(a.plan_H, X, (X == A) ? Bf : A, a.cpb, tH, tid, nth, radH);
   float2* SHp = a.SH + plane * (int64_t)a.NCs * a.Hs;
   for (int idx = tid; idx < ncol * a.Hs; idx += nth) {
-    const int cl = idx / a.Hs, u = idx - cl * a.Hs;
+    const int cl = idx / fHs, u = idx - cl * a.Hs;
     SHp[(int64_t)(v0 + cl) * a.Hs + u] = R[cl * a.Hs + u];
   }
 }
@@ -331,6 +333,7 @@ struct ColOpArgs {
   int64_t C;
   int h, w, s, Hs, Ws, NC, NCs;
   FftPlan plan_h, plan_H;
+  const char *tabs_h, *tabs_H;  // the plans' tables (build_plan_tabs)
   int rad_off;        // byte offset of plan_h's Rader tables in LDS (plan_H's follow)
 };
 
@@ -348,19 +351,18 @@ __global__ void __launch_bounds__(256) k_cols_op(ColOpArgs a) {
   const int64_t c = plane % a.C;
   // any member with an output column?
   if (v0 > a.Ws / 2) return;  // member b = 0 is the smallest
-  build_twiddles(twh, a.h, tid, nth);
-  build_twiddles(twH, a.Hs, tid, nth);
   char* radh = (char*)sm + a.rad_off;
   char* radH = radh + rader_lds_bytes(a.plan_h);
-  build_rader(a.plan_h, radh, tid, nth);
-  build_rader(a.plan_H, radH, tid, nth);
+  load_plan_tabs(a.plan_h, a.tabs_h, twh, radh, tid, nth);
+  load_plan_tabs(a.plan_H, a.tabs_H, twH, radH, tid, nth);
   const float2* Sp = a.S + plane * (int64_t)a.NC * a.h;
   const float2* S0p = a.S0 + plane * (int64_t)a.NCs * a.Hs;
   for (int u = tid; u < a.h; u += nth) {
     Ya[u] = v0 <= a.w / 2 ? Sp[(int64_t)v0 * a.h + u] : cconj(Sp[(int64_t)(a.w - v0) * a.h + u]);
   }
+  const FastDiv fHs = fast_div(a.Hs);
   for (int idx = tid; idx < a.s * a.Hs; idx += nth) {
-    const int b = idx / a.Hs, u = idx - b * a.Hs;
+    const int b = idx / fHs, u = idx - b * a.Hs;
     const int vb = v0 + b * a.w;
     Xa[b * a.Hs + u] = vb <= a.Ws / 2 ? S0p[(int64_t)vb * a.Hs + u]
                                       : cconj(S0p[(int64_t)(a.Ws - vb) * a.Hs + u]);
@@ -395,7 +397,7 @@ __global__ void __launch_bounds__(256) k_cols_op(ColOpArgs a) {
   const float2* R = fft_lds<true>(a.plan_H, Xo, (Xo == Xa) ? Xb : Xa, a.s, twH, tid, nth, radH);
   float2* SHp = a.SH + plane * (int64_t)a.NCs * a.Hs;
   for (int idx = tid; idx < a.s * a.Hs; idx += nth) {
-    const int b = idx / a.Hs, u = idx - b * a.Hs;
+    const int b = idx / fHs, u = idx - b * a.Hs;
     const int vb = v0 + b * a.w;
     if (vb <= a.Ws / 2) SHp[(int64_t)vb * a.Hs + u] = R[b * a.Hs + u];
   }
@@ -411,6 +413,7 @@ struct RowInvArgs {
   int row0, nrows, col0, ncols;  // crop window
   int rpb, act;
   FftPlan plan;      // length Ws
+  const char* tabs;  // the plan's tables (build_plan_tabs)
   int rad_off;       // byte offset of the plan's Rader tables in LDS
 };
 
@@ -423,13 +426,13 @@ __global__ void __launch_bounds__(256) k_rows_inv(RowInvArgs a) {
   float2* Bf = A + ntr * ld;
   const int64_t plane = blockIdx.y;
   const int r0 = blockIdx.x * a.rpb;  // local output row
-  build_twiddles(tw, L, tid, nth);
   char* rad = (char*)sm + a.rad_off;
-  build_rader(a.plan, rad, tid, nth);
+  load_plan_tabs(a.plan, a.tabs, tw, rad, tid, nth);
   const float2* SHp = a.SH + plane * (int64_t)a.NCs * a.Hs;
+  const FastDiv fL = fast_div(L), frpb = fast_div(a.rpb), fnc = fast_div(a.ncols);
   // stage the half spectra: Bf[rl * NCs + v]
   for (int idx = tid; idx < a.NCs * a.rpb; idx += nth) {
-    const int v = idx / a.rpb, rl = idx - v * a.rpb;
+    const int v = idx / frpb, rl = idx - v * a.rpb;
     const int r = r0 + rl;
     float2 val = make_float2(0.f, 0.f);
     if (r < a.nrows) val = SHp[(int64_t)v * a.Hs + a.row0 + r];
@@ -438,7 +441,7 @@ __global__ void __launch_bounds__(256) k_rows_inv(RowInvArgs a) {
   }
   __syncthreads();
   for (int idx = tid; idx < ntr * L; idx += nth) {
-    const int t = idx / L, v = idx - t * L;
+    const int t = idx / fL, v = idx - t * L;
     const bool lo = v <= L / 2;
     const int vv = lo ? v : L - v;
     float2 ha = Bf[(2 * t) * a.NCs + vv], hb = Bf[(2 * t + 1) * a.NCs + vv];
@@ -449,7 +452,7 @@ __global__ void __launch_bounds__(256) k_rows_inv(RowInvArgs a) {
   const float2* Z = fft_lds<true>(a.plan, A, Bf, ntr, tw, tid, nth, rad);
   float* op = a.out + plane * (int64_t)a.nrows * a.ncols;
   for (int idx = tid; idx < a.rpb * a.ncols; idx += nth) {
-    const int rl = idx / a.ncols, cc = idx - rl * a.ncols;
+    const int rl = idx / fnc, cc = idx - rl * a.ncols;
     const int r = r0 + rl;
     if (r >= a.nrows) continue;
     const float2 z = Z[(rl >> 1) * L + a.col0 + cc];
@@ -519,13 +522,51 @@ int module_geo(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, in
   return CVN_OK;
 }
 
-struct ModWs {
-  size_t phi, S, SH, total;
+// FFT plan tables of the four transform lengths a call uses (w, h, Hs, Ws), one region each.
+struct PlanTabs {
+  FftPlan plan[4];
+  size_t off[4], bytes;
 };
-ModWs module_ws(const Geo& g) {
+enum { kTabW = 0, kTabH = 1, kTabHs = 2, kTabWs = 3 };
+bool plan_tabs(const Geo& g, PlanTabs* t) {
+  const int len[4] = {g.w, g.h, g.Hs, g.Ws};
+  size_t o = 0;
+  for (int i = 0; i < 4; ++i) {
+    if (!make_plan(len[i], &t->plan[i])) return false;
+    t->off[i] = o;
+    o += align_up(plan_tab_bytes(t->plan[i]), 256);
+  }
+  t->bytes = o;
+  return true;
+}
+
+struct PlanTabsArgs {
+  FftPlan plan[4];
+  char* dst[4];
+};
+__global__ void __launch_bounds__(256) k_plan_tabs(PlanTabsArgs a) {
+  __shared__ double2 wd[kMaxRaderLen], bd[kMaxRaderLen];
+  build_plan_tabs(a.plan[blockIdx.x], a.dst[blockIdx.x], wd, bd, threadIdx.x, blockDim.x);
+}
+int launch_plan_tabs(const PlanTabs& t, char* base, hipStream_t st) {
+  PlanTabsArgs a;
+  for (int i = 0; i < 4; ++i) {
+    a.plan[i] = t.plan[i];
+    a.dst[i] = base + t.off[i];
+  }
+  hipLaunchKernelGGL(k_plan_tabs, dim3(4), dim3(kThreads), 0, st, a);
+  return check_launch("FFT plan tables");
+}
+
+struct ModWs {
+  size_t phi, tabs, S, SH, total;
+};
+ModWs module_ws(const Geo& g, const PlanTabs& t) {
   ModWs w;
   w.phi = 0;
   size_t o = align_up((size_t)g.Cp * g.NCs * g.Hs * sizeof(float2));
+  w.tabs = o;
+  o += t.bytes;
   w.S = o;
   o += align_up((size_t)g.P * g.NC * g.h * sizeof(float2));
   if (g.s == 1) {
@@ -556,13 +597,14 @@ int launch_phi(const float* psf, const float* bias, float eps, const Geo& g, boo
 }
 
 int launch_rows_fwd(const float* x, int64_t P, int Hin, int Win, int pad, int mode, int h, int w,
-                    float2* S, hipStream_t st) {
+                    const char* tabs, float2* S, hipStream_t st) {
   RowFwdArgs a;
   a.x = x; a.Hin = Hin; a.Win = Win; a.h = h; a.w = w; a.pad = pad; a.mode = mode;
   a.NC = w / 2 + 1;
   a.rpb = rows_per_block(w, h);
   if (!make_plan(w, &a.plan)) return fail(CVN_ERR_UNSUPPORTED, "no plan for length %d", w);
   a.rad_off = (int)align_up(rows_lds(w, a.rpb), 16);
+  a.tabs = tabs;
   a.S = S;
   dim3 grid((h + a.rpb - 1) / a.rpb, (unsigned)P);
   hipLaunchKernelGGL(k_rows_fwd, grid, dim3(kThreads), a.rad_off + rader_lds_bytes(a.plan), st, a);
@@ -570,13 +612,14 @@ int launch_rows_fwd(const float* x, int64_t P, int Hin, int Win, int pad, int mo
 }
 
 int launch_rows_inv(const float2* SH, const Geo& g, int row0, int nrows, int col0, int ncols,
-                    int act, float* out, hipStream_t st) {
+                    int act, const char* tabs, float* out, hipStream_t st) {
   RowInvArgs a;
   a.SH = SH; a.out = out; a.Hs = g.Hs; a.Ws = g.Ws; a.NCs = g.NCs;
   a.row0 = row0; a.nrows = nrows; a.col0 = col0; a.ncols = ncols; a.act = act;
   a.rpb = rows_per_block(g.Ws, nrows);
   if (!make_plan(g.Ws, &a.plan)) return fail(CVN_ERR_UNSUPPORTED, "no plan for length %d", g.Ws);
   a.rad_off = (int)align_up(rows_lds(g.Ws, a.rpb), 16);
+  a.tabs = tabs;
   dim3 grid((nrows + a.rpb - 1) / a.rpb, (unsigned)g.P);
   hipLaunchKernelGGL(k_rows_inv, grid, dim3(kThreads), a.rad_off + rader_lds_bytes(a.plan), st, a);
   return check_launch("row inverse pass");
@@ -612,7 +655,9 @@ int module_route(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, 
     r->table_bytes = fws;
     r->scratch_bytes = 0;
   } else {
-    const ModWs w = module_ws(*g);
+    PlanTabs t;
+    if (!plan_tabs(*g, &t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
+    const ModWs w = module_ws(*g, t);
     r->fused = false;
     r->table_bytes = w.S;
     r->scratch_bytes = w.total - w.S;
@@ -669,6 +714,10 @@ extern "C" int cvn_converse2d_table_f32(const float* psf, int64_t psf_batch, int
     return fail(CVN_ERR_WORKSPACE, "table buffer too small: need %zu bytes", r.table_bytes);
   hipStream_t st = (hipStream_t)stream;
   if (r.fused) return fused_table(psf, bias, eps, g.C, g.Cp / g.C, kh, kw, g.H, g.W, g.pad, table, st);
+  PlanTabs t;
+  if (!plan_tabs(g, &t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
+  const ModWs ws = module_ws(g, t);
+  if ((rc = launch_plan_tabs(t, (char*)table + ws.tabs, st)) != CVN_OK) return rc;
   return launch_phi(psf, bias, eps, g, false, (float2*)table, nullptr, st);
 }
 
@@ -694,24 +743,30 @@ extern "C" int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, in
     return fail(CVN_ERR_WORKSPACE, "scratch too small: need %zu bytes", r.scratch_bytes);
   if (g.P > 65535) return fail(CVN_ERR_UNSUPPORTED, "B*C = %lld planes exceeds 65535", (long long)g.P);
   set_lds_attrs();
-  const ModWs ws = module_ws(g);
+  PlanTabs t;
+  if (!plan_tabs(g, &t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
+  const ModWs ws = module_ws(g, t);
   char* base = (char*)scratch - ws.S;  // scratch holds the workspace regions after the table
   const float2* phi = (const float2*)table;
+  const char* tabs = (const char*)table + ws.tabs;
   float2* S = (float2*)(base + ws.S);
   float2* SH = (float2*)(base + ws.SH);
-  if ((rc = launch_rows_fwd(x, g.P, g.H, g.W, g.pad, pad_mode, g.h, g.w, S, st)) != CVN_OK) return rc;
+  if ((rc = launch_rows_fwd(x, g.P, g.H, g.W, g.pad, pad_mode, g.h, g.w, tabs + t.off[kTabW], S, st)) != CVN_OK)
+    return rc;
   ColModArgs ca;
   ca.S = S; ca.phi = phi; ca.SH = SH; ca.C = g.C; ca.psf_batch = g.Cp / g.C;
   ca.h = g.h; ca.w = g.w; ca.Hs = g.Hs; ca.Ws = g.Ws; ca.NC = g.NC; ca.NCs = g.NCs;
   ca.cpb = cols_per_block(g.h, g.Hs);
   if (!make_plan(g.h, &ca.plan_h) || !make_plan(g.Hs, &ca.plan_H))
     return fail(CVN_ERR_UNSUPPORTED, "no plan for column length");
+  ca.tabs_h = tabs + t.off[kTabH];
+  ca.tabs_H = tabs + t.off[kTabHs];
   ca.rad_off = (int)align_up(cols_lds(g.h, g.Hs, ca.cpb), 16);
   hipLaunchKernelGGL(k_cols_module, dim3((g.NCs + ca.cpb - 1) / ca.cpb, (unsigned)g.P), dim3(kThreads),
                      ca.rad_off + rader_lds_bytes(ca.plan_h) + rader_lds_bytes(ca.plan_H), st, ca);
   if ((rc = check_launch("column pass")) != CVN_OK) return rc;
   const int ps = g.pad * g.s;
-  return launch_rows_inv(SH, g, ps, g.H * g.s, ps, g.W * g.s, act, out, st);
+  return launch_rows_inv(SH, g, ps, g.H * g.s, ps, g.W * g.s, act, tabs + t.off[kTabWs], out, st);
 }
 
 extern "C" int cvn_converse2d_fwd_f32(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
@@ -740,7 +795,9 @@ extern "C" size_t cvn_converse2d_op_workspace(int64_t B, int64_t C, int64_t h, i
                                               int kw, int scale) {
   Geo g;
   if (module_geo(B, C, h, w, 1, kh, kw, scale, 0, &g) != CVN_OK) return 0;
-  size_t o = 0;
+  PlanTabs t;
+  if (!plan_tabs(g, &t)) return 0;
+  size_t o = t.bytes;                                               // FFT plan tables
   o += 2 * align_up((size_t)g.C * g.Ws * g.Hs * sizeof(float2));  // kf, A
   o += align_up((size_t)g.P * g.NC * g.h * sizeof(float2));        // S
   o += align_up((size_t)g.P * g.NCs * g.Hs * sizeof(float2));      // S0
@@ -765,24 +822,33 @@ extern "C" int cvn_converse2d_op_f32(const float* x, const float* x0, int64_t B,
   set_lds_attrs();
   hipStream_t st = (hipStream_t)stream;
   char* base = (char*)workspace;
-  size_t o = 0;
+  PlanTabs t;
+  if (!plan_tabs(g, &t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
+  const char* tabs = base;
+  if ((rc = launch_plan_tabs(t, base, st)) != CVN_OK) return rc;
+  size_t o = t.bytes;
   float2* kf = (float2*)(base + o); o += align_up((size_t)g.C * g.Ws * g.Hs * sizeof(float2));
   float2* Am = (float2*)(base + o); o += align_up((size_t)g.C * g.Ws * g.Hs * sizeof(float2));
   float2* S = (float2*)(base + o); o += align_up((size_t)g.P * g.NC * g.h * sizeof(float2));
   float2* S0 = (float2*)(base + o); o += align_up((size_t)g.P * g.NCs * g.Hs * sizeof(float2));
   float2* SH = (float2*)(base + o);
   if ((rc = launch_phi(psf, bias, eps, g, true, Am, kf, st)) != CVN_OK) return rc;
-  if ((rc = launch_rows_fwd(x, g.P, g.h, g.w, 0, CVN_PAD_ZEROS, g.h, g.w, S, st)) != CVN_OK) return rc;
-  if ((rc = launch_rows_fwd(x0, g.P, g.Hs, g.Ws, 0, CVN_PAD_ZEROS, g.Hs, g.Ws, S0, st)) != CVN_OK) return rc;
+  if ((rc = launch_rows_fwd(x, g.P, g.h, g.w, 0, CVN_PAD_ZEROS, g.h, g.w, tabs + t.off[kTabW], S, st)) != CVN_OK)
+    return rc;
+  if ((rc = launch_rows_fwd(x0, g.P, g.Hs, g.Ws, 0, CVN_PAD_ZEROS, g.Hs, g.Ws, tabs + t.off[kTabWs], S0, st)) !=
+      CVN_OK)
+    return rc;
   ColOpArgs ca;
   ca.S = S; ca.S0 = S0; ca.kf = kf; ca.A = Am; ca.SH = SH; ca.C = g.C;
   ca.h = g.h; ca.w = g.w; ca.s = g.s; ca.Hs = g.Hs; ca.Ws = g.Ws; ca.NC = g.NC; ca.NCs = g.NCs;
   if (!make_plan(g.h, &ca.plan_h) || !make_plan(g.Hs, &ca.plan_H))
     return fail(CVN_ERR_UNSUPPORTED, "no plan for column length");
+  ca.tabs_h = tabs + t.off[kTabH];
+  ca.tabs_H = tabs + t.off[kTabHs];
   ca.rad_off = (int)align_up((size_t)(3 * g.h + g.Hs + 2 * g.s * g.Hs) * sizeof(float2), 16);
   const size_t lds = ca.rad_off + rader_lds_bytes(ca.plan_h) + rader_lds_bytes(ca.plan_H);
   if (lds > kLdsLimit) return fail(CVN_ERR_UNSUPPORTED, "column class does not fit in LDS");
   hipLaunchKernelGGL(k_cols_op, dim3(g.w, (unsigned)g.P), dim3(kThreads), lds, st, ca);
   if ((rc = check_launch("op column pass")) != CVN_OK) return rc;
-  return launch_rows_inv(SH, g, 0, g.Hs, 0, g.Ws, CVN_ACT_NONE, out, st);
+  return launch_rows_inv(SH, g, 0, g.Hs, 0, g.Ws, CVN_ACT_NONE, tabs + t.off[kTabWs], out, st);
 }

@@ -28,6 +28,20 @@ __device__ __forceinline__ float2 twid(float2 w) {  // table entry -> direction-
   return INV ? make_float2(w.x, -w.y) : w;
 }
 
+// Division by a block-uniform divisor d through a multiply-high with m = ceil(2^32 / d): exact for
+// a * d < 2^32, which every index here satisfies (a < 2^20, d <= 4096).  Replaces the ~30-instruction
+// integer division sequence in the index arithmetic of the FFT passes.
+struct FastDiv {
+  uint32_t m;
+  int d;
+};
+__device__ __forceinline__ FastDiv fast_div(int d) {
+  return FastDiv{d > 1 ? 0xFFFFFFFFu / (uint32_t)d + 1u : 0u, d};
+}
+__device__ __forceinline__ int operator/(int a, FastDiv f) {
+  return f.d > 1 ? (int)__umulhi((uint32_t)a, f.m) : a;
+}
+
 // cos / sin of 2 pi m / R, m in [0, R), for the odd prime radices (values computed in double and
 // rounded to float).
 template <int R> struct Roots;
@@ -229,8 +243,8 @@ struct FftPlan {
   RaderPlan rad[kMaxRader];
 };
 
-// LDS tables of one Rader prime (Rm = R - 1 entries each); wd / bd are fp64 scratch for building bf / bi.
-__host__ __device__ constexpr size_t rader_tab_bytes(int R) { return ((size_t)60 * (R - 1) + 15) / 16 * 16; }
+// Tables of one Rader prime (Rm = R - 1 entries each), the same layout in global memory and LDS.
+__host__ __device__ constexpr size_t rader_tab_bytes(int R) { return ((size_t)28 * (R - 1) + 15) / 16 * 16; }
 // Bytes of LDS a plan's Rader tables need (0 without Rader stages).
 __host__ __device__ inline size_t rader_lds_bytes(const FftPlan& plan) {
   size_t b = 0;
@@ -238,8 +252,6 @@ __host__ __device__ inline size_t rader_lds_bytes(const FftPlan& plan) {
   return b;
 }
 struct RaderTab {
-  double2* wd;  // exp(-2 pi i m / Rm)
-  double2* bd;  // b_m = exp(-2 pi i g^-m / R)
   float2* tw;   // twiddles of the inner length-Rm transforms
   float2* bf;   // FFT_Rm(b) / Rm (forward direction)
   float2* bi;   // FFT_Rm(conj b) / Rm (inverse direction)
@@ -250,13 +262,11 @@ __device__ __forceinline__ RaderTab rader_tab(char* base, const RaderPlan& rp) {
   const int Rm = rp.R - 1;
   char* b = base + rp.off;
   RaderTab t;
-  t.wd = (double2*)b;
-  t.bd = (double2*)(b + 16 * Rm);
-  t.tw = (float2*)(b + 32 * Rm);
-  t.bf = (float2*)(b + 40 * Rm);
-  t.bi = (float2*)(b + 48 * Rm);
-  t.gp = (short*)(b + 56 * Rm);
-  t.gq = (short*)(b + 58 * Rm);
+  t.tw = (float2*)b;
+  t.bf = (float2*)(b + 8 * Rm);
+  t.bi = (float2*)(b + 16 * Rm);
+  t.gp = (short*)(b + 24 * Rm);
+  t.gq = (short*)(b + 26 * Rm);
   return t;
 }
 
@@ -269,10 +279,11 @@ __device__ void stockham_pass(const float2* __restrict__ src, float2* __restrict
   const int T = L / R;
   const int twstep = L / (p * R);
   const int total = T * ntr;
+  const FastDiv fT = fast_div(T), fp = fast_div(p);
   for (int idx = tid; idx < total; idx += nth) {
-    const int t = idx / T;
+    const int t = idx / fT;
     const int i = idx - t * T;
-    const int k = i % p;
+    const int k = i - (i / fp) * p;
     const float2* s = src + t * L;
     float2* d = dst + t * L;
     float2 u[R];
@@ -298,10 +309,11 @@ __device__ void stockham_pass_generic(const float2* __restrict__ src, float2* __
   const int twstep = L / (p * R);
   const int rstep = L / R;
   const int total = T * ntr;
+  const FastDiv fT = fast_div(T), fp = fast_div(p);
   for (int idx = tid; idx < total; idx += nth) {
-    const int t = idx / T;
+    const int t = idx / fT;
     const int i = idx - t * T;
-    const int k = i % p;
+    const int k = i - (i / fp) * p;
     const float2* s = src + t * L;
     float2* d = dst + t * L;
     const int j0 = (i - k) * R + k;
@@ -361,13 +373,14 @@ __device__ float2* rader_pass(float2* src, float2* dst, int L, int p, int ntr, c
                               const RaderPlan& rp, const RaderTab& rt, int tid, int nth) {
   const int R = rp.R, Rm = R - 1, T = L / R, NB = T * ntr;
   const int twstep = L / (p * R);
+  const FastDiv fRm = fast_div(Rm), fR = fast_div(R), fT = fast_div(T), fp = fast_div(p);
   float2* tail = dst + NB * Rm;
   for (int idx = tid; idx < NB * Rm; idx += nth) {
-    const int b = idx / Rm, q = idx - b * Rm;
-    const int t = b / T, i = b - t * T;
+    const int b = idx / fRm, q = idx - b * Rm;
+    const int t = b / fT, i = b - t * T;
     const int j = rt.gp[q];
     float2 v = src[t * L + i + j * T];
-    if (p > 1) v = cmul(v, twid<INV>(tw[j * (i % p) * twstep]));
+    if (p > 1) v = cmul(v, twid<INV>(tw[j * (i - (i / fp) * p) * twstep]));
     dst[idx] = v;
     if (q == 0) tail[b] = src[t * L + i];
   }
@@ -375,7 +388,7 @@ __device__ float2* rader_pass(float2* src, float2* dst, int L, int p, int ntr, c
   float2* F = fft_fixed<false>(rp.radix, rp.nst, Rm, dst, src, NB, rt.tw, tid, nth);
   const float2* bh = INV ? rt.bi : rt.bf;
   for (int idx = tid; idx < NB * Rm; idx += nth) {
-    const int b = idx / Rm, m = idx - b * Rm;
+    const int b = idx / fRm, m = idx - b * Rm;
     const float2 v = F[idx];
     float2 w = cmul(v, bh[m]);
     if (m == 0) {  // X_0 = u_0 + sum_p a_p; adding u_0 to bin 0 adds it to every convolution output
@@ -388,9 +401,9 @@ __device__ float2* rader_pass(float2* src, float2* dst, int L, int p, int ntr, c
   __syncthreads();
   const float2* C = fft_fixed<true>(rp.radix, rp.nst, Rm, F, F == dst ? src : dst, NB, rt.tw, tid, nth);
   for (int idx = tid; idx < NB * R; idx += nth) {
-    const int b = idx / R, r = idx - b * R;
-    const int t = b / T, i = b - t * T;
-    const int k = i % p;
+    const int b = idx / fR, r = idx - b * R;
+    const int t = b / fT, i = b - t * T;
+    const int k = i - (i / fp) * p;
     const int n = r == 0 ? 0 : rt.gq[r - 1];
     src[t * L + (i - k) * R + k + n * p] = r == 0 ? tail[b] : C[b * Rm + r - 1];
   }
@@ -398,45 +411,59 @@ __device__ float2* rader_pass(float2* src, float2* dst, int L, int p, int ntr, c
   return src;
 }
 
-__device__ __forceinline__ int powmod_dev(int g, int e, int m) {
-  int r = 1 % m;
-  for (int i = 0; i < e; ++i) r = (r * g) % m;
+__device__ __forceinline__ int powmod_dev(int g, int e, int m) {  // g^e mod m, binary exponentiation
+  int r = 1 % m, b = g % m;
+  while (e > 0) {
+    if (e & 1) r = (r * b) % m;
+    b = (b * b) % m;
+    e >>= 1;
+  }
   return r;
 }
 
-// Fills the Rader tables of every Rader prime of `plan` into the LDS area `base`.  All threads of
-// the block call it; it synchronises.
-__device__ void build_rader(const FftPlan& plan, char* base, int tid, int nth) {
-  if (plan.nrad == 0) return;
+// ---- plan tables: the twiddles exp(-2 pi i m / L), m < L (fp64-evaluated, rounded once), then the
+// Rader tables of each Rader prime.  Built once per geometry into global memory by build_plan_tabs
+// and copied into LDS by each block with load_plan_tabs.
+__host__ __device__ inline size_t plan_tw_bytes(const FftPlan& plan) { return ((size_t)8 * plan.L + 15) / 16 * 16; }
+__host__ __device__ inline size_t plan_tab_bytes(const FftPlan& plan) {
+  return plan_tw_bytes(plan) + rader_lds_bytes(plan);
+}
+
+// One block writes the plan's tables to `g` (16-byte aligned).  `wd` / `bd` are fp64 scratch of
+// kMaxRaderLen entries each (LDS).  All threads of the block call it.
+__device__ void build_plan_tabs(const FftPlan& plan, char* g, double2* wd, double2* bd, int tid, int nth) {
+  float2* tw = (float2*)g;
+  for (int m = tid; m < plan.L; m += nth) {
+    double sn, cs;
+    sincospi(-2.0 * (double)m / (double)plan.L, &sn, &cs);
+    tw[m] = make_float2((float)cs, (float)sn);
+  }
+  char* rbase = g + plan_tw_bytes(plan);
   for (int r = 0; r < plan.nrad; ++r) {
     const RaderPlan& rp = plan.rad[r];
-    const RaderTab t = rader_tab(base, rp);
+    const RaderTab t = rader_tab(rbase, rp);
     const int Rm = rp.R - 1;
+    __syncthreads();  // wd / bd reuse across primes
     for (int m = tid; m < Rm; m += nth) {
       const int gq = powmod_dev(rp.ginv, m, rp.R);
       t.gp[m] = (short)powmod_dev(rp.g, m, rp.R);
       t.gq[m] = (short)gq;
       double sn, cs;
       sincospi(-2.0 * (double)m / (double)Rm, &sn, &cs);
-      t.wd[m] = make_double2(cs, sn);
+      wd[m] = make_double2(cs, sn);
       t.tw[m] = make_float2((float)cs, (float)sn);
       sincospi(-2.0 * (double)gq / (double)rp.R, &sn, &cs);
-      t.bd[m] = make_double2(cs, sn);
+      bd[m] = make_double2(cs, sn);
     }
-  }
-  __syncthreads();
-  for (int r = 0; r < plan.nrad; ++r) {
-    const RaderPlan& rp = plan.rad[r];
-    const RaderTab t = rader_tab(base, rp);
-    const int Rm = rp.R - 1;
+    __syncthreads();
     for (int m = tid; m < Rm; m += nth) {
       double fr = 0.0, fi = 0.0, ir = 0.0, ii = 0.0;
-      int e = 0;  // (p m) mod Rm
+      int e = 0;  // (q m) mod Rm
       for (int q = 0; q < Rm; ++q) {
-        const double2 b = t.bd[q], w = t.wd[e];
+        const double2 b = bd[q], w = wd[e];
         fr += b.x * w.x - b.y * w.y;
         fi += b.x * w.y + b.y * w.x;
-        ir += b.x * w.x + b.y * w.y;   // conj(b) w
+        ir += b.x * w.x + b.y * w.y;  // conj(b) w
         ii += b.x * w.y - b.y * w.x;
         e += m;
         if (e >= Rm) e -= Rm;
@@ -446,12 +473,22 @@ __device__ void build_rader(const FftPlan& plan, char* base, int tid, int nth) {
       t.bi[m] = make_float2((float)(ir * sc), (float)(ii * sc));
     }
   }
-  __syncthreads();
+}
+
+// Copies the plan's tables from global `g` into the block's LDS: twiddles to `tw`, Rader tables to
+// `rader`.  All threads call it; the caller synchronises before use.
+__device__ __forceinline__ void load_plan_tabs(const FftPlan& plan, const char* g, float2* tw, char* rader, int tid,
+                                               int nth) {
+  const float2* gt = (const float2*)g;
+  for (int m = tid; m < plan.L; m += nth) tw[m] = gt[m];
+  const int nr = (int)(rader_lds_bytes(plan) / 16);
+  const float4* gr = (const float4*)(g + plan_tw_bytes(plan));
+  for (int i = tid; i < nr; i += nth) ((float4*)rader)[i] = gr[i];
 }
 
 // Runs the whole plan on `ntr` transforms held in buffer a (workspace b of equal size).  Returns
 // the buffer holding the result.  All threads of the block must call it; it synchronises.
-// `rader` is the plan's Rader LDS area (filled by build_rader), or null when plan.nrad == 0.
+// `rader` is the plan's Rader LDS area (filled by load_plan_tabs), or null when plan.nrad == 0.
 template <bool INV>
 __device__ float2* fft_lds(const FftPlan& plan, float2* a, float2* b, int ntr, const float2* tw,
                            int tid, int nth, char* rader = nullptr) {
@@ -486,15 +523,6 @@ __device__ float2* fft_lds(const FftPlan& plan, float2* a, float2* b, int ntr, c
     dst = t;
   }
   return src;
-}
-
-// exp(-2 pi i m / L) for m in [0, L), fp64-evaluated, written cooperatively into LDS.
-__device__ __forceinline__ void build_twiddles(float2* tw, int L, int tid, int nth) {
-  for (int m = tid; m < L; m += nth) {
-    double sn, cs;
-    sincospi(-2.0 * (double)m / (double)L, &sn, &cs);
-    tw[m] = make_float2((float)cs, (float)sn);
-  }
 }
 
 }  // namespace cvn
