@@ -286,7 +286,7 @@ __device__ __forceinline__ int fpad_src(int i, int n, int p, int mode) {
   }
 }
 
-__device__ __forceinline__ float fgelu(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
+__device__ __forceinline__ float fgelu(float v) { return gelu_fast(v); }
 
 // Rows of one group as float4 loads: wave w takes row positions w, w + 16, ...; lane l the source
 // columns 4 l .. 4 l + 3.  RPW = rows per wave (rounded up).

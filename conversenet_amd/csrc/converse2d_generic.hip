@@ -41,7 +41,7 @@ __device__ __forceinline__ int pad_src(int i, int n, int p, int mode) {
   }
 }
 
-__device__ __forceinline__ float gelu_exact(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
+__device__ __forceinline__ float gelu_exact(float v) { return gelu_fast(v); }
 
 __device__ __forceinline__ double2 dcmul(double2 a, double2 b) {
   return make_double2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);

@@ -20,7 +20,7 @@ namespace cvn {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float gelu_f(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
+__device__ __forceinline__ float gelu_f(float v) { return gelu_fast(v); }
 
 __device__ __forceinline__ v4f mfma4(float a, float b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -76,11 +76,12 @@ __global__ void __launch_bounds__(256) k_ln_cf_any(const float* __restrict__ x, 
 // ------------------------------------------------------------------------------------------------
 // shared pieces of the MFMA kernels
 // ------------------------------------------------------------------------------------------------
-// Stage W (rows x cols, row-major in global) transposed into LDS: Wt[k * ld + i] = W[i][k].
-__device__ __forceinline__ void stage_wt(const float* __restrict__ W, int rows, int cols, float* Wt, int ld) {
-  for (int e = threadIdx.x; e < rows * cols; e += blockDim.x) {
-    const int i = e / cols, k = e - i * cols;
-    Wt[k * ld + i] = W[e];
+// Stage W (ROWS x COLS, row-major in global) transposed into LDS: Wt[k * LD + i] = W[i][k].
+template <int ROWS, int COLS, int LD>
+__device__ __forceinline__ void stage_wt(const float* __restrict__ W, float* Wt) {
+  for (int e = threadIdx.x; e < ROWS * COLS; e += blockDim.x) {
+    const int i = e / COLS, k = e - i * COLS;
+    Wt[k * LD + i] = W[e];
   }
 }
 
@@ -126,16 +127,16 @@ __device__ __forceinline__ void ln_tile(float4 (&xv)[CIN / 4], int g, const floa
     q.x += __shfl_xor(q.x, m); q.y += __shfl_xor(q.y, m);
     q.z += __shfl_xor(q.z, m); q.w += __shfl_xor(q.w, m);
   }
-  const float4 den = make_float4(sqrtf(q.x * inv + eps), sqrtf(q.y * inv + eps), sqrtf(q.z * inv + eps),
-                                 sqrtf(q.w * inv + eps));
+  const float4 rs = make_float4(1.0f / sqrtf(q.x * inv + eps), 1.0f / sqrtf(q.y * inv + eps),
+                                1.0f / sqrtf(q.z * inv + eps), 1.0f / sqrtf(q.w * inv + eps));
 #pragma unroll
   for (int ks = 0; ks < CIN / 4; ++ks) {
     const int k = 4 * ks + g;
     const float ww = lw[k], bb = lb[k];
-    xv[ks].x = fmaf(ww, (xv[ks].x - u.x) / den.x, bb);
-    xv[ks].y = fmaf(ww, (xv[ks].y - u.y) / den.y, bb);
-    xv[ks].z = fmaf(ww, (xv[ks].z - u.z) / den.z, bb);
-    xv[ks].w = fmaf(ww, (xv[ks].w - u.w) / den.w, bb);
+    xv[ks].x = fmaf(ww * rs.x, xv[ks].x - u.x, bb);
+    xv[ks].y = fmaf(ww * rs.y, xv[ks].y - u.y, bb);
+    xv[ks].z = fmaf(ww * rs.z, xv[ks].z - u.z, bb);
+    xv[ks].w = fmaf(ww * rs.w, xv[ks].w - u.w, bb);
   }
 }
 
@@ -204,7 +205,7 @@ __global__ void __launch_bounds__(256) k_conv1x1_mfma(const float* __restrict__ 
                                                       const float* __restrict__ res_scale, float* y) {
   constexpr int LD = COUT + 16;
   __shared__ float Wt[CIN * LD];
-  stage_wt(W, COUT, CIN, Wt, LD);
+  stage_wt<COUT, CIN, LD>(W, Wt);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, j = lane & 15;
   const int64_t b = blockIdx.y;
@@ -232,8 +233,8 @@ __global__ void __launch_bounds__(256) k_ln_mlp_mfma(const float* x, int64_t HW,
   constexpr int LD2 = C + 16;   // W2t[k][i], k < CM, i < C
   __shared__ float W1t[C * LD1];
   __shared__ float W2t[CM * LD2];
-  stage_wt(W1, CM, C, W1t, LD1);
-  stage_wt(W2, C, CM, W2t, LD2);
+  stage_wt<CM, C, LD1>(W1, W1t);
+  stage_wt<C, CM, LD2>(W2, W2t);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, j = lane & 15;
   const int64_t b = blockIdx.y;
