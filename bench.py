@@ -13,7 +13,8 @@ The same JSON line carries:
   cpu_baseline  the reference's own C++ op (oracle/_ref, built from the reference source) timed on
                 this host's cores on the same workload, in a subprocess (its op namespace collides
                 with this package's); falls back to the numpy oracle ("port") if it is not built
-  extra         LayerNorm and 1x1+GELU rooflines at the cfg3 shape, Converse-DnCNN (cfg4) images/s
+  extra         LayerNorm and 1x1+GELU rooflines at the cfg3 shape, single-layer cfg1 and cfg2 timings,
+                Converse-DnCNN (cfg4) and Converse-USRNet (cfg5) images/s
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-model]
 """
@@ -21,6 +22,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import platform
 import statistics
@@ -148,17 +150,74 @@ def load_traffic(name):
         return None
 
 
+def synthetic_image(torch, g, H=256, W=256):
+    """Smooth synthetic image in [0, 1]: the sum of 8 sinusoids (frequency U[1, 16] cycles per image,
+    random orientation and phase) plus 4-8 random axis-aligned constant patches, min-max normalised."""
+    yy, xx = torch.meshgrid(torch.arange(H, dtype=torch.float64) / H, torch.arange(W, dtype=torch.float64) / W,
+                            indexing="ij")
+    img = torch.zeros(H, W, dtype=torch.float64)
+    for _ in range(8):
+        f = 1 + 15 * torch.rand(1, generator=g, dtype=torch.float64)
+        th = math.pi * torch.rand(1, generator=g, dtype=torch.float64)
+        ph = 2 * math.pi * torch.rand(1, generator=g, dtype=torch.float64)
+        img += torch.sin(2 * math.pi * f * (xx * torch.cos(th) + yy * torch.sin(th)) + ph)
+    for _ in range(int(torch.randint(4, 9, (1,), generator=g))):
+        r0, c0 = (int(v) for v in torch.randint(0, H - 16, (2,), generator=g))
+        hh, ww = (int(v) for v in torch.randint(16, H // 2, (2,), generator=g))
+        img[r0:r0 + hh, c0:c0 + ww] = 4 * (torch.rand(1, generator=g, dtype=torch.float64) - 0.5)
+    img = (img - img.min()) / (img.max() - img.min())
+    return img.float()
+
+
 def make_dncnn(torch, dev):
     """Converse-DnCNN (cfg4): default constructor (k7, p6, circular, 20 blocks, 796,353 params),
-    random init (seed 0), B=8 1x256x256 synthetic noisy input."""
+    random init (seed 0), B=8 synthetic 1x256x256 images plus N(0, (25/255)^2) noise, not clipped."""
     sys.path.insert(0, ROOT)
     from conversenet_amd.converse_dncnn import ConverseDnCNN
 
     torch.manual_seed(0)
     m = ConverseDnCNN().to(dev).eval()
     g = torch.Generator().manual_seed(0)
-    x = (torch.rand(8, 1, 256, 256, generator=g) + torch.randn(8, 1, 256, 256, generator=g) * (25 / 255)).to(dev)
+    clean = torch.stack([synthetic_image(torch, g)[None] for _ in range(8)])
+    x = (clean + torch.randn(clean.shape, generator=g) * (25 / 255)).to(dev)
     return m, x
+
+
+def make_usrnet(torch, dev):
+    """Converse-USRNet (cfg5) with KernelNet(kernel_size=25), random init (seed 0), alpha1 / alpha2 /
+    d.alpha drawn from N(0, 0.1) so the body blocks contribute.  Input: B=4 RGB 256x256 synthetic images
+    blurred circularly by a seeded 25x25 anisotropic Gaussian (sigma1, sigma2 ~ U[0.7, 3], angle ~ U[0, pi),
+    centred at (12, 12), sum 1), decimated [0::4, 0::4], plus N(0, (2.55/255)^2); the kernel is the
+    model's second input, scale factor 4."""
+    sys.path.insert(0, ROOT)
+    from conversenet_amd.converse_usrnet import ConverseUSRNet
+
+    torch.manual_seed(0)
+    m = ConverseUSRNet(kernel_size=25)
+    with torch.no_grad():
+        for prm in (m.d.alpha, *[b.alpha1 for b in m.p.m_body], *[b.alpha2 for b in m.p.m_body]):
+            prm.normal_(0, 0.1)
+    m = m.to(dev).eval()
+    g = torch.Generator().manual_seed(0)
+    xs, ks = [], []
+    for _ in range(4):
+        hr = torch.stack([synthetic_image(torch, g) for _ in range(3)]).double()
+        s1, s2 = (0.7 + 2.3 * torch.rand(2, generator=g, dtype=torch.float64)).tolist()
+        th = float(math.pi * torch.rand(1, generator=g, dtype=torch.float64))
+        yy, xx = torch.meshgrid(torch.arange(25, dtype=torch.float64) - 12, torch.arange(25, dtype=torch.float64) - 12,
+                                indexing="ij")
+        u = xx * math.cos(th) + yy * math.sin(th)
+        v = -xx * math.sin(th) + yy * math.cos(th)
+        k = torch.exp(-0.5 * (u ** 2 / s1 ** 2 + v ** 2 / s2 ** 2))
+        k = k / k.sum()
+        kp = torch.zeros(256, 256, dtype=torch.float64)
+        kp[:25, :25] = k
+        kp = torch.roll(kp, shifts=(-12, -12), dims=(0, 1))
+        blur = torch.fft.ifftn(torch.fft.fftn(hr, dim=(-2, -1)) * torch.fft.fftn(kp), dim=(-2, -1)).real
+        lr = blur[:, 0::4, 0::4] + torch.randn(3, 64, 64, generator=g, dtype=torch.float64) * (2.55 / 255)
+        xs.append(lr.float())
+        ks.append(k.float()[None])
+    return m, torch.stack(xs).to(dev), torch.stack(ks).to(dev)
 
 
 def bench_model(torch, dev, iters=3):
@@ -170,6 +229,31 @@ def bench_model(torch, dev, iters=3):
         t = time_events(torch, lambda: m(x), iters)
     return {"workload": "cfg4 Converse-DnCNN B8 1x256x256 fp32 (k7 p6, 20 blocks)", "ms_per_batch": t * 1e3,
             "images_per_s": 8 / t, "params": sum(p.numel() for p in m.parameters()), "iters": iters}
+
+
+def bench_usrnet(torch, dev, iters=3):
+    """Converse-USRNet (cfg5) images/s."""
+    m, x, k = make_usrnet(torch, dev)
+    with torch.no_grad():
+        m(x, k, 4)
+        torch.cuda.synchronize()
+        t = time_events(torch, lambda: m(x, k, 4), iters)
+    return {"workload": "cfg5 Converse-USRNet B4 3x64x64 -> 256x256 x4, KernelNet(25) fp32", "ms_per_batch": t * 1e3,
+            "images_per_s": 4 / t, "params": sum(p.numel() for p in m.parameters()), "iters": iters}
+
+
+def bench_layer(torch, Fh, dev, B, C, H, W, k, s, p, dist, iters):
+    """One Converse2D layer (module level, cached table) at a survey configuration: time and Gpix*ch/s."""
+    g0 = torch.Generator().manual_seed(0)
+    x = (torch.rand(B, C, H, W, generator=g0) if dist == "uniform" else torch.randn(B, C, H, W, generator=g0)).to(dev)
+    g1 = torch.Generator().manual_seed(1)
+    w = torch.softmax(torch.randn(1, C, k * k, generator=g1), dim=-1).reshape(1, C, k, k).to(dev)
+    b = torch.zeros(C, device=dev)
+    fn = lambda: Fh.converse2d_fused(x, w, b, s, p, "circular", 1e-5)
+    t = time_events(torch, fn, iters)
+    nbytes = 4 * B * C * H * W + 4 * B * C * H * s * W * s + 4 * C * (k * k + 1)
+    return {"workload": f"Converse2D B{B} C{C} {H}x{W} k{k} s{s} p{p} circular", "ms": t * 1e3,
+            "Gpix*ch/s": B * C * H * s * W * s / t / 1e9, "GB/s": nbytes / t / 1e9, "frac_hbm": nbytes / t / HBM_PEAK}
 
 
 def only_kernel(torch, Fh, args, dev, x, step):
@@ -192,6 +276,10 @@ def only_kernel(torch, Fh, args, dev, x, step):
         m, xin = make_dncnn(torch, dev)
         torch.set_grad_enabled(False)
         fn = lambda: m(xin)
+    elif args.only == "usrnet":
+        m, xin, kin = make_usrnet(torch, dev)
+        torch.set_grad_enabled(False)
+        fn = lambda: m(xin, kin, 4)
     else:
         raise SystemExit(f"unknown --only {args.only}")
     for _ in range(args.warmup):
@@ -215,7 +303,7 @@ def main():
     ap.add_argument("--cpu-worker", action="store_true")
     ap.add_argument("--cpu-iters", type=int, default=3)
     ap.add_argument("--cpu-threads", type=int, default=16)
-    ap.add_argument("--only", choices=["converse2d", "layernorm", "conv1x1", "copy", "dncnn"],
+    ap.add_argument("--only", choices=["converse2d", "layernorm", "conv1x1", "copy", "dncnn", "usrnet"],
                     help="run one kernel family alone (for rocprofv3)")
     args = ap.parse_args()
 
@@ -279,6 +367,9 @@ def main():
                                 "frac_mfma": cv_flops / t_cv / FP32_MFMA_PEAK}
     if not args.no_model:
         extra["converse_dncnn"] = bench_model(torch, dev)
+        extra["converse_usrnet"] = bench_usrnet(torch, dev)
+    extra["cfg1"] = bench_layer(torch, Fh, dev, 1, 64, 128, 128, 5, 1, 2, "uniform", max(20, args.steps))
+    extra["cfg2"] = bench_layer(torch, Fh, dev, 8, 64, 64, 64, 3, 2, 1, "normal", max(20, args.steps))
 
     cpu = None
     if not args.no_cpu:
