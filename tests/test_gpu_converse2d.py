@@ -215,3 +215,39 @@ def test_rader_op_level(s):
     dev = torch.device("cuda")
     got = Fh.converse2d_op(*(torch.from_numpy(a).to(dev) for a in (x, x0, wt, b)), s, 1e-5).cpu().numpy()
     assert np.abs(got - ref).max() <= TOL
+
+
+# ---------------------------------------------------------------------------------------------
+# 268 x 268 planes (Converse-DnCNN: 256^2, padding 6): in-place prime-factor path 268 = 4 * 67
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("k", [7, 5])
+def test_pfa268_vs_oracle(mode, k):
+    rng = seeded("pfa268", mode, k)
+    B, C, H, W = 2, 3, 256, 256
+    x = rng.standard_normal((B, C, H, W)).astype(np.float32)
+    w = softmax_psf(rng, C, k)
+    b = (0.4 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    ref = O.converse2d_module(x, w, b, 1, 6, mode, 1e-5)
+    got = _run_fused(x, w, b, 1, 6, mode, 1e-5)
+    err = np.abs(got - ref).max()
+    print(f"pfa268 {mode} k{k}: max-abs {err:.3e}")
+    assert err <= TOL, err
+
+
+def test_pfa268_per_sample_psf_gelu_and_generic_agreement(monkeypatch):
+    from conversenet_amd import functional as Fh
+    rng = seeded("pfa268-ps")
+    B, C, H, W, k = 2, 2, 258, 258, 7
+    x = rng.standard_normal((B, C, H, W)).astype(np.float32)
+    w = softmax_psf(rng, C, k, batch=B)
+    b = (0.4 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    ref = O.gelu(O.converse2d_module(x, w, b, 1, 5, "circular", 1e-3))
+    dev = torch.device("cuda")
+    args = (torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev), torch.from_numpy(b).reshape(-1).to(dev), 1, 5,
+            "circular", 1e-3)
+    got = Fh.converse2d_fused(*args, act="gelu").cpu().numpy()
+    assert np.abs(got - ref).max() <= TOL
+    monkeypatch.setenv("CVN_DISABLE_FUSED", "1")
+    generic = Fh.converse2d_fused(*args, act="gelu", cache=False).cpu().numpy()
+    assert np.abs(got - generic).max() <= TOL
