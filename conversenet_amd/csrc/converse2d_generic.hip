@@ -43,6 +43,10 @@ __device__ __forceinline__ int pad_src(int i, int n, int p, int mode) {
 
 __device__ __forceinline__ float gelu_exact(float v) { return gelu_fast(v); }
 
+// Global-memory loops issue kBatch independent loads per thread before using any of them, so each
+// wave keeps many requests in flight (a plain loop waits out the full memory latency per element).
+constexpr int kBatch = 8;
+
 __device__ __forceinline__ double2 dcmul(double2 a, double2 b) {
   return make_double2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
 }
@@ -222,22 +226,33 @@ __global__ void __launch_bounds__(256) k_rows_fwd(RowFwdArgs a) {
   load_plan_tabs(a.plan, a.tabs, tw, rad, tid, nth);
   const float* xp = a.x + plane * (int64_t)a.Hin * a.Win;
   const FastDiv fL = fast_div(L), frpb = fast_div(a.rpb);
-  for (int idx = tid; idx < ntr * L; idx += nth) {
-    const int t = idx / fL, c = idx - t * L;
-    const int ra = r0 + 2 * t, rb = ra + 1;
-    const int sc = pad_src(c, a.Win, a.pad, a.mode);
-    float va = 0.f, vb = 0.f;
-    if (sc >= 0) {
-      if (ra < a.h) {
-        const int sr = pad_src(ra, a.Hin, a.pad, a.mode);
-        if (sr >= 0) va = xp[(int64_t)sr * a.Win + sc];
-      }
-      if (rb < a.h) {
-        const int sr = pad_src(rb, a.Hin, a.pad, a.mode);
-        if (sr >= 0) vb = xp[(int64_t)sr * a.Win + sc];
+  for (int i0 = tid; i0 < ntr * L; i0 += kBatch * nth) {
+    float2 v[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int idx = i0 + k * nth;
+      v[k] = make_float2(0.f, 0.f);
+      if (idx < ntr * L) {
+        const int t = idx / fL, c = idx - t * L;
+        const int ra = r0 + 2 * t, rb = ra + 1;
+        const int sc = pad_src(c, a.Win, a.pad, a.mode);
+        if (sc >= 0) {
+          if (ra < a.h) {
+            const int sr = pad_src(ra, a.Hin, a.pad, a.mode);
+            if (sr >= 0) v[k].x = xp[(int64_t)sr * a.Win + sc];
+          }
+          if (rb < a.h) {
+            const int sr = pad_src(rb, a.Hin, a.pad, a.mode);
+            if (sr >= 0) v[k].y = xp[(int64_t)sr * a.Win + sc];
+          }
+        }
       }
     }
-    A[t * L + c] = make_float2(va, vb);
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int idx = i0 + k * nth;
+      if (idx < ntr * L) A[idx] = v[k];  // A[t L + c] with idx = t L + c
+    }
   }
   __syncthreads();
   const float2* Z = fft_lds<false>(a.plan, A, Bf, ntr, tw, tid, nth, rad);
@@ -292,25 +307,50 @@ __global__ void __launch_bounds__(256) k_cols_module(ColModArgs a) {
   else radH = radh;
   const float2* Sp = a.S + plane * (int64_t)a.NC * a.h;
   const FastDiv fh = fast_div(a.h), fHs = fast_div(a.Hs);
-  for (int idx = tid; idx < a.cpb * a.h; idx += nth) {
-    const int cl = idx / fh, u = idx - cl * a.h;
-    float2 val = make_float2(0.f, 0.f);
-    if (cl < ncol) {
-      const int vv = (v0 + cl) % a.w;
-      // row spectra of a real row are Hermitian in the column index (same row)
-      val = vv <= a.w / 2 ? Sp[(int64_t)vv * a.h + u] : cconj(Sp[(int64_t)(a.w - vv) * a.h + u]);
+  for (int i0 = tid; i0 < a.cpb * a.h; i0 += kBatch * nth) {
+    float2 val[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int idx = i0 + k * nth;
+      val[k] = make_float2(0.f, 0.f);
+      if (idx < a.cpb * a.h) {
+        const int cl = idx / fh, u = idx - cl * a.h;
+        if (cl < ncol) {
+          const int vv = (v0 + cl) % a.w;
+          // row spectra of a real row are Hermitian in the column index (same row)
+          val[k] = vv <= a.w / 2 ? Sp[(int64_t)vv * a.h + u] : cconj(Sp[(int64_t)(a.w - vv) * a.h + u]);
+        }
+      }
     }
-    A[cl * a.h + u] = val;
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int idx = i0 + k * nth;
+      if (idx < a.cpb * a.h) A[idx] = val[k];  // A[cl h + u] with idx = cl h + u
+    }
   }
   __syncthreads();
   float2* Y = fft_lds<false>(a.plan_h, A, Bf, a.cpb, twh, tid, nth, radh);
   float2* X = (Y == A) ? Bf : A;
   const float2* ph = a.phi + cp * (int64_t)a.NCs * a.Hs;
-  for (int idx = tid; idx < a.cpb * a.Hs; idx += nth) {
-    const int cl = idx / fHs, u = idx - cl * a.Hs;
-    float2 val = make_float2(0.f, 0.f);
-    if (cl < ncol) val = cmul(Y[cl * a.h + (u - (u / fh) * a.h)], ph[(int64_t)(v0 + cl) * a.Hs + u]);
-    X[cl * a.Hs + u] = val;
+  for (int i0 = tid; i0 < a.cpb * a.Hs; i0 += kBatch * nth) {
+    float2 f[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int idx = i0 + k * nth;
+      f[k] = make_float2(0.f, 0.f);
+      if (idx < a.cpb * a.Hs) {
+        const int cl = idx / fHs, u = idx - cl * a.Hs;
+        if (cl < ncol) f[k] = ph[(int64_t)(v0 + cl) * a.Hs + u];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int idx = i0 + k * nth;
+      if (idx < a.cpb * a.Hs) {
+        const int cl = idx / fHs, u = idx - cl * a.Hs;
+        X[idx] = cl < ncol ? cmul(Y[cl * a.h + (u - (u / fh) * a.h)], f[k]) : make_float2(0.f, 0.f);
+      }
+    }
   }
   __syncthreads();
   const float2* R = fft_lds<true>(a.plan_H, X, (X == A) ? Bf : A, a.cpb, tH, tid, nth, radH);
@@ -431,13 +471,26 @@ __global__ void __launch_bounds__(256) k_rows_inv(RowInvArgs a) {
   const float2* SHp = a.SH + plane * (int64_t)a.NCs * a.Hs;
   const FastDiv fL = fast_div(L), frpb = fast_div(a.rpb), fnc = fast_div(a.ncols);
   // stage the half spectra: Bf[rl * NCs + v]
-  for (int idx = tid; idx < a.NCs * a.rpb; idx += nth) {
-    const int v = idx / frpb, rl = idx - v * a.rpb;
-    const int r = r0 + rl;
-    float2 val = make_float2(0.f, 0.f);
-    if (r < a.nrows) val = SHp[(int64_t)v * a.Hs + a.row0 + r];
-    if (v == 0 || 2 * v == L) val.y = 0.f;
-    Bf[rl * a.NCs + v] = val;
+  for (int i0 = tid; i0 < a.NCs * a.rpb; i0 += kBatch * nth) {
+    float2 val[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int idx = i0 + k * nth;
+      val[k] = make_float2(0.f, 0.f);
+      if (idx < a.NCs * a.rpb) {
+        const int v = idx / frpb, rl = idx - v * a.rpb;
+        if (r0 + rl < a.nrows) val[k] = SHp[(int64_t)v * a.Hs + a.row0 + r0 + rl];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int idx = i0 + k * nth;
+      if (idx < a.NCs * a.rpb) {
+        const int v = idx / frpb, rl = idx - v * a.rpb;
+        if (v == 0 || 2 * v == L) val[k].y = 0.f;
+        Bf[rl * a.NCs + v] = val[k];
+      }
+    }
   }
   __syncthreads();
   for (int idx = tid; idx < ntr * L; idx += nth) {
