@@ -200,6 +200,164 @@ __global__ void k_phi_op(PhiArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------
+// Transfer tables, block-tiled form (module and op tables), scale S <= 4.  One block per (psf plane,
+// chunk of vc consecutive LR column classes v0).  The block first builds, in LDS and in fp64,
+// z_u = exp(-2 pi i u / Hs), the centring phase exp(+2 pi i u ch / Hs) and the hold response of
+// every HR row u, the same three quantities for the chunk's HR columns vb = v0 + b w, and the psf
+// row sums P[v][b][i] = sum_j psf[i][j] exp(-2 pi i vb (j - cw) / Ws).  Then one thread per alias
+// class (u0, v0) evaluates the S*S members' K = phase_u * sum_i P[v][b][i] z_u^i (Horner's rule as
+// four interleaved chains in z^4, four fp64 FMAs per psf row), keeps them in registers for the
+// class sums, and writes the class's table entries (coalesced along u).  Same quantities and
+// formulas as k_phi_module / k_phi_op.
+// ------------------------------------------------------------------------------------------------
+struct PhiTileLds {
+  int zH, phH, hH, zW, phW, hW, P, psf, total;  // byte offsets
+};
+__host__ __device__ inline int round4(int n) { return (n + 3) & ~3; }
+__host__ __device__ inline PhiTileLds phi_tile_lds(int s, int Hs, int kh, int kw, int vc) {
+  PhiTileLds L;
+  int o = 0;
+  L.zH = o; o += Hs * 16;
+  L.phH = o; o += Hs * 16;
+  L.hH = o; o += (s > 1 ? Hs : 0) * 16;
+  L.zW = o; o += vc * s * 16;
+  L.phW = o; o += vc * s * 16;
+  L.hW = o; o += vc * s * 16;
+  L.P = o; o += vc * s * round4(kh) * 16;
+  L.psf = o; o += kh * round4(kw) * 4;
+  L.total = (o + 15) & ~15;
+  return L;
+}
+
+// c z + p
+__device__ __forceinline__ double2 cmadd(double2 c, double2 z, double2 p) {
+  return make_double2(fma(c.x, z.x, fma(-c.y, z.y, p.x)), fma(c.x, z.y, fma(c.y, z.x, p.y)));
+}
+
+// sum_{i<n4} P[i] z^i, n4 a multiple of 4: four independent Horner chains in z^4, then Horner in z
+__device__ __forceinline__ double2 horner4(const double2* P, int n4, double2 z) {
+  const double2 z2 = dcmul(z, z), z4 = dcmul(z2, z2);
+  double2 c0 = P[n4 - 4], c1 = P[n4 - 3], c2 = P[n4 - 2], c3 = P[n4 - 1];
+  for (int i = n4 - 8; i >= 0; i -= 4) {
+    c0 = cmadd(c0, z4, P[i]);
+    c1 = cmadd(c1, z4, P[i + 1]);
+    c2 = cmadd(c2, z4, P[i + 2]);
+    c3 = cmadd(c3, z4, P[i + 3]);
+  }
+  return cmadd(cmadd(cmadd(c3, z, c2), z, c1), z, c0);
+}
+
+template <int S>
+__global__ void __launch_bounds__(256) k_phi_tile(PhiArgs a, int op, int vc, int nchunk) {
+  extern __shared__ __align__(16) unsigned char phl[];
+  const int tid = threadIdx.x, nth = blockDim.x;
+  const int64_t cp = blockIdx.x / nchunk;
+  const int chunk = (int)(blockIdx.x - cp * nchunk);
+  const int vbeg = chunk * vc;
+  const int nv = min(vc, a.nv0 - vbeg);
+  const int c = (int)(cp % a.C);
+  const int Hs = a.Hs, Ws = a.Ws, h = a.h, kh = a.kh, kw = a.kw;
+  const int kh4 = round4(kh), kw4 = round4(kw);
+  const PhiTileLds L = phi_tile_lds(S, Hs, kh, kw, vc);
+  double2* zH = (double2*)(phl + L.zH);
+  double2* phH = (double2*)(phl + L.phH);
+  double2* hH = (double2*)(phl + L.hH);
+  double2* zW = (double2*)(phl + L.zW);
+  double2* phW = (double2*)(phl + L.phW);
+  double2* hW = (double2*)(phl + L.hW);
+  double2* P = (double2*)(phl + L.P);
+  float* ps = (float*)(phl + L.psf);
+
+  const float* psf = a.psf + cp * kh * kw;
+  for (int e = tid; e < kh * kw4; e += nth) {
+    const int i = e / kw4, j = e - i * kw4;
+    ps[e] = j < kw ? psf[i * kw + j] : 0.f;
+  }
+  for (int u = tid; u < Hs; u += nth) {
+    zH[u] = dexpi((double)u, (double)Hs);
+    phH[u] = dexpi(-(double)(((int64_t)u * (kh / 2)) % Hs), (double)Hs);
+    if (S > 1) hH[u] = hold(S, u, Hs);
+  }
+  for (int e = tid; e < nv * S; e += nth) {
+    const int v = e / S, b = e - v * S;
+    const int64_t vb = vbeg + v + (int64_t)b * a.w;
+    zW[e] = dexpi((double)vb, (double)Ws);
+    phW[e] = dexpi(-(double)((vb * (kw / 2)) % Ws), (double)Ws);
+    hW[e] = hold(S, vb, Ws);
+  }
+  __syncthreads();
+  // row sums (real coefficients, same four-chain Horner); rows zero-padded to kh4
+  for (int e = tid; e < nv * S * kh4; e += nth) {
+    const int vbq = e / kh4, i = e - vbq * kh4;
+    double2 acc = make_double2(0.0, 0.0);
+    if (i < kh) {
+      const double2 z = zW[vbq], z2 = dcmul(z, z), z4 = dcmul(z2, z2);
+      const float* row = ps + i * kw4;
+      double2 q[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) q[r] = make_double2((double)row[kw4 - 4 + r], 0.0);
+      for (int j = kw4 - 8; j >= 0; j -= 4)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) q[r] = cmadd(q[r], z4, make_double2((double)row[j + r], 0.0));
+      acc = dcmul(cmadd(cmadd(cmadd(q[3], z, q[2]), z, q[1]), z, q[0]), phW[vbq]);
+    }
+    P[e] = acc;
+  }
+  __syncthreads();
+
+  const double lmb = lambda_of(a, c);
+  const double norm = 1.0 / ((double)Hs * (double)Ws);
+  const double inv_s2 = 1.0 / (double)(S * S);
+  const int items = nv * h;
+  for (int it = tid; it < items; it += nth) {
+    const int v = it / h, u0 = it - v * h;
+    double2 K[S][S];  // [b][a]: member (u0 + a h, vbeg + v + b w)
+    double2 mkh = make_double2(0.0, 0.0);
+    double mk2 = 0.0;
+#pragma unroll
+    for (int b = 0; b < S; ++b) {
+      const double2* Pvb = P + (v * S + b) * kh4;
+      const double2 hv = hW[v * S + b];
+#pragma unroll
+      for (int aa = 0; aa < S; ++aa) {
+        const int u = u0 + aa * h;
+        K[b][aa] = dcmul(horner4(Pvb, kh4, zH[u]), phH[u]);
+        mk2 += K[b][aa].x * K[b][aa].x + K[b][aa].y * K[b][aa].y;
+        if (!op) {
+          const double2 khn = S > 1 ? dcmul(K[b][aa], dcmul(hH[u], hv)) : K[b][aa];
+          mkh.x += khn.x;
+          mkh.y += khn.y;
+        }
+      }
+    }
+    const double rD = 1.0 / (mk2 * inv_s2 + lmb);
+    const double2 g = make_double2((1.0 - mkh.x * inv_s2) * rD, -mkh.y * inv_s2 * rD);  // module
+    const double gop = rD * norm;                                                       // op
+#pragma unroll
+    for (int b = 0; b < S; ++b) {
+      const int64_t vb = vbeg + v + (int64_t)b * a.w;
+      if (!op && vb > Ws / 2) continue;
+      const double2 hv = hW[v * S + b];
+#pragma unroll
+      for (int aa = 0; aa < S; ++aa) {
+        const int u = u0 + aa * h;
+        const double2 k = K[b][aa];
+        if (op) {
+          const int64_t o = (cp * Ws + vb) * Hs + u;
+          a.kf[o] = make_float2((float)k.x, (float)k.y);
+          a.phi[o] = make_float2((float)(k.x * gop), (float)(-k.y * gop));
+        } else {
+          const double2 hn = S > 1 ? dcmul(hH[u], hv) : make_double2(1.0, 0.0);
+          const double2 t = dcmul(make_double2(k.x, -k.y), g);
+          a.phi[(cp * a.NCs + vb) * Hs + u] =
+              make_float2((float)((hn.x + t.x) * norm), (float)((hn.y + t.y) * norm));
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
 // Forward row pass: real rows of a (possibly padded) plane -> half spectrum S[plane][c][r]
 // ------------------------------------------------------------------------------------------------
 struct RowFwdArgs {
@@ -639,6 +797,26 @@ int launch_phi(const float* psf, const float* bias, float eps, const Geo& g, boo
   a.h = g.h; a.w = g.w; a.Hs = g.Hs; a.Ws = g.Ws; a.NCs = g.NCs; a.eps = (double)eps;
   a.phi = phi; a.kf = kf;
   a.nv0 = (!op && g.s == 1) ? g.NC : g.w;
+  // tiled kernel (scales 1..4): about 2048 blocks, chunk size bounded by an LDS budget of 64 KiB
+  if (g.s <= 4) {
+    constexpr int kTileLds = 64 * 1024;
+    int nchunk = (int)std::min<int64_t>(a.nv0, std::max<int64_t>(1, (2048 + g.Cp - 1) / g.Cp));
+    int vc = (a.nv0 + nchunk - 1) / nchunk;
+    while (vc > 1 && phi_tile_lds(g.s, g.Hs, g.kh, g.kw, vc).total > kTileLds) --vc;
+    const int lds = phi_tile_lds(g.s, g.Hs, g.kh, g.kw, vc).total;
+    nchunk = (a.nv0 + vc - 1) / vc;
+    if (lds <= kTileLds && g.Cp * nchunk <= 0x7fffffff) {
+      const dim3 grid((unsigned)(g.Cp * nchunk));
+      const int o = op ? 1 : 0;
+      switch (g.s) {
+        case 1: hipLaunchKernelGGL(k_phi_tile<1>, grid, dim3(kThreads), (size_t)lds, st, a, o, vc, nchunk); break;
+        case 2: hipLaunchKernelGGL(k_phi_tile<2>, grid, dim3(kThreads), (size_t)lds, st, a, o, vc, nchunk); break;
+        case 3: hipLaunchKernelGGL(k_phi_tile<3>, grid, dim3(kThreads), (size_t)lds, st, a, o, vc, nchunk); break;
+        default: hipLaunchKernelGGL(k_phi_tile<4>, grid, dim3(kThreads), (size_t)lds, st, a, o, vc, nchunk); break;
+      }
+      return check_launch("transfer table");
+    }
+  }
   const size_t lds = (size_t)g.s * g.kh * sizeof(double2);
   const int64_t blocks = g.Cp * a.nv0;
   if (blocks > 0x7fffffff) return fail(CVN_ERR_UNSUPPORTED, "too many transfer blocks");

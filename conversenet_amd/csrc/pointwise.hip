@@ -14,6 +14,8 @@
 // is the B operand of a k-step whose channel for lane group g is 16 rb + 4 g + r.
 #include <math.h>
 
+#include <algorithm>
+
 #include "cvn_common.h"
 
 namespace cvn {
@@ -74,203 +76,309 @@ __global__ void __launch_bounds__(256) k_ln_cf_any(const float* __restrict__ x, 
 }
 
 // ------------------------------------------------------------------------------------------------
-// shared pieces of the MFMA kernels
+// shared pieces of the MFMA kernels.  A wave owns 16 Q pixels: lane l = 16 g + j holds pixels
+// p0 + Q j .. p0 + Q j + Q - 1 (Q = 2: one float2 per channel), so per k-step the Q register
+// components are the B operands of Q independent 16-pixel blocks.
 // ------------------------------------------------------------------------------------------------
 // Stage W (ROWS x COLS, row-major in global) transposed into LDS: Wt[k * LD + i] = W[i][k].
+// Consecutive threads take consecutive rows i of one column k, so the LDS writes are contiguous.
 template <int ROWS, int COLS, int LD>
 __device__ __forceinline__ void stage_wt(const float* __restrict__ W, float* Wt) {
   for (int e = threadIdx.x; e < ROWS * COLS; e += blockDim.x) {
-    const int i = e / COLS, k = e - i * COLS;
-    Wt[k * LD + i] = W[e];
+    const int k = e / ROWS, i = e - k * ROWS;
+    Wt[k * LD + i] = W[i * COLS + k];
   }
 }
 
-// Load the wave's CIN x 64-pixel tile (float4 per k-step), zero beyond HW.
-template <int CIN>
-__device__ __forceinline__ void load_tile(const float* __restrict__ xb, int64_t HW, int64_t px, int g,
-                                          float4 (&xv)[CIN / 4]) {
+// Stage a per-channel parameter vector into LDS (def where the pointer is null).  Read from LDS
+// inside the tile loop, these stay out of the vector registers; read from global memory, the
+// compiler keeps every lane's copy live across the loop.
+template <int N>
+__device__ __forceinline__ void stage_vec(const float* src, float def, float* dst) {
+  for (int e = threadIdx.x; e < N; e += blockDim.x) dst[e] = src ? src[e] : def;
+}
+
+template <int Q>
+__device__ __forceinline__ void ldq(const float* p, float (&v)[Q]) {
+  if constexpr (Q == 4) {
+    const float4 t = *(const float4*)p;
+    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+  } else if constexpr (Q == 2) {
+    const float2 t = *(const float2*)p;
+    v[0] = t.x; v[1] = t.y;
+  } else {
+    v[0] = *p;
+  }
+}
+template <int Q>
+__device__ __forceinline__ void stq(float* p, const float (&v)[Q]) {
+  if constexpr (Q == 4) *(float4*)p = make_float4(v[0], v[1], v[2], v[3]);
+  else if constexpr (Q == 2) *(float2*)p = make_float2(v[0], v[1]);
+  else *p = v[0];
+}
+
+// Addressing: every access is a wave-uniform pointer (image, channel row, wave's first pixel) plus
+// a 32-bit per-lane byte offset, so the compiler can use the scalar-base form of the global memory
+// instructions instead of keeping a 64-bit address per access in vector registers.
+__device__ __forceinline__ const float* at_off(const float* p, uint32_t off) {
+  return (const float*)((const char*)p + off);
+}
+__device__ __forceinline__ float* at_off(float* p, uint32_t off) { return (float*)((char*)p + off); }
+
+// Load the wave's CIN x 16Q-pixel tile (xw: channel 0 at the wave's first pixel; xoff: lane
+// offset of channel g, pixel Q j), zero beyond HW.
+template <int CIN, int Q>
+__device__ __forceinline__ void load_tile(const float* xw, int64_t HW, bool inb, uint32_t xoff,
+                                          float (&xv)[CIN / 4][Q]) {
 #pragma unroll
   for (int ks = 0; ks < CIN / 4; ++ks) {
-    const int k = 4 * ks + g;
-    xv[ks] = (px < HW) ? *(const float4*)(xb + (int64_t)k * HW + px) : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (inb) {
+      ldq<Q>(at_off(xw + 4 * ks * HW, xoff), xv[ks]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < Q; ++q) xv[ks][q] = 0.f;
+    }
   }
 }
 
 // Channels-first LayerNorm of the register tile (statistics over all CIN channels of each pixel;
 // the four lane groups g hold disjoint channel subsets).
-template <int CIN>
-__device__ __forceinline__ void ln_tile(float4 (&xv)[CIN / 4], int g, const float* __restrict__ lw,
-                                        const float* __restrict__ lb, float eps) {
-  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-  for (int ks = 0; ks < CIN / 4; ++ks) {
-    s.x += xv[ks].x; s.y += xv[ks].y; s.z += xv[ks].z; s.w += xv[ks].w;
-  }
-#pragma unroll
-  for (int m = 16; m <= 32; m <<= 1) {
-    s.x += __shfl_xor(s.x, m); s.y += __shfl_xor(s.y, m);
-    s.z += __shfl_xor(s.z, m); s.w += __shfl_xor(s.w, m);
-  }
+template <int CIN, int Q>
+__device__ __forceinline__ void ln_tile(float (&xv)[CIN / 4][Q], int g, const float* lw, const float* lb,
+                                        float eps) {
   const float inv = 1.0f / (float)CIN;
-  const float4 u = make_float4(s.x * inv, s.y * inv, s.z * inv, s.w * inv);
-  float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+  float u[Q], rs[Q];
 #pragma unroll
-  for (int ks = 0; ks < CIN / 4; ++ks) {
-    float d;
-    d = xv[ks].x - u.x; q.x = fmaf(d, d, q.x);
-    d = xv[ks].y - u.y; q.y = fmaf(d, d, q.y);
-    d = xv[ks].z - u.z; q.z = fmaf(d, d, q.z);
-    d = xv[ks].w - u.w; q.w = fmaf(d, d, q.w);
+  for (int q = 0; q < Q; ++q) {
+    float s = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < CIN / 4; ++ks) s += xv[ks][q];
+    s += __shfl_xor(s, 16);
+    s += __shfl_xor(s, 32);
+    u[q] = s * inv;
   }
 #pragma unroll
-  for (int m = 16; m <= 32; m <<= 1) {
-    q.x += __shfl_xor(q.x, m); q.y += __shfl_xor(q.y, m);
-    q.z += __shfl_xor(q.z, m); q.w += __shfl_xor(q.w, m);
+  for (int q = 0; q < Q; ++q) {
+    float v = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < CIN / 4; ++ks) {
+      const float d = xv[ks][q] - u[q];
+      v = fmaf(d, d, v);
+    }
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    rs[q] = 1.0f / sqrtf(v * inv + eps);
   }
-  const float4 rs = make_float4(1.0f / sqrtf(q.x * inv + eps), 1.0f / sqrtf(q.y * inv + eps),
-                                1.0f / sqrtf(q.z * inv + eps), 1.0f / sqrtf(q.w * inv + eps));
 #pragma unroll
   for (int ks = 0; ks < CIN / 4; ++ks) {
     const int k = 4 * ks + g;
     const float ww = lw[k], bb = lb[k];
-    xv[ks].x = fmaf(ww * rs.x, xv[ks].x - u.x, bb);
-    xv[ks].y = fmaf(ww * rs.y, xv[ks].y - u.y, bb);
-    xv[ks].z = fmaf(ww * rs.z, xv[ks].z - u.z, bb);
-    xv[ks].w = fmaf(ww * rs.w, xv[ks].w - u.w, bb);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) xv[ks][q] = fmaf(ww * rs[q], xv[ks][q] - u[q], bb);
   }
 }
 
-// acc[rb][q] += W[16 rb + row][k] * x[k][block q]  over all k-steps of the register tile
-template <int CIN, int COUT>
-__device__ __forceinline__ void gemm_tile(const float4 (&xv)[CIN / 4], const float* Wt, int ld, int g, int j,
-                                          v4f (&acc)[COUT / 16][4]) {
+// Keeps the compiler from moving memory operations across this point.  The GEMM loops place it
+// once per k-step so that only the next step's weights are loaded ahead: without it the scheduler
+// front-loads every LDS weight read of the unrolled loop, and the registers that costs halve the
+// occupancy.
+__device__ __forceinline__ void mem_fence_sched() { asm volatile("" ::: "memory"); }
+
+// A copy of the (wave-uniform) plane stride that the compiler cannot see through.  Row offsets
+// computed from it inside the tile loop stay per-iteration scalar arithmetic; computed from the
+// kernel argument they are hoisted out of the loop as 64-bit values, which spill into vector
+// registers.
+__device__ __forceinline__ int64_t opaque_stride(int64_t v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+
+// acc[rb][q] += W[16 rb + row][k] * x[k][block q]  over all k-steps of the register tile; the
+// weights of step ks + 1 are read while step ks runs.
+template <int CIN, int COUT, int Q>
+__device__ __forceinline__ void gemm_tile(const float (&xv)[CIN / 4][Q], const float* Wt, int ld, int g, int j,
+                                          v4f (&acc)[COUT / 16][Q]) {
+  float a[2][COUT / 16];
+#pragma unroll
+  for (int rb = 0; rb < COUT / 16; ++rb) a[0][rb] = Wt[g * ld + j + 16 * rb];
 #pragma unroll
   for (int ks = 0; ks < CIN / 4; ++ks) {
-    const float* wk = Wt + (4 * ks + g) * ld + j;
+    if (ks + 1 < CIN / 4) {
+      const float* wk = Wt + (4 * (ks + 1) + g) * ld + j;
 #pragma unroll
-    for (int rb = 0; rb < COUT / 16; ++rb) {
-      const float a = wk[16 * rb];
-      acc[rb][0] = mfma4(a, xv[ks].x, acc[rb][0]);
-      acc[rb][1] = mfma4(a, xv[ks].y, acc[rb][1]);
-      acc[rb][2] = mfma4(a, xv[ks].z, acc[rb][2]);
-      acc[rb][3] = mfma4(a, xv[ks].w, acc[rb][3]);
+      for (int rb = 0; rb < COUT / 16; ++rb) a[(ks + 1) & 1][rb] = wk[16 * rb];
     }
+#pragma unroll
+    for (int rb = 0; rb < COUT / 16; ++rb)
+#pragma unroll
+      for (int q = 0; q < Q; ++q) acc[rb][q] = mfma4(a[ks & 1][rb], xv[ks][q], acc[rb][q]);
+    mem_fence_sched();
   }
 }
 
-template <int COUT>
-__device__ __forceinline__ void zero_acc(v4f (&acc)[COUT / 16][4]) {
+template <int COUT, int Q>
+__device__ __forceinline__ void zero_acc(v4f (&acc)[COUT / 16][Q]) {
 #pragma unroll
   for (int rb = 0; rb < COUT / 16; ++rb)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) acc[rb][q] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < Q; ++q) acc[rb][q] = v4f{0.f, 0.f, 0.f, 0.f};
 }
 
-// Epilogue: bias, activation, optional alpha-scaled residual, float4 store.
-template <int COUT>
-__device__ __forceinline__ void store_tile(v4f (&acc)[COUT / 16][4], float* __restrict__ yb,
-                                           const float* __restrict__ rb_ptr, int64_t HW, int64_t px, int g,
-                                           const float* __restrict__ bias, int act,
-                                           const float* __restrict__ res_scale) {
-  if (px >= HW) return;
+// Epilogue: bias, activation, optional alpha-scaled residual, vector store.  yw / rw: output and
+// residual at channel 0 and the wave's first pixel; yoff: lane offset of channel 4 g, pixel Q j;
+// bias / res_scale: per-channel vectors staged in LDS.
+template <int COUT, int Q>
+__device__ __forceinline__ void store_tile(v4f (&acc)[COUT / 16][Q], float* yw, const float* rw, int64_t HW,
+                                           bool inb, uint32_t yoff, int g, const float* bias, int act,
+                                           const float* res_scale) {
+  if (!inb) return;
 #pragma unroll
   for (int rb = 0; rb < COUT / 16; ++rb) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int o = 16 * rb + 4 * g + r;
-      const float bo = bias ? bias[o] : 0.f;
-      float4 v = make_float4(acc[rb][0][r] + bo, acc[rb][1][r] + bo, acc[rb][2][r] + bo, acc[rb][3][r] + bo);
-      if (act == CVN_ACT_GELU) {
-        v.x = gelu_f(v.x); v.y = gelu_f(v.y); v.z = gelu_f(v.z); v.w = gelu_f(v.w);
+      const int64_t row = (int64_t)(16 * rb + r) * HW;
+      const float bo = bias[o];
+      float v[Q];
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        v[q] = acc[rb][q][r] + bo;
+        if (act == CVN_ACT_GELU) v[q] = gelu_f(v[q]);
       }
-      if (rb_ptr) {
-        const float sc = res_scale ? res_scale[o] : 1.f;
-        const float4 rr = *(const float4*)(rb_ptr + (int64_t)o * HW + px);
-        v.x = fmaf(sc, v.x, rr.x); v.y = fmaf(sc, v.y, rr.y);
-        v.z = fmaf(sc, v.z, rr.z); v.w = fmaf(sc, v.w, rr.w);
+      if (rw) {
+        const float sc = res_scale[o];
+        float rr[Q];
+        ldq<Q>(at_off(rw + row, yoff), rr);
+#pragma unroll
+        for (int q = 0; q < Q; ++q) v[q] = fmaf(sc, v[q], rr[q]);
       }
-      *(float4*)(yb + (int64_t)o * HW + px) = v;
+      stq<Q>(at_off(yw + row, yoff), v);
     }
   }
 }
 
+// Tiles: a block of 4 waves covers 64 Q consecutive pixels of one image; tile t is image
+// t / tpb, pixels (t % tpb) 64 Q ...  Blocks stage the weights once and then loop over tiles
+// t = blockIdx.x, blockIdx.x + gridDim.x, ...  The empty asm with a memory clobber at the top of
+// each iteration keeps the compiler from hoisting the (loop-invariant) LDS weight reads into
+// registers, which would cost occupancy.  Returns the wave's first pixel (wave-uniform).
+__device__ __forceinline__ int64_t tile_px(int64_t t, int64_t tpb, int Q, int wave, int64_t* b) {
+  *b = t / tpb;
+  return (t - *b * tpb) * (64 * Q) + wave * (16 * Q);
+}
+
 // ------------------------------------------------------------------------------------------------
-// 1x1 conv (+ LN prologue) on MFMA.  Block = 4 waves = 256 pixels; grid (ceil(HW/256), B).
+// 1x1 conv (+ LN prologue) on MFMA.  Block = 4 waves; persistent over pixel tiles.
 // ------------------------------------------------------------------------------------------------
-template <int CIN, int COUT, bool LN>
-__global__ void __launch_bounds__(256) k_conv1x1_mfma(const float* __restrict__ x, int64_t HW,
-                                                      const float* __restrict__ W, const float* __restrict__ bias,
-                                                      const float* __restrict__ lw, const float* __restrict__ lb,
-                                                      float eps, int act, const float* residual,
-                                                      const float* __restrict__ res_scale, float* y) {
-  constexpr int LD = COUT + 16;
+template <int CIN, int COUT, bool LN, int Q>
+__global__ void __launch_bounds__(256) k_conv1x1_mfma(const float* __restrict__ x, int64_t HW, int64_t tpb,
+                                                      int64_t ntiles, const float* __restrict__ W,
+                                                      const float* __restrict__ bias, const float* __restrict__ lw,
+                                                      const float* __restrict__ lb, float eps, int act,
+                                                      const float* residual, const float* __restrict__ res_scale,
+                                                      float* y) {
+  constexpr int LD = COUT + 16;  // (4 ks + g) LD + j + 16 rb: 16 g + j distinct banks
   __shared__ float Wt[CIN * LD];
+  __shared__ float prm[2 * COUT + 2 * CIN];  // bias, residual scale, LN weight, LN bias
   stage_wt<COUT, CIN, LD>(W, Wt);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = lane >> 4, j = lane & 15;
-  const int64_t b = blockIdx.y;
-  const int64_t px = (int64_t)blockIdx.x * 256 + wave * 64 + 4 * j;
-  const float* xb = x + b * CIN * HW;
-  float4 xv[CIN / 4];
-  load_tile<CIN>(xb, HW, px, g, xv);
-  if (LN) ln_tile<CIN>(xv, g, lw, lb, eps);
+  stage_vec<COUT>(bias, 0.f, prm);
+  stage_vec<COUT>(res_scale, 1.f, prm + COUT);
+  if (LN) {
+    stage_vec<CIN>(lw, 1.f, prm + 2 * COUT);
+    stage_vec<CIN>(lb, 0.f, prm + 2 * COUT + CIN);
+  }
   __syncthreads();
-  v4f acc[COUT / 16][4];
-  zero_acc<COUT>(acc);
-  gemm_tile<CIN, COUT>(xv, Wt, LD, g, j, acc);
-  store_tile<COUT>(acc, y + b * COUT * HW, residual ? residual + b * COUT * HW : nullptr, HW, px, g, bias, act,
-                   res_scale);
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, j = lane & 15;
+  const uint32_t xoff = (uint32_t)(((int64_t)g * HW + Q * j) * 4);
+  const uint32_t yoff = (uint32_t)(((int64_t)4 * g * HW + Q * j) * 4);
+  for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+    mem_fence_sched();
+    const int64_t hw = opaque_stride(HW);
+    int64_t b;
+    const int64_t pw = tile_px(t, tpb, Q, wave, &b);
+    const bool inb = pw + Q * j < hw;
+    float xv[CIN / 4][Q];
+    load_tile<CIN, Q>(x + b * CIN * hw + pw, hw, inb, xoff, xv);
+    if (LN) ln_tile<CIN, Q>(xv, g, prm + 2 * COUT, prm + 2 * COUT + CIN, eps);
+    v4f acc[COUT / 16][Q];
+    zero_acc<COUT, Q>(acc);
+    gemm_tile<CIN, COUT, Q>(xv, Wt, LD, g, j, acc);
+    store_tile<COUT, Q>(acc, y + b * COUT * hw + pw, residual ? residual + b * COUT * hw + pw : nullptr, hw, inb,
+                        yoff, g, prm, act, prm + COUT);
+  }
 }
 
 // ConverseBlock conv2 branch: y = x + res_scale * (W2 GELU(W1 LN(x) + b1) + b2)
-template <int C, int CM>
-__global__ void __launch_bounds__(256) k_ln_mlp_mfma(const float* x, int64_t HW, const float* __restrict__ lw,
-                                                     const float* __restrict__ lb, float eps,
-                                                     const float* __restrict__ W1, const float* __restrict__ b1,
-                                                     const float* __restrict__ W2, const float* __restrict__ b2,
+template <int C, int CM, int Q>
+__global__ void __launch_bounds__(256) k_ln_mlp_mfma(const float* x, int64_t HW, int64_t tpb, int64_t ntiles,
+                                                     const float* __restrict__ lw, const float* __restrict__ lb,
+                                                     float eps, const float* __restrict__ W1,
+                                                     const float* __restrict__ b1, const float* __restrict__ W2,
+                                                     const float* __restrict__ b2,
                                                      const float* __restrict__ res_scale, float* y) {
-  constexpr int LD1 = CM + 16;  // W1t[k][i], k < C, i < CM
-  constexpr int LD2 = C + 16;   // W2t[k][i], k < CM, i < C
+  constexpr int LD1 = CM + 16;  // W1t[k][i], k < C, i < CM; read at (4 ks + g) LD1 + 16 rb + j
+  constexpr int LD2 = C + 4;    // W2t[k][i], k < CM, i < C; read at (16 rb + 4 g + r) LD2 + 16 ob + j
   __shared__ float W1t[C * LD1];
   __shared__ float W2t[CM * LD2];
+  __shared__ float prm[CM + 4 * C];  // b1, b2, residual scale, LN weight, LN bias
   stage_wt<CM, C, LD1>(W1, W1t);
   stage_wt<C, CM, LD2>(W2, W2t);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = lane >> 4, j = lane & 15;
-  const int64_t b = blockIdx.y;
-  const int64_t px = (int64_t)blockIdx.x * 256 + wave * 64 + 4 * j;
-  const float* xb = x + b * C * HW;
-  float4 xv[C / 4];
-  load_tile<C>(xb, HW, px, g, xv);
-  ln_tile<C>(xv, g, lw, lb, eps);
+  stage_vec<CM>(b1, 0.f, prm);
+  stage_vec<C>(b2, 0.f, prm + CM);
+  stage_vec<C>(res_scale, 1.f, prm + CM + C);
+  stage_vec<C>(lw, 1.f, prm + CM + 2 * C);
+  stage_vec<C>(lb, 0.f, prm + CM + 3 * C);
   __syncthreads();
-  v4f h[CM / 16][4];
-  zero_acc<CM>(h);
-  gemm_tile<C, CM>(xv, W1t, LD1, g, j, h);
-  // bias + GELU on the hidden activations (channel 16 rb + 4 g + r)
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, j = lane & 15;
+  const uint32_t xoff = (uint32_t)(((int64_t)g * HW + Q * j) * 4);
+  const uint32_t yoff = (uint32_t)(((int64_t)4 * g * HW + Q * j) * 4);
+  for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+    mem_fence_sched();
+    const int64_t hw = opaque_stride(HW);
+    int64_t b;
+    const int64_t pw = tile_px(t, tpb, Q, wave, &b);
+    const bool inb = pw + Q * j < hw;
+    const float* xw = x + b * C * hw + pw;
+    float xv[C / 4][Q];
+    load_tile<C, Q>(xw, hw, inb, xoff, xv);
+    ln_tile<C, Q>(xv, g, prm + CM + 2 * C, prm + CM + 3 * C, eps);
+    v4f h[CM / 16][Q];
+    zero_acc<CM, Q>(h);
+    gemm_tile<C, CM, Q>(xv, W1t, LD1, g, j, h);
+    // bias + GELU on the hidden activations (channel 16 rb + 4 g + r)
 #pragma unroll
-  for (int rb = 0; rb < CM / 16; ++rb)
+    for (int rb = 0; rb < CM / 16; ++rb)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float bo = b1[16 * rb + 4 * g + r];
+      for (int r = 0; r < 4; ++r) {
+        const float bo = prm[16 * rb + 4 * g + r];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) h[rb][q][r] = gelu_f(h[rb][q][r] + bo);
-    }
-  v4f acc[C / 16][4];
-  zero_acc<C>(acc);
-#pragma unroll
-  for (int rb = 0; rb < CM / 16; ++rb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float* wk = W2t + (16 * rb + 4 * g + r) * LD2 + j;
-#pragma unroll
-      for (int ob = 0; ob < C / 16; ++ob) {
-        const float a = wk[16 * ob];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc[ob][q] = mfma4(a, h[rb][q][r], acc[ob][q]);
+        for (int q = 0; q < Q; ++q) h[rb][q][r] = gelu_f(h[rb][q][r] + bo);
       }
+    v4f acc[C / 16][Q];
+    zero_acc<C, Q>(acc);
+    // k-step kk = 4 rb + r: lane group g supplies hidden channel 16 rb + 4 g + r
+    float a[2][C / 16];
+#pragma unroll
+    for (int ob = 0; ob < C / 16; ++ob) a[0][ob] = W2t[(4 * g) * LD2 + j + 16 * ob];
+#pragma unroll
+    for (int kk = 0; kk < CM / 4; ++kk) {
+      const int rb = kk >> 2, r = kk & 3;
+      if (kk + 1 < CM / 4) {
+        const int rn = (kk + 1) >> 2, sn = (kk + 1) & 3;
+        const float* wk = W2t + (16 * rn + 4 * g + sn) * LD2 + j;
+#pragma unroll
+        for (int ob = 0; ob < C / 16; ++ob) a[(kk + 1) & 1][ob] = wk[16 * ob];
+      }
+#pragma unroll
+      for (int ob = 0; ob < C / 16; ++ob)
+#pragma unroll
+        for (int q = 0; q < Q; ++q) acc[ob][q] = mfma4(a[kk & 1][ob], h[rb][q][r], acc[ob][q]);
+      mem_fence_sched();
     }
-  store_tile<C>(acc, y + b * C * HW, xb, HW, px, g, b2, CVN_ACT_NONE, res_scale);
+    store_tile<C, Q>(acc, y + b * C * hw + pw, xw, hw, inb, yoff, g, prm + CM, CVN_ACT_NONE, prm + CM + C);
+  }
 }
 
 // Plain VALU 1x1 conv for channel counts / sizes the MFMA tiles do not cover (e.g. 1 or 3 channels).
@@ -300,13 +408,32 @@ namespace {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+constexpr int kQ = 2;  // 16-pixel blocks per wave
+
+// Persistent grid: as many blocks as fit on the device at once (occupancy query, cached per kernel),
+// at most one per tile.
+template <typename K>
+unsigned persistent_grid(K kernel, int64_t ntiles) {
+  static int resident = 0;
+  if (resident == 0) {
+    int dev = 0, cus = 0, per_cu = 0;
+    hipGetDevice(&dev);
+    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kernel, 256, 0);
+    hipGetLastError();
+    resident = std::max(1, cus) * std::max(1, per_cu);
+  }
+  return (unsigned)std::min<int64_t>(ntiles, resident);
+}
+
 template <int CIN, int COUT, bool LN>
 int launch_mfma(const float* x, int64_t B, int64_t HW, const float* W, const float* bias, const float* lw,
                 const float* lb, float eps, int act, const float* residual, const float* res_scale, float* y,
                 hipStream_t st) {
-  dim3 grid((unsigned)((HW + 255) / 256), (unsigned)B);
-  hipLaunchKernelGGL((k_conv1x1_mfma<CIN, COUT, LN>), grid, dim3(256), 0, st, x, HW, W, bias, lw, lb, eps, act,
-                     residual, res_scale, y);
+  const int64_t tpb = (HW + 64 * kQ - 1) / (64 * kQ), ntiles = B * tpb;
+  auto kern = k_conv1x1_mfma<CIN, COUT, LN, kQ>;
+  hipLaunchKernelGGL(kern, dim3(persistent_grid(kern, ntiles)), dim3(256), 0, st, x, HW, tpb, ntiles, W, bias,
+                     lw, lb, eps, act, residual, res_scale, y);
   return check_launch("1x1 conv");
 }
 
@@ -403,13 +530,15 @@ extern "C" int cvn_ln_mlp_residual_f32(const float* x, int64_t B, int64_t C, int
   if (HW % 4 != 0 || !aligned16(x) || !aligned16(y))
     return fail(CVN_ERR_UNSUPPORTED, "fused branch needs HW %% 4 == 0 and 16-byte aligned buffers");
   hipStream_t st = (hipStream_t)stream;
-  dim3 grid((unsigned)((HW + 255) / 256), (unsigned)B);
+  const int64_t tpb = (HW + 64 * kQ - 1) / (64 * kQ), ntiles = B * tpb;
   if (C == 64 && Cmid == 128) {
-    hipLaunchKernelGGL((k_ln_mlp_mfma<64, 128>), grid, dim3(256), 0, st, x, HW, ln_w, ln_b, ln_eps, w1, b1, w2, b2,
-                       res_scale, y);
+    auto kern = k_ln_mlp_mfma<64, 128, kQ>;
+    hipLaunchKernelGGL(kern, dim3(persistent_grid(kern, ntiles)), dim3(256), 0, st, x, HW, tpb, ntiles, ln_w, ln_b,
+                       ln_eps, w1, b1, w2, b2, res_scale, y);
   } else if (C == 32 && Cmid == 64) {
-    hipLaunchKernelGGL((k_ln_mlp_mfma<32, 64>), grid, dim3(256), 0, st, x, HW, ln_w, ln_b, ln_eps, w1, b1, w2, b2,
-                       res_scale, y);
+    auto kern = k_ln_mlp_mfma<32, 64, kQ>;
+    hipLaunchKernelGGL(kern, dim3(persistent_grid(kern, ntiles)), dim3(256), 0, st, x, HW, tpb, ntiles, ln_w, ln_b,
+                       ln_eps, w1, b1, w2, b2, res_scale, y);
   } else {
     return fail(CVN_ERR_UNSUPPORTED, "fused branch supports (C, Cmid) in {(64,128), (32,64)}");
   }

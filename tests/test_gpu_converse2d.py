@@ -251,3 +251,52 @@ def test_pfa268_per_sample_psf_gelu_and_generic_agreement(monkeypatch):
     monkeypatch.setenv("CVN_DISABLE_FUSED", "1")
     generic = Fh.converse2d_fused(*args, act="gelu", cache=False).cpu().numpy()
     assert np.abs(got - generic).max() <= TOL
+
+
+# ---------------------------------------------------------------------------------------------
+# ConvReverseDataNet step (converse_usrnet.py:41-68): per-sample 25x25 psf of KernelNet scale (not
+# normalised), eps 1e-3, padding 0; plane sides chosen so the transfer-table kernel runs partial
+# column chunks, several rows per thread (Hs > 256) and every scale of the data steps.
+# ---------------------------------------------------------------------------------------------
+DATA_STEP_CASES = [
+    # (B, C, h, w, s)
+    (2, 5, 64, 64, 1),
+    (2, 3, 300, 40, 1),
+    (2, 4, 16, 16, 4),
+    (1, 3, 64, 64, 4),
+    (2, 3, 30, 26, 2),
+    (1, 2, 100, 34, 3),
+]
+
+
+@pytest.mark.parametrize("B,C,h,w,s", DATA_STEP_CASES)
+def test_data_step_per_sample_psf(B, C, h, w, s):
+    from conversenet_amd import functional as Fh
+    rng = np.random.default_rng(1000 + 7 * s + h)
+    x = rng.random((B, C, h, w)).astype(np.float32)
+    k = (0.05 * rng.standard_normal((B, C, 25, 25))).astype(np.float32)
+    alpha = (0.1 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    ref = O.conv_reverse_datanet(x, k, s, alpha, 1e-3)
+    dev = torch.device("cuda")
+    got = Fh.converse2d_fused(torch.from_numpy(x).to(dev), torch.from_numpy(k).to(dev),
+                              torch.from_numpy(alpha).to(dev).reshape(-1), s, 0, "circular", 1e-3,
+                              cache=False).cpu().numpy()
+    err = np.abs(got - ref).max()
+    scale = max(1.0, float(np.abs(ref).max()))
+    print(f"data step B{B} C{C} {h}x{w} s{s}: max-abs {err:.3e} (|ref| max {scale:.2f})")
+    assert err <= TOL * scale
+
+
+@pytest.mark.parametrize("s", [1, 4])
+def test_op_level_large_psf(s):
+    from conversenet_amd import functional as Fh
+    rng = np.random.default_rng(77 + s)
+    B, C, h, w, k = 2, 3, 30, 26, 25
+    x = rng.standard_normal((B, C, h, w)).astype(np.float32)
+    x0 = rng.standard_normal((B, C, h * s, w * s)).astype(np.float32)
+    wt = softmax_psf(rng, C, k)
+    b = (0.3 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    ref = O.converse2d_op(x, x0, wt, b, s, 1e-5)
+    dev = torch.device("cuda")
+    got = Fh.converse2d_op(*(torch.from_numpy(a).to(dev) for a in (x, x0, wt, b)), s, 1e-5).cpu().numpy()
+    assert np.abs(got - ref).max() <= TOL
