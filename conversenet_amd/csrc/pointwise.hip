@@ -257,21 +257,21 @@ __device__ __forceinline__ void store_tile(v4f (&acc)[COUT / 16][Q], float* yw, 
   }
 }
 
-// Tiles: a block of 4 waves covers 64 Q consecutive pixels of one image; tile t is image
-// t / tpb, pixels (t % tpb) 64 Q ...  Blocks stage the weights once and then loop over tiles
+// Tiles: a block of NW waves covers 16 NW Q consecutive pixels of one image; tile t is image
+// t / tpb, pixels (t % tpb) 16 NW Q ...  Blocks stage the weights once and then loop over tiles
 // t = blockIdx.x, blockIdx.x + gridDim.x, ...  The empty asm with a memory clobber at the top of
 // each iteration keeps the compiler from hoisting the (loop-invariant) LDS weight reads into
 // registers, which would cost occupancy.  Returns the wave's first pixel (wave-uniform).
-__device__ __forceinline__ int64_t tile_px(int64_t t, int64_t tpb, int Q, int wave, int64_t* b) {
+__device__ __forceinline__ int64_t tile_px(int64_t t, int64_t tpb, int Q, int NW, int wave, int64_t* b) {
   *b = t / tpb;
-  return (t - *b * tpb) * (64 * Q) + wave * (16 * Q);
+  return (t - *b * tpb) * (16 * NW * Q) + wave * (16 * Q);
 }
 
 // ------------------------------------------------------------------------------------------------
-// 1x1 conv (+ LN prologue) on MFMA.  Block = 4 waves; persistent over pixel tiles.
+// 1x1 conv (+ LN prologue) on MFMA.  Block = NW waves; persistent over pixel tiles.
 // ------------------------------------------------------------------------------------------------
-template <int CIN, int COUT, bool LN, int Q>
-__global__ void __launch_bounds__(256) k_conv1x1_mfma(const float* __restrict__ x, int64_t HW, int64_t tpb,
+template <int CIN, int COUT, bool LN, int Q, int NW>
+__global__ void __launch_bounds__(64 * NW) k_conv1x1_mfma(const float* __restrict__ x, int64_t HW, int64_t tpb,
                                                       int64_t ntiles, const float* __restrict__ W,
                                                       const float* __restrict__ bias, const float* __restrict__ lw,
                                                       const float* __restrict__ lb, float eps, int act,
@@ -296,7 +296,7 @@ __global__ void __launch_bounds__(256) k_conv1x1_mfma(const float* __restrict__ 
     mem_fence_sched();
     const int64_t hw = opaque_stride(HW);
     int64_t b;
-    const int64_t pw = tile_px(t, tpb, Q, wave, &b);
+    const int64_t pw = tile_px(t, tpb, Q, NW, wave, &b);
     const bool inb = pw + Q * j < hw;
     float xv[CIN / 4][Q];
     load_tile<CIN, Q>(x + b * CIN * hw + pw, hw, inb, xoff, xv);
@@ -310,8 +310,8 @@ __global__ void __launch_bounds__(256) k_conv1x1_mfma(const float* __restrict__ 
 }
 
 // ConverseBlock conv2 branch: y = x + res_scale * (W2 GELU(W1 LN(x) + b1) + b2)
-template <int C, int CM, int Q>
-__global__ void __launch_bounds__(256) k_ln_mlp_mfma(const float* x, int64_t HW, int64_t tpb, int64_t ntiles,
+template <int C, int CM, int Q, int NW>
+__global__ void __launch_bounds__(64 * NW) k_ln_mlp_mfma(const float* x, int64_t HW, int64_t tpb, int64_t ntiles,
                                                      const float* __restrict__ lw, const float* __restrict__ lb,
                                                      float eps, const float* __restrict__ W1,
                                                      const float* __restrict__ b1, const float* __restrict__ W2,
@@ -338,7 +338,7 @@ __global__ void __launch_bounds__(256) k_ln_mlp_mfma(const float* x, int64_t HW,
     mem_fence_sched();
     const int64_t hw = opaque_stride(HW);
     int64_t b;
-    const int64_t pw = tile_px(t, tpb, Q, wave, &b);
+    const int64_t pw = tile_px(t, tpb, Q, NW, wave, &b);
     const bool inb = pw + Q * j < hw;
     const float* xw = x + b * C * hw + pw;
     float xv[C / 4][Q];
@@ -408,18 +408,36 @@ namespace {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-constexpr int kQ = 2;  // 16-pixel blocks per wave
+constexpr int64_t kMaxMfmaHW = (int64_t)1 << 26;
+
+// Tile shape per kernel: Q 16-pixel blocks per wave, NW waves per block.  Large blocks share one
+// LDS copy of the weights among many waves (the weights, not the registers, bound the number of
+// resident waves); the Q values are the measured best at 4 x 64 x 256 x 256.
+// 1024-thread blocks cap a thread at 128 registers: the wider shapes take Q = 1 so that nothing
+// spills.
+template <int CIN, int COUT, bool LN>
+struct ConvTile {
+  static constexpr int Q = (CIN + COUT > 192 || (LN && CIN + COUT >= 192)) ? 1 : 2, NW = 16;
+};
+template <>
+struct ConvTile<128, 64, false> {
+  static constexpr int Q = 2, NW = 16;
+};
+template <int C, int CM>
+struct MlpTile {
+  static constexpr int Q = 1, NW = 16;
+};
 
 // Persistent grid: as many blocks as fit on the device at once (occupancy query, cached per kernel),
 // at most one per tile.
 template <typename K>
-unsigned persistent_grid(K kernel, int64_t ntiles) {
+unsigned persistent_grid(K kernel, int threads, int64_t ntiles) {
   static int resident = 0;
   if (resident == 0) {
     int dev = 0, cus = 0, per_cu = 0;
     hipGetDevice(&dev);
     hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kernel, 256, 0);
+    hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kernel, threads, 0);
     hipGetLastError();
     resident = std::max(1, cus) * std::max(1, per_cu);
   }
@@ -430,11 +448,24 @@ template <int CIN, int COUT, bool LN>
 int launch_mfma(const float* x, int64_t B, int64_t HW, const float* W, const float* bias, const float* lw,
                 const float* lb, float eps, int act, const float* residual, const float* res_scale, float* y,
                 hipStream_t st) {
-  const int64_t tpb = (HW + 64 * kQ - 1) / (64 * kQ), ntiles = B * tpb;
-  auto kern = k_conv1x1_mfma<CIN, COUT, LN, kQ>;
-  hipLaunchKernelGGL(kern, dim3(persistent_grid(kern, ntiles)), dim3(256), 0, st, x, HW, tpb, ntiles, W, bias,
-                     lw, lb, eps, act, residual, res_scale, y);
+  constexpr int Q = ConvTile<CIN, COUT, LN>::Q, NW = ConvTile<CIN, COUT, LN>::NW;
+  const int64_t tpb = (HW + 16 * NW * Q - 1) / (16 * NW * Q), ntiles = B * tpb;
+  auto kern = k_conv1x1_mfma<CIN, COUT, LN, Q, NW>;
+  hipLaunchKernelGGL(kern, dim3(persistent_grid(kern, 64 * NW, ntiles)), dim3(64 * NW), 0, st, x, HW, tpb, ntiles,
+                     W, bias, lw, lb, eps, act, residual, res_scale, y);
   return check_launch("1x1 conv");
+}
+
+template <int C, int CM>
+int launch_mlp(const float* x, int64_t B, int64_t HW, const float* ln_w, const float* ln_b, float ln_eps,
+               const float* w1, const float* b1, const float* w2, const float* b2, const float* res_scale, float* y,
+               hipStream_t st) {
+  constexpr int Q = MlpTile<C, CM>::Q, NW = MlpTile<C, CM>::NW;
+  const int64_t tpb = (HW + 16 * NW * Q - 1) / (16 * NW * Q), ntiles = B * tpb;
+  auto kern = k_ln_mlp_mfma<C, CM, Q, NW>;
+  hipLaunchKernelGGL(kern, dim3(persistent_grid(kern, 64 * NW, ntiles)), dim3(64 * NW), 0, st, x, HW, tpb, ntiles,
+                     ln_w, ln_b, ln_eps, w1, b1, w2, b2, res_scale, y);
+  return check_launch("fused LN-MLP branch");
 }
 
 template <bool LN>
@@ -485,7 +516,9 @@ static int conv_impl(const float* x, int64_t B, int64_t Cin, int64_t HW, const f
   int rc = conv_args_ok(x, B, Cin, HW, weight, Cout, act, y);
   if (rc != CVN_OK) return rc;
   if (B == 0 || HW == 0) return CVN_OK;
-  const bool vec_ok = (HW % 4 == 0) && aligned16(x) && aligned16(y) && (!residual || aligned16(residual));
+  // the MFMA kernels address a lane's pixels with 32-bit byte offsets within 16 channel rows
+  const bool vec_ok = (HW % 4 == 0) && HW <= kMaxMfmaHW && aligned16(x) && aligned16(y) &&
+                      (!residual || aligned16(residual));
   if (vec_ok) {
     bool done = false;
     if (ln_w)
@@ -527,20 +560,13 @@ extern "C" int cvn_ln_mlp_residual_f32(const float* x, int64_t B, int64_t C, int
   if (B < 0 || HW < 0) return fail(CVN_ERR_ARG, "bad shape");
   if (B > 65535) return fail(CVN_ERR_UNSUPPORTED, "batch exceeds 65535");
   if (B == 0 || HW == 0) return CVN_OK;
-  if (HW % 4 != 0 || !aligned16(x) || !aligned16(y))
-    return fail(CVN_ERR_UNSUPPORTED, "fused branch needs HW %% 4 == 0 and 16-byte aligned buffers");
+  if (HW % 4 != 0 || HW > kMaxMfmaHW || !aligned16(x) || !aligned16(y))
+    return fail(CVN_ERR_UNSUPPORTED,
+                "fused branch needs HW %% 4 == 0, HW <= 2^26 and 16-byte aligned buffers");
   hipStream_t st = (hipStream_t)stream;
-  const int64_t tpb = (HW + 64 * kQ - 1) / (64 * kQ), ntiles = B * tpb;
-  if (C == 64 && Cmid == 128) {
-    auto kern = k_ln_mlp_mfma<64, 128, kQ>;
-    hipLaunchKernelGGL(kern, dim3(persistent_grid(kern, ntiles)), dim3(256), 0, st, x, HW, tpb, ntiles, ln_w, ln_b,
-                       ln_eps, w1, b1, w2, b2, res_scale, y);
-  } else if (C == 32 && Cmid == 64) {
-    auto kern = k_ln_mlp_mfma<32, 64, kQ>;
-    hipLaunchKernelGGL(kern, dim3(persistent_grid(kern, ntiles)), dim3(256), 0, st, x, HW, tpb, ntiles, ln_w, ln_b,
-                       ln_eps, w1, b1, w2, b2, res_scale, y);
-  } else {
-    return fail(CVN_ERR_UNSUPPORTED, "fused branch supports (C, Cmid) in {(64,128), (32,64)}");
-  }
-  return check_launch("fused LN-MLP branch");
+  if (C == 64 && Cmid == 128)
+    return launch_mlp<64, 128>(x, B, HW, ln_w, ln_b, ln_eps, w1, b1, w2, b2, res_scale, y, st);
+  if (C == 32 && Cmid == 64)
+    return launch_mlp<32, 64>(x, B, HW, ln_w, ln_b, ln_eps, w1, b1, w2, b2, res_scale, y, st);
+  return fail(CVN_ERR_UNSUPPORTED, "fused branch supports (C, Cmid) in {(64,128), (32,64)}");
 }
