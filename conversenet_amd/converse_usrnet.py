@@ -42,10 +42,22 @@ class ConvReverseDataNet(nn.Module):
         self.alpha = nn.Parameter(torch.zeros(1, 64, 1, 1))
         self.eps = eps
 
+    @property
+    def biaseps(self):
+        """sigmoid(alpha - 9) + eps as the reference's forward stores it (converse_usrnet.py:46); the HIP
+        path computes this tensor only when it is read."""
+        v = self.__dict__.get("_biaseps")
+        return torch.sigmoid(self.alpha - 9.0) + self.eps if v is None else v
+
+    @biaseps.setter
+    def biaseps(self, v):
+        self.__dict__["_biaseps"] = v
+
     def forward(self, x, k, sf, padding=0, padding_mode="circular"):
-        self.biaseps = torch.sigmoid(self.alpha - 9.0) + self.eps
         if _hip_eligible(x, k, self.alpha):
+            self.biaseps = None  # read lazily from the current alpha
             return functional.converse2d_fused(x, k, self.alpha.reshape(-1), sf, padding, padding_mode, self.eps)
+        self.biaseps = torch.sigmoid(self.alpha - 9.0) + self.eps
         return composite.converse2d_module(x, k, self.alpha, sf, padding, padding_mode, self.eps)
 
     def splits(self, a, scale):

@@ -381,7 +381,10 @@ __global__ void __launch_bounds__(64 * NW) k_ln_mlp_mfma(const float* x, int64_t
   }
 }
 
-// Plain VALU 1x1 conv for channel counts / sizes the MFMA tiles do not cover (e.g. 1 or 3 channels).
+// Plain VALU 1x1 conv for channel counts / sizes the MFMA tiles do not cover (e.g. 1 or 3 channels,
+// or pixel counts that are not a multiple of 4).  Thread = one pixel and a group of kOutGroup
+// output channels (grid z); each input channel value is loaded once and feeds the whole group.
+constexpr int kOutGroup = 8;
 __global__ void __launch_bounds__(256) k_conv1x1_any(const float* __restrict__ x, int64_t HW, int Cin,
                                                      const float* __restrict__ W, const float* __restrict__ bias,
                                                      int Cout, int act, const float* residual,
@@ -389,14 +392,27 @@ __global__ void __launch_bounds__(256) k_conv1x1_any(const float* __restrict__ x
   const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (p >= HW) return;
   const int64_t b = blockIdx.y;
+  const int o0 = blockIdx.z * kOutGroup;
+  const int no = min(kOutGroup, Cout - o0);
   const float* xb = x + b * Cin * HW + p;
-  for (int o = 0; o < Cout; ++o) {
-    float acc = bias ? bias[o] : 0.f;
-    for (int c = 0; c < Cin; ++c) acc = fmaf(W[o * Cin + c], xb[(int64_t)c * HW], acc);
-    if (act == CVN_ACT_GELU) acc = gelu_f(acc);
+  float acc[kOutGroup];
+#pragma unroll
+  for (int k = 0; k < kOutGroup; ++k) acc[k] = (k < no && bias) ? bias[o0 + k] : 0.f;
+  for (int c = 0; c < Cin; ++c) {
+    const float xv = xb[(int64_t)c * HW];
+#pragma unroll
+    for (int k = 0; k < kOutGroup; ++k)
+      if (k < no) acc[k] = fmaf(W[(o0 + k) * Cin + c], xv, acc[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < kOutGroup; ++k) {
+    if (k >= no) break;
+    const int o = o0 + k;
+    float v = acc[k];
+    if (act == CVN_ACT_GELU) v = gelu_f(v);
     const int64_t oi = (b * Cout + o) * HW + p;
-    if (residual) acc = fmaf(res_scale ? res_scale[o] : 1.f, acc, residual[oi]);
-    y[oi] = acc;
+    if (residual) v = fmaf(res_scale ? res_scale[o] : 1.f, v, residual[oi]);
+    y[oi] = v;
   }
 }
 
@@ -530,7 +546,8 @@ static int conv_impl(const float* x, int64_t B, int64_t Cin, int64_t HW, const f
     if (done) return rc;
   }
   if (ln_w) return fail(CVN_ERR_UNSUPPORTED, "LayerNorm-fused 1x1 conv needs an MFMA tile shape");
-  dim3 grid((unsigned)((HW + 255) / 256), (unsigned)B);
+  if ((Cout + kOutGroup - 1) / kOutGroup > 65535) return fail(CVN_ERR_UNSUPPORTED, "too many output channels");
+  dim3 grid((unsigned)((HW + 255) / 256), (unsigned)B, (unsigned)((Cout + kOutGroup - 1) / kOutGroup));
   hipLaunchKernelGGL(k_conv1x1_any, grid, dim3(256), 0, st, x, HW, (int)Cin, weight, bias, (int)Cout, act,
                      residual, res_scale, y);
   return check_launch("1x1 conv");

@@ -146,12 +146,25 @@ class Converse2D(nn.Module):
             return False
         return _hip_eligible(x, self.weight, self.bias)
 
+    @property
+    def biaseps(self):
+        """lambda = sigmoid(bias - 9) + eps, as the reference's forward stores it (util_converse.py:150).
+        The HIP path evaluates lambda inside the transfer-table kernel and computes this tensor only
+        when it is read."""
+        v = self.__dict__.get("_biaseps")
+        return torch.sigmoid(self.bias - 9.0) + self.eps if v is None else v
+
+    @biaseps.setter
+    def biaseps(self, v):
+        self.__dict__["_biaseps"] = v
+
     def forward(self, x, act=None):
         """act='gelu' applies exact GELU to the output (fused on store on the HIP path)."""
-        self.biaseps = torch.sigmoid(self.bias - 9.0) + self.eps
         if self._use_hip(x):
+            self.biaseps = None  # read lazily from the current bias
             return functional.converse2d_fused(x, self.weight, self.bias.reshape(-1), self.scale, self.padding,
                                                self.padding_mode, self.eps, act)
+        self.biaseps = torch.sigmoid(self.bias - 9.0) + self.eps
         out = composite.converse2d_module(x, self.weight, self.bias, self.scale, self.padding, self.padding_mode,
                                           self.eps)
         return F.gelu(out) if act == "gelu" else out
@@ -186,7 +199,7 @@ def _fused_block_forward(blk, x, alpha1=None, alpha2=None):
     if (x.shape[2] * x.shape[3]) % 4 != 0 or not isinstance(cv, Converse2D) or _backend(cv.backend) == "pytorch":
         return None
     t = functional.conv1x1(x, c11.weight, c11.bias, act="gelu", ln=(ln1.weight, ln1.bias, ln1.eps))
-    cv.biaseps = torch.sigmoid(cv.bias - 9.0) + cv.eps
+    cv.biaseps = None  # read lazily from the current bias
     t = functional.converse2d_fused(t, cv.weight, cv.bias.reshape(-1), cv.scale, cv.padding, cv.padding_mode,
                                     cv.eps, act="gelu")
     x = functional.conv1x1(t, c15.weight, c15.bias, residual=x,

@@ -300,3 +300,20 @@ def test_op_level_large_psf(s):
     dev = torch.device("cuda")
     got = Fh.converse2d_op(*(torch.from_numpy(a).to(dev) for a in (x, x0, wt, b)), s, 1e-5).cpu().numpy()
     assert np.abs(got - ref).max() <= TOL
+
+
+def test_module_biaseps_after_hip_forward():
+    """The HIP path leaves biaseps = sigmoid(bias - 9) + eps readable after forward, as the reference's
+    Converse2D.forward (util_converse.py:150) and ConvReverseDataNet.forward (converse_usrnet.py:46)."""
+    from conversenet_amd.util_converse import Converse2D
+    from conversenet_amd.converse_usrnet import ConvReverseDataNet
+    dev = torch.device("cuda")
+    m = Converse2D(4, 4, 3).to(dev)
+    d = ConvReverseDataNet().to(dev)
+    with torch.no_grad():
+        m.bias.fill_(0.3)
+        d.alpha.fill_(-0.2)
+        m(torch.randn(1, 4, 12, 12, device=dev))
+        d(torch.randn(1, 64, 8, 8, device=dev), torch.rand(1, 64, 3, 3, device=dev), 2)
+    assert torch.allclose(m.biaseps, torch.sigmoid(m.bias - 9.0) + 1e-5)
+    assert torch.allclose(d.biaseps, torch.sigmoid(d.alpha - 9.0) + 1e-3)
