@@ -256,6 +256,39 @@ def bench_layer(torch, Fh, dev, B, C, H, W, k, s, p, dist, iters):
             "Gpix*ch/s": B * C * H * s * W * s / t / 1e9, "GB/s": nbytes / t / 1e9, "frac_hbm": nbytes / t / HBM_PEAK}
 
 
+def bench_block_pointwise(torch, Fh, dev, iters):
+    """The three channel-mixing kernels of one ConverseBlockAlphaVariant at the Converse-USRNet body
+    shape (B4 C64 256x256, hidden 128): LN + 1x1 64->128 + GELU, 1x1 128->64 + alpha-scaled residual,
+    and the fused LN -> 1x1 -> GELU -> 1x1 -> residual branch.  Bytes are the algorithmic HBM bytes
+    (each activation read or written once), FLOPs the 1x1 products (2 per multiply-add)."""
+    B, C, H, W = 4, 64, 256, 256
+    npx = B * H * W
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn(B, C, H, W, device=dev, generator=g)
+    h = torch.randn(B, 2 * C, H, W, device=dev, generator=g)
+    w1 = torch.randn(2 * C, C, 1, 1, device=dev, generator=g) / 8
+    b1 = torch.randn(2 * C, device=dev, generator=g)
+    w2 = torch.randn(C, 2 * C, 1, 1, device=dev, generator=g) / 11
+    b2 = torch.randn(C, device=dev, generator=g)
+    lw, lb = torch.ones(C, device=dev), torch.zeros(C, device=dev)
+    al = torch.randn(C, device=dev, generator=g)
+    y = torch.empty_like(x)
+    cases = {
+        "ln_conv1x1_64_128_gelu": (lambda: Fh.conv1x1(x, w1, b1, act="gelu", ln=(lw, lb, 1e-5)),
+                                   4 * npx * (C + 2 * C), 2 * npx * C * 2 * C),
+        "conv1x1_128_64_residual": (lambda: Fh.conv1x1(h, w2, b2, residual=x, res_scale=al),
+                                    4 * npx * (2 * C + C + C), 2 * npx * C * 2 * C),
+        "ln_mlp_64_128_residual": (lambda: Fh.ln_mlp_residual(x, lw, lb, 1e-5, w1, b1, w2, b2, res_scale=al, out=y),
+                                   4 * npx * 2 * C, 4 * npx * C * 2 * C),
+    }
+    out = {"workload": "ConverseBlockAlphaVariant channel mixing, B4 C64 256x256, hidden 128, fp32"}
+    for name, (fn, nbytes, flops) in cases.items():
+        t = time_events(torch, fn, iters)
+        out[name] = {"us": t * 1e6, "GB/s": nbytes / t / 1e9, "frac_hbm": nbytes / t / HBM_PEAK,
+                     "TFLOP/s": flops / t / 1e12, "frac_mfma_fp32": flops / t / FP32_MFMA_PEAK}
+    return out
+
+
 def only_kernel(torch, Fh, args, dev, x, step):
     """Runs one kernel family alone (warmup + steps) for rocprofv3 runs; prints a short JSON line.
     copy: the calibration copy kernel over COPY_FLOATS floats (bytes moved = 8 * COPY_FLOATS)."""
@@ -365,6 +398,7 @@ def main():
     extra["conv1x1_gelu_64"] = {"ms": t_cv * 1e3, "GB/s": cv_bytes / t_cv / 1e9,
                                 "frac_hbm": cv_bytes / t_cv / HBM_PEAK, "TFLOP/s": cv_flops / t_cv / 1e12,
                                 "frac_mfma": cv_flops / t_cv / FP32_MFMA_PEAK}
+    extra["block_pointwise"] = bench_block_pointwise(torch, Fh, dev, max(10, args.steps // 2))
     if not args.no_model:
         extra["converse_dncnn"] = bench_model(torch, dev)
         extra["converse_usrnet"] = bench_usrnet(torch, dev)
