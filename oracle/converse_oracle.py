@@ -18,6 +18,8 @@ How each function is pinned (checked by tests/test_oracle.py and tests/test_orac
   converse2d_op       the reference's own compiled C++ op (oracle/_ref, fp64 and fp32), I4, I6, I7
   converse2d_module   the compiled reference op + F.pad + crop; I6 normal equations; I7; I8
   converse2d_op_stable   algebraic identity I5 against converse2d_op in fp64
+  converse2d_module_backward   central finite differences of converse2d_module in fp64, and torch
+                      autograd (fp64) of the reference op sequence restated in torch
   layernorm_cf        zero mean / unit biased variance closed form; torch F.layer_norm
   conv1x1, gelu       einsum definition; erf special values; torch F.conv2d / F.gelu
   converse_block, converse_dncnn, conv_reverse_datanet, converse_usrnet
@@ -201,6 +203,102 @@ def converse2d_module(x, weight, bias, scale=1, padding=2, padding_mode="circula
         ps = padding * s
         out = out[..., ps:-ps, ps:-ps]
     return np.ascontiguousarray(out)
+
+
+# ------------------------------------------------------------------------------------------------
+# Backward of the module path (the reference differentiates util_converse.py:142-192 through torch
+# autograd: converse2d.cpp:223-227 registers the op as CompositeImplicitAutograd; gradients are
+# compared in test/test_error.py:51-54,73-76).  Explicit spectral adjoint, fp64.
+# ------------------------------------------------------------------------------------------------
+def hold(s, n):
+    """Nearest-hold response H_s(u; n) = sum_{a<s} exp(-2 pi i u a / n) for u in [0, n) (identity I2)."""
+    u = np.arange(n)[:, None]
+    return np.exp(-2j * np.pi * u * np.arange(s)[None, :] / n).sum(axis=1)
+
+
+def pad_adjoint(dy, p, mode, H, W):
+    """Adjoint of pad_nchw: every padded sample's gradient is added to the source sample it copies
+    (constant-mode padding samples are dropped)."""
+    if p == 0:
+        return dy.copy()
+    ih = [pad_index(i, H, p, mode) for i in range(H + 2 * p)]
+    iw = [pad_index(i, W, p, mode) for i in range(W + 2 * p)]
+    rows = np.zeros(dy.shape[:-2] + (H, dy.shape[-1]), dtype=dy.dtype)
+    for i, si in enumerate(ih):
+        if si >= 0:
+            rows[..., si, :] += dy[..., i, :]
+    out = np.zeros(dy.shape[:-2] + (H, W), dtype=dy.dtype)
+    for j, sj in enumerate(iw):
+        if sj >= 0:
+            out[..., sj] += rows[..., j]
+    return out
+
+
+def module_transfer(weight, bias, scale, h, w, eps):
+    """The module path's transfer function, in the form the backward differentiates:
+    out_full = Re ifft2(Phi * tile_s(fft2(y))) with Phi = Hn + conj(K) g, g = (1 - M(K Hn)) / D,
+    D = M(|K|^2) + lambda (M = alias-class mean tiled back; this is the reference solve
+    util_converse.py:176-187 with x0 = nearest(y), whose spectrum is Hn tile(Y)).
+    Returns (K, Hn, g, D, Phi) with K, g, D, Phi of shape (Pb, C, Hs, Ws)."""
+    s = int(scale)
+    Hs, Ws = h * s, w * s
+    K = p2o(weight.astype(np.float64), (Hs, Ws))
+    Hn = hold(s, Hs)[:, None] * hold(s, Ws)[None, :]
+    C = weight.shape[1]
+    lmb = lam(np.asarray(bias, np.float64).reshape(1, C, 1, 1), eps)
+
+    def mt(a):
+        return np.tile(splits_mean(a, s), (1, 1, s, s))
+
+    D = mt(np.abs(K) ** 2) + lmb
+    g = (1.0 - mt(K * Hn)) / D
+    return K, Hn, g, D, Hn + np.conj(K) * g
+
+
+def converse2d_module_backward(x, weight, bias, gout, scale=1, padding=2, padding_mode="circular", eps=1e-5):
+    """Gradients (dx, dweight, dbias) of sum(gout * converse2d_module(x, weight, bias, ...)), fp64.
+
+    x (B,C,H,W); weight (1 or B, C, kh, kw); bias (1,C,1,1) or (C,); gout (B,C,H*s,W*s).
+    Chain: dX = fft2(uncrop(gout)) / (Hs Ws); dx = pad^T(Re F*_{hw}(alias_sum(conj(Phi) dX)));
+    dPhi = sum over the samples sharing a psf of conj(tile Y) dX; per alias class, with
+    P = sum_m dPhi_m K_m and rho = -Re(conj(P) g) / D:
+      dK_m = conj(dPhi_m) g - P conj(Hn_m) / (s^2 D) + 2 rho K_m / s^2,   dlambda = sum rho;
+    dweight[i, j] = Re sum_{u,v} dK[u,v] exp(+2 pi i (u (i - kh//2) / Hs + v (j - kw//2) / Ws));
+    dbias = dlambda * sigmoid'(bias - 9)."""
+    s, p = int(scale), int(padding)
+    x = np.asarray(x, np.float64)
+    B, C, H, W = x.shape
+    y = pad_nchw(x, p, padding_mode) if p > 0 else x
+    h, w = y.shape[-2:]
+    Hs, Ws = h * s, w * s
+    kh, kw = weight.shape[-2:]
+    K, Hn, g, D, Phi = module_transfer(weight, bias, s, h, w, eps)
+    Gf = np.zeros((B, C, Hs, Ws))
+    ps = p * s
+    Gf[..., ps:ps + H * s, ps:ps + W * s] = np.asarray(gout, np.float64)
+    dX = fft2(Gf) / (Hs * Ws)
+    # dx
+    dT = np.conj(Phi) * dX
+    dY = splits_mean(dT, s) * (s * s)
+    dy = np.real(ifft2(dY)) * (h * w)
+    dx = pad_adjoint(dy, p, padding_mode, H, W)
+    # dPhi (summed over the samples that share a psf)
+    T = np.tile(fft2(y), (1, 1, s, s))
+    dPhi = np.conj(T) * dX
+    if weight.shape[0] == 1:
+        dPhi = dPhi.sum(axis=0, keepdims=True)
+    Pm = np.tile(splits_mean(dPhi * K, s), (1, 1, s, s)) * (s * s)
+    rho = -np.real(np.conj(Pm) * g) / D
+    dK = np.conj(dPhi) * g - Pm * np.conj(Hn) / (s * s * D) + 2.0 * rho * K / (s * s)
+    dlmb = rho.sum(axis=(-2, -1)) / (s * s)                         # (Pb, C)
+    full = ifft2(dK) * (Hs * Ws)                                     # sum dK exp(+...)
+    mi = (np.arange(kh) - kh // 2) % Hs
+    nj = (np.arange(kw) - kw // 2) % Ws
+    dweight = np.real(full[..., mi[:, None], nj[None, :]])
+    b = np.asarray(bias, np.float64).reshape(C)
+    sig = 1.0 / (1.0 + np.exp(-(b - 9.0)))
+    dbias = (dlmb.sum(axis=0) * sig * (1.0 - sig)).reshape(1, C, 1, 1)
+    return dx, dweight, dbias
 
 
 # ------------------------------------------------------------------------------------------------
