@@ -45,6 +45,9 @@ SIGNATURES = {
     "cvn_converse2d_op_workspace": (_size, [_i64, _i64, _i64, _i64, _int, _int, _int]),
     "cvn_converse2d_op_f32": (_int, [_ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _int, _int, _ptr, _f32, _int, _ptr,
                                      _ptr, _size, _ptr]),
+    "cvn_converse2d_bwd_workspace": (_size, [_i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int]),
+    "cvn_converse2d_bwd_f32": (_int, [_ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _int, _int, _ptr, _f32, _int,
+                                      _int, _int, _ptr, _ptr, _ptr, _ptr, _size, _ptr]),
     "cvn_clear_cache": (_int, []),
     "cvn_layernorm_cf_f32": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _f32, _ptr, _ptr]),
     "cvn_conv1x1_f32": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _i64, _int, _ptr, _ptr, _ptr, _ptr]),

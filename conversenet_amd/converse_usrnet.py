@@ -10,7 +10,7 @@ import torch
 import torch.nn as nn
 
 from . import composite, functional
-from .util_converse import ConverseBlock, ConverseBlockAlphaVariant, _hip_eligible, sequential
+from .util_converse import _hip_grad_eligible, ConverseBlock, ConverseBlockAlphaVariant, _hip_eligible, sequential
 
 
 class MultiConverseBlock(nn.Module):
@@ -57,6 +57,9 @@ class ConvReverseDataNet(nn.Module):
         if _hip_eligible(x, k, self.alpha):
             self.biaseps = None  # read lazily from the current alpha
             return functional.converse2d_fused(x, k, self.alpha.reshape(-1), sf, padding, padding_mode, self.eps)
+        if k.dim() == 4 and _hip_grad_eligible(x, k, self.alpha, sf, padding, padding_mode):
+            self.biaseps = None
+            return functional.converse2d_train(x, k, self.alpha, sf, padding, padding_mode, self.eps)
         self.biaseps = torch.sigmoid(self.alpha - 9.0) + self.eps
         return composite.converse2d_module(x, k, self.alpha, sf, padding, padding_mode, self.eps)
 

@@ -247,6 +247,67 @@ __device__ __forceinline__ double2 horner4(const double2* P, int n4, double2 z) 
   return cmadd(cmadd(cmadd(c3, z, c2), z, c1), z, c0);
 }
 
+// Per-block LDS tables of the tiled transfer-table kernels (k_phi_tile, k_phi_grad): row tables for
+// every HR row, column tables for the chunk's HR columns vbeg + v + b w (v < nv, b < S), and the psf
+// row sums P[(v S + b) kh4 + i] (rows zero-padded to kh4).
+struct PhiTileView {
+  double2 *zH, *phH, *hH, *zW, *phW, *hW, *P;
+};
+template <int S>
+__device__ PhiTileView phi_tile_prep(const PhiArgs& a, unsigned char* phl, int64_t cp, int vbeg, int nv, int vc) {
+  const int tid = threadIdx.x, nth = blockDim.x;
+  const int Hs = a.Hs, Ws = a.Ws, kh = a.kh, kw = a.kw;
+  const int kh4 = round4(kh), kw4 = round4(kw);
+  const PhiTileLds L = phi_tile_lds(S, Hs, kh, kw, vc);
+  PhiTileView t;
+  t.zH = (double2*)(phl + L.zH);
+  t.phH = (double2*)(phl + L.phH);
+  t.hH = (double2*)(phl + L.hH);
+  t.zW = (double2*)(phl + L.zW);
+  t.phW = (double2*)(phl + L.phW);
+  t.hW = (double2*)(phl + L.hW);
+  t.P = (double2*)(phl + L.P);
+  float* ps = (float*)(phl + L.psf);
+
+  const float* psf = a.psf + cp * kh * kw;
+  for (int e = tid; e < kh * kw4; e += nth) {
+    const int i = e / kw4, j = e - i * kw4;
+    ps[e] = j < kw ? psf[i * kw + j] : 0.f;
+  }
+  for (int u = tid; u < Hs; u += nth) {
+    t.zH[u] = dexpi((double)u, (double)Hs);
+    t.phH[u] = dexpi(-(double)(((int64_t)u * (kh / 2)) % Hs), (double)Hs);
+    if (S > 1) t.hH[u] = hold(S, u, Hs);
+  }
+  for (int e = tid; e < nv * S; e += nth) {
+    const int v = e / S, b = e - v * S;
+    const int64_t vb = vbeg + v + (int64_t)b * a.w;
+    t.zW[e] = dexpi((double)vb, (double)Ws);
+    t.phW[e] = dexpi(-(double)((vb * (kw / 2)) % Ws), (double)Ws);
+    t.hW[e] = hold(S, vb, Ws);
+  }
+  __syncthreads();
+  // row sums (real coefficients, same four-chain Horner); rows zero-padded to kh4
+  for (int e = tid; e < nv * S * kh4; e += nth) {
+    const int vbq = e / kh4, i = e - vbq * kh4;
+    double2 acc = make_double2(0.0, 0.0);
+    if (i < kh) {
+      const double2 z = t.zW[vbq], z2 = dcmul(z, z), z4 = dcmul(z2, z2);
+      const float* row = ps + i * kw4;
+      double2 q[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) q[r] = make_double2((double)row[kw4 - 4 + r], 0.0);
+      for (int j = kw4 - 8; j >= 0; j -= 4)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) q[r] = cmadd(q[r], z4, make_double2((double)row[j + r], 0.0));
+      acc = dcmul(cmadd(cmadd(cmadd(q[3], z, q[2]), z, q[1]), z, q[0]), t.phW[vbq]);
+    }
+    t.P[e] = acc;
+  }
+  __syncthreads();
+  return t;
+}
+
 template <int S>
 __global__ void __launch_bounds__(256) k_phi_tile(PhiArgs a, int op, int vc, int nchunk) {
   extern __shared__ __align__(16) unsigned char phl[];
@@ -256,54 +317,10 @@ __global__ void __launch_bounds__(256) k_phi_tile(PhiArgs a, int op, int vc, int
   const int vbeg = chunk * vc;
   const int nv = min(vc, a.nv0 - vbeg);
   const int c = (int)(cp % a.C);
-  const int Hs = a.Hs, Ws = a.Ws, h = a.h, kh = a.kh, kw = a.kw;
-  const int kh4 = round4(kh), kw4 = round4(kw);
-  const PhiTileLds L = phi_tile_lds(S, Hs, kh, kw, vc);
-  double2* zH = (double2*)(phl + L.zH);
-  double2* phH = (double2*)(phl + L.phH);
-  double2* hH = (double2*)(phl + L.hH);
-  double2* zW = (double2*)(phl + L.zW);
-  double2* phW = (double2*)(phl + L.phW);
-  double2* hW = (double2*)(phl + L.hW);
-  double2* P = (double2*)(phl + L.P);
-  float* ps = (float*)(phl + L.psf);
-
-  const float* psf = a.psf + cp * kh * kw;
-  for (int e = tid; e < kh * kw4; e += nth) {
-    const int i = e / kw4, j = e - i * kw4;
-    ps[e] = j < kw ? psf[i * kw + j] : 0.f;
-  }
-  for (int u = tid; u < Hs; u += nth) {
-    zH[u] = dexpi((double)u, (double)Hs);
-    phH[u] = dexpi(-(double)(((int64_t)u * (kh / 2)) % Hs), (double)Hs);
-    if (S > 1) hH[u] = hold(S, u, Hs);
-  }
-  for (int e = tid; e < nv * S; e += nth) {
-    const int v = e / S, b = e - v * S;
-    const int64_t vb = vbeg + v + (int64_t)b * a.w;
-    zW[e] = dexpi((double)vb, (double)Ws);
-    phW[e] = dexpi(-(double)((vb * (kw / 2)) % Ws), (double)Ws);
-    hW[e] = hold(S, vb, Ws);
-  }
-  __syncthreads();
-  // row sums (real coefficients, same four-chain Horner); rows zero-padded to kh4
-  for (int e = tid; e < nv * S * kh4; e += nth) {
-    const int vbq = e / kh4, i = e - vbq * kh4;
-    double2 acc = make_double2(0.0, 0.0);
-    if (i < kh) {
-      const double2 z = zW[vbq], z2 = dcmul(z, z), z4 = dcmul(z2, z2);
-      const float* row = ps + i * kw4;
-      double2 q[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) q[r] = make_double2((double)row[kw4 - 4 + r], 0.0);
-      for (int j = kw4 - 8; j >= 0; j -= 4)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) q[r] = cmadd(q[r], z4, make_double2((double)row[j + r], 0.0));
-      acc = dcmul(cmadd(cmadd(cmadd(q[3], z, q[2]), z, q[1]), z, q[0]), phW[vbq]);
-    }
-    P[e] = acc;
-  }
-  __syncthreads();
+  const int Hs = a.Hs, Ws = a.Ws, h = a.h, kh = a.kh;
+  const int kh4 = round4(kh);
+  const PhiTileView tv = phi_tile_prep<S>(a, phl, cp, vbeg, nv, vc);
+  const double2 *zH = tv.zH, *phH = tv.phH, *hH = tv.hH, *hW = tv.hW, *P = tv.P;
 
   const double lmb = lambda_of(a, c);
   const double norm = 1.0 / ((double)Hs * (double)Ws);
@@ -674,6 +691,327 @@ __global__ void __launch_bounds__(256) k_rows_inv(RowInvArgs a) {
 }
 
 // ================================================================================================
+// Backward of the module path.  With G = uncrop(grad_out) on the HR grid, dZ = F_{HsWs}(G):
+//   dx      = pad^T(Re F*_{hw}(alias_sum(conj(Phi') dZ)))          (Phi' = Phi / (Hs Ws), the table)
+//   dPhi    = sum over the samples sharing a psf of conj(tile Y) dZ / (Hs Ws),   Y = F_{hw}(pad x)
+//   per alias class, with g = (1 - M(K Hn)) / D, D = M(|K|^2) + lambda, P = sum_m dPhi_m K_m and
+//   rho = -Re(conj(P) g) / D:   dK_m = conj(dPhi_m) g - P conj(Hn_m) / (s^2 D) + 2 rho K_m / s^2,
+//   dlambda = sum rho;   dpsf[i][j] = Re sum_{u,v} dK[u,v] exp(+2 pi i (u (i - ch) / Hs + v (j - cw) / Ws));
+//   dbias = dlambda sigmoid'(bias - 9).
+// The same chain as autograd through util_converse.py:142-192 (the reference registers its op as
+// CompositeImplicitAutograd, converse2d.cpp:223-227).
+// ================================================================================================
+
+// Column pass: one block per (LR column class v0 in [0, NC), psf group); the block loops over the
+// planes that share the group's psf (psf_batch 1: the B planes of channel c; otherwise one plane).
+struct ColBwdArgs {
+  const float2* Sg;   // (P, NCs, Hs) row spectra of uncrop(grad_out)
+  float2* Sx;         // (P, NC, h)   row spectra of pad(x) in (weight gradients), dS out (in place)
+  const float2* phi;  // (Cp, NCs, Hs) module table Phi'
+  float2* dphi;       // (Cp, Ws, Hs) or null: columns of the processed classes
+  int64_t B, C, psf_batch;
+  int h, w, s, Hs, Ws, NC, NCs;
+  FftPlan plan_h, plan_H;
+  const char *tabs_h, *tabs_H;
+  int rad_off;
+};
+
+__host__ __device__ inline size_t cols_bwd_lds(int h, int Hs, int s, bool wg) {
+  return (size_t)(h + Hs + 3 * h + 2 * s * Hs + (wg ? s * Hs : 0)) * sizeof(float2);
+}
+
+__global__ void __launch_bounds__(256) k_cols_bwd(ColBwdArgs a) {
+  extern __shared__ float2 sm[];
+  const int tid = threadIdx.x, nth = blockDim.x;
+  const bool wg = a.dphi != nullptr;
+  float2* twh = sm;
+  float2* twH = twh + a.h;
+  float2* Ya = twH + a.Hs;         // h: Y (pad x, LR column spectrum)
+  float2* Yb = Ya + a.h;           // h
+  float2* Yc = Yb + a.h;           // h: dY
+  float2* Xa = Yc + a.h;           // s Hs: dZ
+  float2* Xb = Xa + a.s * a.Hs;    // s Hs
+  float2* acc = Xb + a.s * a.Hs;   // s Hs: dPhi (weight gradients only)
+  const int v0 = blockIdx.x;
+  const int64_t grp = blockIdx.y;  // psf plane: c (psf_batch 1) or the plane (psf_batch B)
+  char* radh = (char*)sm + a.rad_off;
+  char* radH = radh + rader_lds_bytes(a.plan_h);
+  load_plan_tabs(a.plan_h, a.tabs_h, twh, radh, tid, nth);
+  if (a.Hs != a.h) load_plan_tabs(a.plan_H, a.tabs_H, twH, radH, tid, nth);
+  else radH = radh;
+  const float2* tH = (a.Hs != a.h) ? twH : twh;
+  const float2* ph = a.phi + grp * (int64_t)a.NCs * a.Hs;
+  const FastDiv fHs = fast_div(a.Hs), fh = fast_div(a.h);
+  const float norm = 1.0f / ((float)a.Hs * (float)a.Ws);
+  if (wg)
+    for (int i = tid; i < a.s * a.Hs; i += nth) acc[i] = make_float2(0.f, 0.f);
+  const int64_t nplanes = (a.psf_batch == 1) ? a.B : 1;
+  for (int64_t ib = 0; ib < nplanes; ++ib) {
+    const int64_t plane = (a.psf_batch == 1) ? ib * a.C + grp : grp;
+    const float2* Sgp = a.Sg + plane * (int64_t)a.NCs * a.Hs;
+    float2* Sxp = a.Sx + plane * (int64_t)a.NC * a.h;
+    __syncthreads();  // the previous plane's LDS reads are done
+    for (int idx = tid; idx < a.s * a.Hs; idx += nth) {
+      const int b = idx / fHs, u = idx - b * a.Hs;
+      const int vb = v0 + b * a.w;
+      // row spectra of real rows are Hermitian in the column index
+      Xa[idx] = vb <= a.Ws / 2 ? Sgp[(int64_t)vb * a.Hs + u] : cconj(Sgp[(int64_t)(a.Ws - vb) * a.Hs + u]);
+    }
+    if (wg)
+      for (int u = tid; u < a.h; u += nth) Ya[u] = Sxp[(int64_t)v0 * a.h + u];
+    __syncthreads();
+    const float2* dZ = fft_lds<false>(a.plan_H, Xa, Xb, a.s, tH, tid, nth, radH);
+    if (wg) {
+      const float2* Y = fft_lds<false>(a.plan_h, Ya, Yb, 1, twh, tid, nth, radh);
+      for (int idx = tid; idx < a.s * a.Hs; idx += nth) {
+        const int u = idx - (idx / fHs) * a.Hs;
+        const float2 t = cmul(cconj(Y[u - (u / fh) * a.h]), dZ[idx]);
+        acc[idx].x = fmaf(t.x, norm, acc[idx].x);
+        acc[idx].y = fmaf(t.y, norm, acc[idx].y);
+      }
+    }
+    for (int u0 = tid; u0 < a.h; u0 += nth) {
+      float2 m = make_float2(0.f, 0.f);
+      for (int b = 0; b < a.s; ++b) {
+        const int vb = v0 + b * a.w;
+        for (int aa = 0; aa < a.s; ++aa) {
+          const int u = u0 + aa * a.h;
+          const float2 f = vb <= a.Ws / 2 ? ph[(int64_t)vb * a.Hs + u]
+                                          : cconj(ph[(int64_t)(a.Ws - vb) * a.Hs + (u == 0 ? 0 : a.Hs - u)]);
+          const float2 t = cmul(cconj(f), dZ[b * a.Hs + u]);
+          m.x += t.x;
+          m.y += t.y;
+        }
+      }
+      Yc[u0] = m;
+    }
+    __syncthreads();
+    const float2* R = fft_lds<true>(a.plan_h, Yc, (Yc == Ya) ? Yb : Ya, 1, twh, tid, nth, radh);
+    for (int r = tid; r < a.h; r += nth) Sxp[(int64_t)v0 * a.h + r] = R[r];
+  }
+  if (wg) {
+    __syncthreads();
+    float2* dp = a.dphi + grp * (int64_t)a.Ws * a.Hs;
+    for (int idx = tid; idx < a.s * a.Hs; idx += nth) {
+      const int b = idx / fHs, u = idx - b * a.Hs;
+      dp[(int64_t)(v0 + b * a.w) * a.Hs + u] = acc[idx];
+    }
+  }
+}
+
+// Adjoint of the padding: dx[i][j] = sum of dy over the padded samples that copy source (i, j).
+__global__ void __launch_bounds__(256) k_pad_adj(const float* __restrict__ dy, int64_t P, int H, int W, int pad,
+                                                 int mode, float* __restrict__ dx) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= P * H * W) return;
+  const int64_t plane = e / ((int64_t)H * W);
+  const int rem = (int)(e - plane * H * W);
+  const int i = rem / W, j = rem - (rem / W) * W;
+  const int h = H + 2 * pad, w = W + 2 * pad;
+  int rows[16], cols[16];
+  int nr = 0, nc = 0;
+  rows[nr++] = i + pad;
+  cols[nc++] = j + pad;
+  for (int q = 0; q < 2 * pad && nr < 16; ++q) {  // border rows / columns: [0, pad) and [H + pad, h)
+    const int r = q < pad ? q : H + q;
+    if (pad_src(r, H, pad, mode) == i) rows[nr++] = r;
+  }
+  for (int q = 0; q < 2 * pad && nc < 16; ++q) {
+    const int c = q < pad ? q : W + q;
+    if (pad_src(c, W, pad, mode) == j) cols[nc++] = c;
+  }
+  const float* p = dy + plane * (int64_t)h * w;
+  float acc = 0.f;
+  for (int a = 0; a < nr; ++a)
+    for (int b = 0; b < nc; ++b) acc += p[(int64_t)rows[a] * w + cols[b]];
+  dx[e] = acc;
+}
+
+// Per-class gradient of the transfer function: block = (psf plane, chunk of vc column classes
+// v0 in [0, w)), thread = alias class, same LDS tables as k_phi_tile.  Writes dK for every member
+// (full width) and the block's sum of rho (the lambda gradient).
+struct PhiGradArgs {
+  const float2* dphi;  // (Cp, Ws, Hs): columns of classes v0 <= w / 2; the others by symmetry
+  float2* dK;          // (Cp, Ws, Hs)
+  double* part;        // (Cp, nchunk): per-block sums of rho
+};
+
+template <int S>
+__global__ void __launch_bounds__(256) k_phi_grad(PhiArgs a, PhiGradArgs gr, int vc, int nchunk) {
+  extern __shared__ __align__(16) unsigned char phl[];
+  __shared__ double red[256];
+  const int tid = threadIdx.x, nth = blockDim.x;
+  const int64_t cp = blockIdx.x / nchunk;
+  const int chunk = (int)(blockIdx.x - cp * nchunk);
+  const int vbeg = chunk * vc;
+  const int nv = min(vc, a.nv0 - vbeg);
+  const int c = (int)(cp % a.C);
+  const int Hs = a.Hs, Ws = a.Ws, h = a.h, w = a.w, kh = a.kh;
+  const int kh4 = round4(kh);
+  const PhiTileView tv = phi_tile_prep<S>(a, phl, cp, vbeg, nv, vc);
+  const double lmb = lambda_of(a, c);
+  const double inv_s2 = 1.0 / (double)(S * S);
+  const float2* dp = gr.dphi + cp * (int64_t)Ws * Hs;
+  float2* dk = gr.dK + cp * (int64_t)Ws * Hs;
+  double rsum = 0.0;
+  const int items = nv * h;
+  for (int it = tid; it < items; it += nth) {
+    const int v = it / h, u0 = it - v * h;
+    const bool direct = 2 * (vbeg + v) <= w;  // this class's columns were written by the column pass
+    double2 K[S][S], G[S][S], Hn[S][S];
+    double2 s1 = make_double2(0.0, 0.0);
+    double k2 = 0.0;
+#pragma unroll
+    for (int b = 0; b < S; ++b) {
+      const double2* Pvb = tv.P + (v * S + b) * kh4;
+      const double2 hv = tv.hW[v * S + b];
+      const int vb = vbeg + v + b * w;
+#pragma unroll
+      for (int aa = 0; aa < S; ++aa) {
+        const int u = u0 + aa * h;
+        K[b][aa] = dcmul(horner4(Pvb, kh4, tv.zH[u]), tv.phH[u]);
+        Hn[b][aa] = S > 1 ? dcmul(tv.hH[u], hv) : make_double2(1.0, 0.0);
+        const float2 d = direct ? dp[(int64_t)vb * Hs + u]
+                                : cconj(dp[(int64_t)(Ws - vb) * Hs + (u == 0 ? 0 : Hs - u)]);
+        G[b][aa] = make_double2((double)d.x, (double)d.y);
+        const double2 kh_ = dcmul(K[b][aa], Hn[b][aa]);
+        s1.x += kh_.x;
+        s1.y += kh_.y;
+        k2 += K[b][aa].x * K[b][aa].x + K[b][aa].y * K[b][aa].y;
+      }
+    }
+    const double D = k2 * inv_s2 + lmb, rD = 1.0 / D;
+    const double2 g = make_double2((1.0 - s1.x * inv_s2) * rD, -s1.y * inv_s2 * rD);
+    double2 P = make_double2(0.0, 0.0);
+#pragma unroll
+    for (int b = 0; b < S; ++b)
+#pragma unroll
+      for (int aa = 0; aa < S; ++aa) {
+        const double2 t = dcmul(G[b][aa], K[b][aa]);
+        P.x += t.x;
+        P.y += t.y;
+      }
+    const double rho = -(P.x * g.x + P.y * g.y) * rD;  // -Re(conj(P) g) / D
+    rsum += rho;
+    const double cP = inv_s2 * rD, cK = 2.0 * rho * inv_s2;
+#pragma unroll
+    for (int b = 0; b < S; ++b) {
+      const int vb = vbeg + v + b * w;
+#pragma unroll
+      for (int aa = 0; aa < S; ++aa) {
+        const int u = u0 + aa * h;
+        const double2 t1 = dcmul(make_double2(G[b][aa].x, -G[b][aa].y), g);
+        const double2 t2 = dcmul(P, make_double2(Hn[b][aa].x, -Hn[b][aa].y));
+        const double2 r = make_double2(t1.x - cP * t2.x + cK * K[b][aa].x, t1.y - cP * t2.y + cK * K[b][aa].y);
+        dk[(int64_t)vb * Hs + u] = make_float2((float)r.x, (float)r.y);
+      }
+    }
+  }
+  red[tid] = rsum;
+  __syncthreads();
+  for (int st = nth / 2; st > 0; st >>= 1) {
+    if (tid < st) red[tid] += red[tid + st];
+    __syncthreads();
+  }
+  if (tid == 0) gr.part[cp * nchunk + chunk] = red[0];
+}
+
+// Transposed DFT along the columns: T[cp][u][j] = sum_v dK[cp][v][u] exp(+2 pi i v (j - cw) / Ws),
+// fp64 accumulation; thread = row u, kJ taps j at a time.
+constexpr int kJ = 8;
+__global__ void __launch_bounds__(256) k_psf_grad_a(const float2* __restrict__ dK, int Hs, int Ws, int kw,
+                                                    double2* __restrict__ T) {
+  extern __shared__ double2 twW[];  // exp(+2 pi i m / Ws)
+  const int tid = threadIdx.x;
+  const int64_t cp = blockIdx.y;
+  for (int m = tid; m < Ws; m += blockDim.x) {
+    const double2 e = dexpi((double)m, (double)Ws);
+    twW[m] = make_double2(e.x, -e.y);
+  }
+  __syncthreads();
+  const int u = blockIdx.x * blockDim.x + tid;
+  if (u >= Hs) return;
+  const float2* col = dK + cp * (int64_t)Ws * Hs + u;
+  const int cw = kw / 2;
+  for (int j0 = 0; j0 < kw; j0 += kJ) {
+    double2 acc[kJ];
+    int idx[kJ], step[kJ];
+#pragma unroll
+    for (int q = 0; q < kJ; ++q) {
+      acc[q] = make_double2(0.0, 0.0);
+      idx[q] = 0;
+      const int d = (j0 + q - cw) % Ws;
+      step[q] = d < 0 ? d + Ws : d;
+    }
+    for (int v = 0; v < Ws; ++v) {
+      const float2 gf = col[(int64_t)v * Hs];
+      const double2 gd = make_double2((double)gf.x, (double)gf.y);
+#pragma unroll
+      for (int q = 0; q < kJ; ++q) {
+        const double2 e = twW[idx[q]];
+        acc[q].x = fma(gd.x, e.x, fma(-gd.y, e.y, acc[q].x));
+        acc[q].y = fma(gd.x, e.y, fma(gd.y, e.x, acc[q].y));
+        idx[q] += step[q];
+        if (idx[q] >= Ws) idx[q] -= Ws;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kJ; ++q)
+      if (j0 + q < kw) T[(cp * Hs + u) * kw + j0 + q] = acc[q];
+  }
+}
+
+// Second pass, one block per channel: dpsf[cp][i][j] = Re sum_u T[cp][u][j] exp(+2 pi i u (i - ch) / Hs)
+// for every psf plane cp of channel c, and dbias[c] = sum of the lambda gradient x sigmoid'(bias - 9).
+__global__ void __launch_bounds__(256) k_psf_grad_b(const double2* __restrict__ T, const double* __restrict__ part,
+                                                    int nchunk, int64_t C, int64_t psf_batch, int Hs, int kh, int kw,
+                                                    const float* __restrict__ bias, float* __restrict__ dpsf,
+                                                    float* __restrict__ dbias) {
+  extern __shared__ double2 twH[];  // exp(+2 pi i m / Hs)
+  __shared__ double red[256];
+  const int tid = threadIdx.x, nth = blockDim.x;
+  const int64_t c = blockIdx.x;
+  for (int m = tid; m < Hs; m += nth) {
+    const double2 e = dexpi((double)m, (double)Hs);
+    twH[m] = make_double2(e.x, -e.y);
+  }
+  __syncthreads();
+  const int ch = kh / 2;
+  double lsum = 0.0;
+  for (int64_t pb = 0; pb < psf_batch; ++pb) {
+    const int64_t cp = pb * C + c;
+    if (dpsf) {
+      for (int e = tid; e < kh * kw; e += nth) {
+        const int i = e / kw, j = e - i * kw;
+        int d = (i - ch) % Hs;
+        if (d < 0) d += Hs;
+        int idx = 0;
+        double acc = 0.0;
+        const double2* Tc = T + cp * (int64_t)Hs * kw + j;
+        for (int u = 0; u < Hs; ++u) {
+          const double2 t = Tc[(int64_t)u * kw], e2 = twH[idx];
+          acc = fma(t.x, e2.x, fma(-t.y, e2.y, acc));
+          idx += d;
+          if (idx >= Hs) idx -= Hs;
+        }
+        dpsf[cp * kh * kw + e] = (float)acc;
+      }
+    }
+    for (int k = tid; k < nchunk; k += nth) lsum += part[cp * nchunk + k];
+  }
+  red[tid] = lsum;
+  __syncthreads();
+  for (int st = nth / 2; st > 0; st >>= 1) {
+    if (tid < st) red[tid] += red[tid + st];
+    __syncthreads();
+  }
+  if (tid == 0 && dbias) {
+    const double sg = 1.0 / (1.0 + exp(-((double)bias[c] - 9.0)));
+    dbias[c] = (float)(red[0] * sg * (1.0 - sg));
+  }
+}
+
+// ================================================================================================
 // host side
 // ================================================================================================
 namespace {
@@ -688,6 +1026,13 @@ void set_lds_attrs() {
   hipFuncSetAttribute((const void*)k_cols_module, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
   hipFuncSetAttribute((const void*)k_cols_op, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
   hipFuncSetAttribute((const void*)k_rows_inv, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+  hipFuncSetAttribute((const void*)k_cols_bwd, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+  hipFuncSetAttribute((const void*)k_phi_grad<1>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+  hipFuncSetAttribute((const void*)k_phi_grad<2>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+  hipFuncSetAttribute((const void*)k_phi_grad<3>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+  hipFuncSetAttribute((const void*)k_phi_grad<4>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+  hipFuncSetAttribute((const void*)k_psf_grad_a, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+  hipFuncSetAttribute((const void*)k_psf_grad_b, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
   hipGetLastError();
   g_attr_done = true;
 }
@@ -906,6 +1251,32 @@ int check_mode_act(int64_t H, int64_t W, int pad, int pad_mode, int act) {
   return CVN_OK;
 }
 
+// ---- backward workspace: plan tables, module table, HR grad spectra (later dy), LR spectra / dS,
+// and for weight gradients dPhi, dK, the column-transposed DFT T and the per-block lambda sums.
+struct BwdWs {
+  size_t tabs, phi, Sg, Sx, dphi, dK, T, part, total;
+  int vc, nchunk, lds;
+};
+constexpr int kGradLds = 64 * 1024;
+void bwd_layout(const Geo& g, const PlanTabs& t, BwdWs* w) {
+  size_t o = 0;
+  w->tabs = o; o += align_up(t.bytes);
+  w->phi = o; o += align_up((size_t)g.Cp * g.NCs * g.Hs * sizeof(float2));
+  w->Sg = o; o += align_up((size_t)g.P * g.NCs * g.Hs * sizeof(float2));  // >= P h w floats (dy)
+  w->Sx = o; o += align_up((size_t)g.P * g.NC * g.h * sizeof(float2));
+  // weight-gradient chunks over all w column classes, as in launch_phi
+  w->nchunk = (int)std::min<int64_t>(g.w, std::max<int64_t>(1, (2048 + g.Cp - 1) / g.Cp));
+  w->vc = (g.w + w->nchunk - 1) / w->nchunk;
+  while (w->vc > 1 && phi_tile_lds(g.s, g.Hs, g.kh, g.kw, w->vc).total > kGradLds) --w->vc;
+  w->lds = phi_tile_lds(g.s, g.Hs, g.kh, g.kw, w->vc).total;
+  w->nchunk = (g.w + w->vc - 1) / w->vc;
+  w->dphi = o; o += align_up((size_t)g.Cp * g.Ws * g.Hs * sizeof(float2));
+  w->dK = o; o += align_up((size_t)g.Cp * g.Ws * g.Hs * sizeof(float2));
+  w->T = o; o += align_up((size_t)g.Cp * g.Hs * g.kw * sizeof(double2));
+  w->part = o; o += align_up((size_t)g.Cp * w->nchunk * sizeof(double));
+  w->total = o;
+}
+
 }  // namespace
 
 extern "C" size_t cvn_converse2d_table_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, int kh,
@@ -1087,4 +1458,120 @@ extern "C" int cvn_converse2d_op_f32(const float* x, const float* x0, int64_t B,
   hipLaunchKernelGGL(k_cols_op, dim3(g.w, (unsigned)g.P), dim3(kThreads), lds, st, ca);
   if ((rc = check_launch("op column pass")) != CVN_OK) return rc;
   return launch_rows_inv(SH, g, 0, g.Hs, 0, g.Ws, CVN_ACT_NONE, tabs + t.off[kTabWs], out, st);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Backward of the module path (Converse2D.forward, util_converse.py:142-192, differentiated as the
+// reference's CompositeImplicitAutograd registration does, converse2d.cpp:223-227).
+// ------------------------------------------------------------------------------------------------
+extern "C" size_t cvn_converse2d_bwd_workspace(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch,
+                                               int kh, int kw, int scale, int pad) {
+  Geo g;
+  if (module_geo(B, C, H, W, psf_batch, kh, kw, scale, pad, &g) != CVN_OK) return 0;
+  PlanTabs t;
+  if (!plan_tabs(g, &t)) return 0;
+  BwdWs w;
+  bwd_layout(g, t, &w);
+  return w.total;
+}
+
+extern "C" int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int64_t B, int64_t C, int64_t H,
+                                      int64_t W, const float* psf, int64_t psf_batch, int kh, int kw,
+                                      const float* bias, float eps, int scale, int pad, int pad_mode, float* grad_x,
+                                      float* grad_psf, float* grad_bias, void* workspace, size_t workspace_bytes,
+                                      cvn_stream_t stream) {
+  Geo g;
+  int rc = module_geo(B, C, H, W, psf_batch, kh, kw, scale, pad, &g);
+  if (rc != CVN_OK) return rc;
+  if ((rc = check_mode_act(H, W, pad, pad_mode, CVN_ACT_NONE)) != CVN_OK) return rc;
+  const bool wg = grad_psf || grad_bias;
+  if (!grad_out || !psf || !bias || (wg && !x)) return fail(CVN_ERR_ARG, "null pointer");
+  if (!grad_x && !wg) return CVN_OK;
+  if (B == 0) return CVN_OK;
+  if (g.P > 65535) return fail(CVN_ERR_UNSUPPORTED, "B*C = %lld planes exceeds 65535", (long long)g.P);
+  if (wg && g.s > 4) return fail(CVN_ERR_UNSUPPORTED, "weight gradients support scale <= 4");
+  if (pad_mode == CVN_PAD_REPLICATE && pad > 15)
+    return fail(CVN_ERR_UNSUPPORTED, "replicate padding above 15 in the backward");
+  PlanTabs t;
+  if (!plan_tabs(g, &t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
+  BwdWs ws;
+  bwd_layout(g, t, &ws);
+  if (!workspace || workspace_bytes < ws.total)
+    return fail(CVN_ERR_WORKSPACE, "workspace too small: need %zu bytes", ws.total);
+  if (wg && ws.lds > kGradLds) return fail(CVN_ERR_UNSUPPORTED, "plane too large for the weight gradient");
+  hipStream_t st = (hipStream_t)stream;
+  set_lds_attrs();
+  char* base = (char*)workspace;
+  const char* tabs = base + ws.tabs;
+  float2* phi = (float2*)(base + ws.phi);
+  float2* Sg = (float2*)(base + ws.Sg);
+  float2* Sx = (float2*)(base + ws.Sx);
+  if ((rc = launch_plan_tabs(t, base + ws.tabs, st)) != CVN_OK) return rc;
+  if ((rc = launch_phi(psf, bias, eps, g, false, phi, nullptr, st)) != CVN_OK) return rc;
+  // row spectra of uncrop(grad_out) on the HR grid, and of pad(x) for the weight gradients
+  if ((rc = launch_rows_fwd(grad_out, g.P, g.H * g.s, g.W * g.s, g.pad * g.s, CVN_PAD_ZEROS, g.Hs, g.Ws,
+                            tabs + t.off[kTabWs], Sg, st)) != CVN_OK)
+    return rc;
+  if (wg && (rc = launch_rows_fwd(x, g.P, g.H, g.W, g.pad, pad_mode, g.h, g.w, tabs + t.off[kTabW], Sx, st)) !=
+                CVN_OK)
+    return rc;
+  // column pass: dS (in place over Sx) and dPhi
+  {
+    ColBwdArgs a;
+    a.Sg = Sg; a.Sx = Sx; a.phi = phi; a.dphi = wg ? (float2*)(base + ws.dphi) : nullptr;
+    a.B = g.B; a.C = g.C; a.psf_batch = g.Cp / g.C;
+    a.h = g.h; a.w = g.w; a.s = g.s; a.Hs = g.Hs; a.Ws = g.Ws; a.NC = g.NC; a.NCs = g.NCs;
+    a.plan_h = t.plan[kTabH]; a.plan_H = t.plan[kTabHs];
+    a.tabs_h = tabs + t.off[kTabH]; a.tabs_H = tabs + t.off[kTabHs];
+    a.rad_off = (int)align_up(cols_bwd_lds(g.h, g.Hs, g.s, wg), 16);
+    const size_t lds = a.rad_off + rader_lds_bytes(a.plan_h) + rader_lds_bytes(a.plan_H);
+    if (lds > kLdsLimit) return fail(CVN_ERR_UNSUPPORTED, "plane too large for the backward column pass");
+    const dim3 grid((unsigned)g.NC, (unsigned)(a.psf_batch == 1 ? g.C : g.P));
+    hipLaunchKernelGGL(k_cols_bwd, grid, dim3(kThreads), lds, st, a);
+    if ((rc = check_launch("backward column pass")) != CVN_OK) return rc;
+  }
+  // dy = C2R rows of dS (LR grid, uncropped), then the padding adjoint
+  if (grad_x) {
+    Geo gl = g;
+    gl.Hs = g.h; gl.Ws = g.w; gl.NCs = g.NC;
+    float* dy = (float*)(base + ws.Sg);
+    if ((rc = launch_rows_inv(Sx, gl, 0, g.h, 0, g.w, CVN_ACT_NONE, tabs + t.off[kTabW], dy, st)) != CVN_OK) return rc;
+    const int64_t n = g.P * g.H * g.W;
+    hipLaunchKernelGGL(k_pad_adj, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, dy, g.P, g.H, g.W, g.pad,
+                       pad_mode, grad_x);
+    if ((rc = check_launch("padding adjoint")) != CVN_OK) return rc;
+  }
+  if (!wg) return CVN_OK;
+  {
+    PhiArgs a;
+    a.psf = psf; a.bias = bias; a.Cp = g.Cp; a.C = (int)g.C; a.kh = g.kh; a.kw = g.kw; a.s = g.s;
+    a.h = g.h; a.w = g.w; a.Hs = g.Hs; a.Ws = g.Ws; a.NCs = g.NCs; a.eps = (double)eps;
+    a.phi = nullptr; a.kf = nullptr;
+    a.nv0 = g.w;
+    PhiGradArgs gr;
+    gr.dphi = (const float2*)(base + ws.dphi);
+    gr.dK = (float2*)(base + ws.dK);
+    gr.part = (double*)(base + ws.part);
+    if (g.Cp * ws.nchunk > 0x7fffffff) return fail(CVN_ERR_UNSUPPORTED, "too many gradient blocks");
+    const dim3 grid((unsigned)(g.Cp * ws.nchunk));
+    switch (g.s) {
+      case 1: hipLaunchKernelGGL(k_phi_grad<1>, grid, dim3(kThreads), (size_t)ws.lds, st, a, gr, ws.vc, ws.nchunk); break;
+      case 2: hipLaunchKernelGGL(k_phi_grad<2>, grid, dim3(kThreads), (size_t)ws.lds, st, a, gr, ws.vc, ws.nchunk); break;
+      case 3: hipLaunchKernelGGL(k_phi_grad<3>, grid, dim3(kThreads), (size_t)ws.lds, st, a, gr, ws.vc, ws.nchunk); break;
+      default: hipLaunchKernelGGL(k_phi_grad<4>, grid, dim3(kThreads), (size_t)ws.lds, st, a, gr, ws.vc, ws.nchunk); break;
+    }
+    if ((rc = check_launch("transfer-function gradient")) != CVN_OK) return rc;
+  }
+  double2* T = (double2*)(base + ws.T);
+  if (grad_psf) {
+    const dim3 grid((unsigned)((g.Hs + 255) / 256), (unsigned)g.Cp);
+    if (g.Cp > 65535) return fail(CVN_ERR_UNSUPPORTED, "too many psf planes");
+    hipLaunchKernelGGL(k_psf_grad_a, grid, dim3(256), (size_t)g.Ws * sizeof(double2), st,
+                       (const float2*)(base + ws.dK), g.Hs, g.Ws, g.kw, T);
+    if ((rc = check_launch("psf gradient (columns)")) != CVN_OK) return rc;
+  }
+  hipLaunchKernelGGL(k_psf_grad_b, dim3((unsigned)g.C), dim3(256), (size_t)g.Hs * sizeof(double2), st, T,
+                     (const double*)(base + ws.part), ws.nchunk, g.C, g.Cp / g.C, g.Hs, g.kh, g.kw, bias, grad_psf,
+                     grad_bias);
+  return check_launch("psf / bias gradient");
 }

@@ -142,6 +142,72 @@ def converse2d_fused(x, weight, bias, scale=1, padding=2, padding_mode="circular
     return out
 
 
+def converse2d_backward(grad_out, x, weight, bias, scale=1, padding=2, padding_mode="circular", eps=1e-5,
+                        need_x=True, need_weight=True, need_bias=True):
+    """Gradients of Converse2D.forward (util_converse.py:142-192) in one library call: returns
+    (grad_x, grad_weight, grad_bias), None where not requested.  grad_out (B,C,H*s,W*s); weight
+    (1 or B, C, kh, kw); bias (1,C,1,1) or (C,)."""
+    lib = _lib.load()
+    _need_hip(grad_out, x, weight, bias)
+    B, C, H, W = x.shape
+    s, p = int(scale), int(padding)
+    if tuple(grad_out.shape) != (B, C, H * s, W * s):
+        raise RuntimeError("grad_out must be (B,C,H*scale,W*scale)")
+    if weight.dim() != 4 or weight.shape[1] != C or weight.shape[0] not in (1, B):
+        raise RuntimeError("weight must be (1,C,kh,kw) or (B,C,kh,kw)")
+    if padding_mode not in _lib.PAD_MODES:
+        raise ValueError(f"unknown padding_mode {padding_mode!r}")
+    kh, kw = int(weight.shape[2]), int(weight.shape[3])
+    pb = int(weight.shape[0])
+    dev = x.device
+    go = grad_out.contiguous()
+    xc = x.contiguous()
+    wc = weight.contiguous()
+    bc = bias.contiguous()
+    gx = torch.empty((B, C, H, W), dtype=torch.float32, device=dev) if need_x else None
+    gw = torch.empty((pb, C, kh, kw), dtype=torch.float32, device=dev) if need_weight else None
+    gb = torch.empty((C,), dtype=torch.float32, device=dev) if need_bias else None
+    if B == 0 or not (need_x or need_weight or need_bias):
+        for t in (gw, gb):
+            if t is not None:
+                t.zero_()
+        return gx, gw, gb.reshape(bias.shape) if gb is not None else None
+    nb = lib.cvn_converse2d_bwd_workspace(B, C, H, W, pb, kh, kw, s, p)
+    if nb == 0:
+        _lib.check(_lib.CVN_ERR_ARG, "converse2d_backward")
+    ws = _workspace(dev, nb)
+    ptr = lambda t: t.data_ptr() if t is not None else None  # noqa: E731
+    rc = lib.cvn_converse2d_bwd_f32(go.data_ptr(), xc.data_ptr(), B, C, H, W, wc.data_ptr(), pb, kh, kw,
+                                    bc.data_ptr(), float(eps), s, p, _lib.PAD_MODES[padding_mode], ptr(gx), ptr(gw),
+                                    ptr(gb), ws.data_ptr(), nb, _stream(dev))
+    _lib.check(rc, "converse2d_backward")
+    return gx, gw, gb.reshape(bias.shape) if gb is not None else None
+
+
+class Converse2DFunction(torch.autograd.Function):
+    """Converse2D.forward with the library's forward and backward kernels (the reference gets its
+    gradients from autograd through the composite op, converse2d.cpp:223-227)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, scale, padding, padding_mode, eps):
+        ctx.save_for_backward(x, weight, bias)
+        ctx.cfg = (scale, padding, padding_mode, eps)
+        return converse2d_fused(x, weight, bias.reshape(-1), scale, padding, padding_mode, eps, cache=True)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, weight, bias = ctx.saved_tensors
+        s, p, mode, eps = ctx.cfg
+        nx, nw, nb = ctx.needs_input_grad[:3]
+        gx, gw, gb = converse2d_backward(grad_out, x, weight, bias, s, p, mode, eps, nx, nw, nb)
+        return gx, gw, gb, None, None, None, None
+
+
+def converse2d_train(x, weight, bias, scale=1, padding=2, padding_mode="circular", eps=1e-5):
+    """Differentiable Converse2D forward on the HIP kernels (forward and backward)."""
+    return Converse2DFunction.apply(x, weight, bias, scale, padding, padding_mode, eps)
+
+
 def converse2d_op(x, x0, weight, bias, scale, eps=1e-5):
     """The reference op (converse2d.cpp:165-209): x padded (B,C,h,w), x0 (B,C,h*s,w*s) arbitrary;
     returns the uncropped (B,C,h*s,w*s) solution."""

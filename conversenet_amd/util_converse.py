@@ -11,7 +11,9 @@ Dispatch (mirrors the reference's backend selection, util_converse.py:150-169):
   * backend "cuda": requires the HIP library and a HIP tensor (RuntimeError otherwise, as :156-158).
   * backend "pytorch": always the PyTorch composition.
   * $CONVERSE2D_BACKEND overrides the module's backend (:150).
-The HIP kernels are forward-only; a forward that autograd must differentiate runs the composition.
+A forward that autograd must differentiate runs the library's forward and backward kernels
+(functional.Converse2DFunction) where the backward supports the configuration, and the composition
+otherwise; the LayerNorm / 1x1 kernels are forward-only (the composition runs under autograd).
 """
 from __future__ import annotations
 
@@ -49,6 +51,24 @@ def _hip_eligible(*ts) -> bool:
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts):
         return False
     _lib.load()  # ImportError when libcvn_hip.so is not built
+    return True
+
+
+def _hip_grad_eligible(x, weight, bias, scale, padding, padding_mode) -> bool:
+    """True when a forward that autograd must differentiate can run on the library's forward and
+    backward kernels (fp32 HIP tensors, a configuration the backward supports)."""
+    ts = (x, weight, bias)
+    if not all(t.is_cuda and t.dtype == torch.float32 for t in ts):
+        return False
+    if not (torch.is_grad_enabled() and any(t.requires_grad for t in ts)):
+        return False
+    if (weight.requires_grad or bias.requires_grad) and int(scale) > 4:
+        return False
+    if padding_mode == "replicate" and int(padding) > 15:
+        return False
+    if x.dim() != 4 or x.shape[0] * x.shape[1] > 65535:
+        return False
+    _lib.load()
     return True
 
 
@@ -158,12 +178,22 @@ class Converse2D(nn.Module):
     def biaseps(self, v):
         self.__dict__["_biaseps"] = v
 
+    def _use_hip_grad(self, x) -> bool:
+        if _backend(self.backend) == "pytorch":
+            return False
+        return _hip_grad_eligible(x, self.weight, self.bias, self.scale, self.padding, self.padding_mode)
+
     def forward(self, x, act=None):
         """act='gelu' applies exact GELU to the output (fused on store on the HIP path)."""
         if self._use_hip(x):
             self.biaseps = None  # read lazily from the current bias
             return functional.converse2d_fused(x, self.weight, self.bias.reshape(-1), self.scale, self.padding,
                                                self.padding_mode, self.eps, act)
+        if self._use_hip_grad(x):
+            self.biaseps = None
+            out = functional.converse2d_train(x, self.weight, self.bias, self.scale, self.padding, self.padding_mode,
+                                              self.eps)
+            return F.gelu(out) if act == "gelu" else out
         self.biaseps = torch.sigmoid(self.bias - 9.0) + self.eps
         out = composite.converse2d_module(x, self.weight, self.bias, self.scale, self.padding, self.padding_mode,
                                           self.eps)

@@ -81,6 +81,20 @@ int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, int64_t H, in
                              int act, const void* table, void* scratch, size_t scratch_bytes,
                              float* out, cvn_stream_t stream);
 
+/* Backward of the module-level forward (act = none), the gradients the reference obtains by autograd
+ * through Converse2D.forward (util_converse.py:142-192; its op is registered
+ * CompositeImplicitAutograd, converse2d.cpp:223-227; gradient checks in test/test_error.py:51-54).
+ * grad_out: (B,C,H*scale,W*scale).  Outputs (each may be null when not wanted): grad_x (B,C,H,W),
+ * grad_psf (psf_batch,C,kh,kw), grad_bias (C).  x is read only for grad_psf / grad_bias.  Weight
+ * gradients support scale <= 4; replicate padding up to 15. */
+size_t cvn_converse2d_bwd_workspace(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch,
+                                    int kh, int kw, int scale, int pad);
+int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int64_t B, int64_t C, int64_t H,
+                           int64_t W, const float* psf, int64_t psf_batch, int kh, int kw,
+                           const float* bias, float eps, int scale, int pad, int pad_mode,
+                           float* grad_x, float* grad_psf, float* grad_bias, void* workspace,
+                           size_t workspace_bytes, cvn_stream_t stream);
+
 /* Op-level forward with the reference op's semantics: x (B,C,h,w) is the already padded input,
  * x0 (B,C,h*scale,w*scale) is arbitrary, psf (1,C,kh,kw), bias (C).  out: (B,C,h*scale,w*scale),
  * uncropped. */
