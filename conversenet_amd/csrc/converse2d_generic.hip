@@ -702,38 +702,43 @@ __global__ void __launch_bounds__(256) k_rows_inv(RowInvArgs a) {
 // CompositeImplicitAutograd, converse2d.cpp:223-227).
 // ================================================================================================
 
-// Column pass: one block per (LR column class v0 in [0, NC), psf group); the block loops over the
-// planes that share the group's psf (psf_batch 1: the B planes of channel c; otherwise one plane).
+// Column pass: one block per (cpb consecutive LR column classes v0 in [0, NC), psf group); the block
+// loops over the planes that share the group's psf (psf_batch 1: the B planes of channel c;
+// otherwise one plane).  Per plane: forward HR column FFTs of the classes' members (dZ), forward LR
+// column FFTs of pad(x) (Y, weight gradients only), dY = alias sum of conj(Phi') dZ, inverse LR
+// column FFTs -> dS; dPhi accumulates in LDS over the planes.
 struct ColBwdArgs {
   const float2* Sg;   // (P, NCs, Hs) row spectra of uncrop(grad_out)
   float2* Sx;         // (P, NC, h)   row spectra of pad(x) in (weight gradients), dS out (in place)
   const float2* phi;  // (Cp, NCs, Hs) module table Phi'
   float2* dphi;       // (Cp, Ws, Hs) or null: columns of the processed classes
   int64_t B, C, psf_batch;
-  int h, w, s, Hs, Ws, NC, NCs;
+  int h, w, s, Hs, Ws, NC, NCs, cpb;
   FftPlan plan_h, plan_H;
   const char *tabs_h, *tabs_H;
   int rad_off;
 };
 
-__host__ __device__ inline size_t cols_bwd_lds(int h, int Hs, int s, bool wg) {
-  return (size_t)(h + Hs + 3 * h + 2 * s * Hs + (wg ? s * Hs : 0)) * sizeof(float2);
+__host__ __device__ inline size_t cols_bwd_lds(int h, int Hs, int s, int cpb, bool wg) {
+  return (size_t)(h + Hs + 3 * cpb * h + 2 * cpb * s * Hs + (wg ? cpb * s * Hs : 0)) * sizeof(float2);
 }
 
 __global__ void __launch_bounds__(256) k_cols_bwd(ColBwdArgs a) {
   extern __shared__ float2 sm[];
   const int tid = threadIdx.x, nth = blockDim.x;
   const bool wg = a.dphi != nullptr;
+  const int cpb = a.cpb, sH = a.s * a.Hs;
   float2* twh = sm;
   float2* twH = twh + a.h;
-  float2* Ya = twH + a.Hs;         // h: Y (pad x, LR column spectrum)
-  float2* Yb = Ya + a.h;           // h
-  float2* Yc = Yb + a.h;           // h: dY
-  float2* Xa = Yc + a.h;           // s Hs: dZ
-  float2* Xb = Xa + a.s * a.Hs;    // s Hs
-  float2* acc = Xb + a.s * a.Hs;   // s Hs: dPhi (weight gradients only)
-  const int v0 = blockIdx.x;
-  const int64_t grp = blockIdx.y;  // psf plane: c (psf_batch 1) or the plane (psf_batch B)
+  float2* Ya = twH + a.Hs;           // cpb h: Y (LR column spectra of pad x)
+  float2* Yb = Ya + cpb * a.h;       // cpb h
+  float2* Yc = Yb + cpb * a.h;       // cpb h: dY
+  float2* Xa = Yc + cpb * a.h;       // cpb s Hs: dZ
+  float2* Xb = Xa + cpb * sH;        // cpb s Hs
+  float2* acc = Xb + cpb * sH;       // cpb s Hs: dPhi (weight gradients only)
+  const int vbase = blockIdx.x * cpb;
+  const int ncol = min(cpb, a.NC - vbase);
+  const int64_t grp = blockIdx.y;    // psf plane: c (psf_batch 1) or the plane (psf_batch B)
   char* radh = (char*)sm + a.rad_off;
   char* radH = radh + rader_lds_bytes(a.plan_h);
   load_plan_tabs(a.plan_h, a.tabs_h, twh, radh, tid, nth);
@@ -741,90 +746,143 @@ __global__ void __launch_bounds__(256) k_cols_bwd(ColBwdArgs a) {
   else radH = radh;
   const float2* tH = (a.Hs != a.h) ? twH : twh;
   const float2* ph = a.phi + grp * (int64_t)a.NCs * a.Hs;
-  const FastDiv fHs = fast_div(a.Hs), fh = fast_div(a.h);
+  const FastDiv fHs = fast_div(a.Hs), fh = fast_div(a.h), fsH = fast_div(sH);
   const float norm = 1.0f / ((float)a.Hs * (float)a.Ws);
   if (wg)
-    for (int i = tid; i < a.s * a.Hs; i += nth) acc[i] = make_float2(0.f, 0.f);
+    for (int i = tid; i < cpb * sH; i += nth) acc[i] = make_float2(0.f, 0.f);
   const int64_t nplanes = (a.psf_batch == 1) ? a.B : 1;
   for (int64_t ib = 0; ib < nplanes; ++ib) {
     const int64_t plane = (a.psf_batch == 1) ? ib * a.C + grp : grp;
     const float2* Sgp = a.Sg + plane * (int64_t)a.NCs * a.Hs;
     float2* Sxp = a.Sx + plane * (int64_t)a.NC * a.h;
     __syncthreads();  // the previous plane's LDS reads are done
-    for (int idx = tid; idx < a.s * a.Hs; idx += nth) {
-      const int b = idx / fHs, u = idx - b * a.Hs;
-      const int vb = v0 + b * a.w;
-      // row spectra of real rows are Hermitian in the column index
-      Xa[idx] = vb <= a.Ws / 2 ? Sgp[(int64_t)vb * a.Hs + u] : cconj(Sgp[(int64_t)(a.Ws - vb) * a.Hs + u]);
+    // member columns vb = v0 + b w of each class (row spectra of real rows are Hermitian in the column)
+    for (int i0 = tid; i0 < cpb * sH; i0 += kBatch * nth) {
+      float2 val[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const int idx = i0 + k * nth;
+        val[k] = make_float2(0.f, 0.f);
+        if (idx < cpb * sH) {
+          const int cl = idx / fsH, r = idx - cl * sH;
+          const int b = r / fHs, u = r - b * a.Hs;
+          if (cl < ncol) {
+            const int vb = vbase + cl + b * a.w;
+            val[k] = vb <= a.Ws / 2 ? Sgp[(int64_t)vb * a.Hs + u] : cconj(Sgp[(int64_t)(a.Ws - vb) * a.Hs + u]);
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const int idx = i0 + k * nth;
+        if (idx < cpb * sH) Xa[idx] = val[k];
+      }
     }
-    if (wg)
-      for (int u = tid; u < a.h; u += nth) Ya[u] = Sxp[(int64_t)v0 * a.h + u];
-    __syncthreads();
-    const float2* dZ = fft_lds<false>(a.plan_H, Xa, Xb, a.s, tH, tid, nth, radH);
     if (wg) {
-      const float2* Y = fft_lds<false>(a.plan_h, Ya, Yb, 1, twh, tid, nth, radh);
-      for (int idx = tid; idx < a.s * a.Hs; idx += nth) {
-        const int u = idx - (idx / fHs) * a.Hs;
-        const float2 t = cmul(cconj(Y[u - (u / fh) * a.h]), dZ[idx]);
+      for (int i0 = tid; i0 < cpb * a.h; i0 += kBatch * nth) {
+        float2 val[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          const int idx = i0 + k * nth;
+          val[k] = make_float2(0.f, 0.f);
+          if (idx < ncol * a.h) val[k] = Sxp[(int64_t)vbase * a.h + idx];  // columns vbase.. are contiguous
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          const int idx = i0 + k * nth;
+          if (idx < cpb * a.h) Ya[idx] = val[k];
+        }
+      }
+    }
+    __syncthreads();
+    const float2* dZ = fft_lds<false>(a.plan_H, Xa, Xb, cpb * a.s, tH, tid, nth, radH);
+    if (wg) {
+      const float2* Y = fft_lds<false>(a.plan_h, Ya, Yb, cpb, twh, tid, nth, radh);
+      for (int idx = tid; idx < cpb * sH; idx += nth) {
+        const int cl = idx / fsH, r = idx - cl * sH;
+        const int u = r - (r / fHs) * a.Hs;
+        const float2 t = cmul(cconj(Y[cl * a.h + u - (u / fh) * a.h]), dZ[idx]);
         acc[idx].x = fmaf(t.x, norm, acc[idx].x);
         acc[idx].y = fmaf(t.y, norm, acc[idx].y);
       }
     }
-    for (int u0 = tid; u0 < a.h; u0 += nth) {
+    for (int idx = tid; idx < cpb * a.h; idx += nth) {
+      const int cl = idx / fh, u0 = idx - cl * a.h;
       float2 m = make_float2(0.f, 0.f);
-      for (int b = 0; b < a.s; ++b) {
-        const int vb = v0 + b * a.w;
-        for (int aa = 0; aa < a.s; ++aa) {
-          const int u = u0 + aa * a.h;
-          const float2 f = vb <= a.Ws / 2 ? ph[(int64_t)vb * a.Hs + u]
-                                          : cconj(ph[(int64_t)(a.Ws - vb) * a.Hs + (u == 0 ? 0 : a.Hs - u)]);
-          const float2 t = cmul(cconj(f), dZ[b * a.Hs + u]);
-          m.x += t.x;
-          m.y += t.y;
+      if (cl < ncol) {
+        for (int b = 0; b < a.s; ++b) {
+          const int vb = vbase + cl + b * a.w;
+          for (int aa = 0; aa < a.s; ++aa) {
+            const int u = u0 + aa * a.h;
+            const float2 f = vb <= a.Ws / 2 ? ph[(int64_t)vb * a.Hs + u]
+                                            : cconj(ph[(int64_t)(a.Ws - vb) * a.Hs + (u == 0 ? 0 : a.Hs - u)]);
+            const float2 t = cmul(cconj(f), dZ[cl * sH + b * a.Hs + u]);
+            m.x += t.x;
+            m.y += t.y;
+          }
         }
       }
-      Yc[u0] = m;
+      Yc[idx] = m;
     }
     __syncthreads();
-    const float2* R = fft_lds<true>(a.plan_h, Yc, (Yc == Ya) ? Yb : Ya, 1, twh, tid, nth, radh);
-    for (int r = tid; r < a.h; r += nth) Sxp[(int64_t)v0 * a.h + r] = R[r];
+    const float2* R = fft_lds<true>(a.plan_h, Yc, Ya, cpb, twh, tid, nth, radh);
+    for (int idx = tid; idx < ncol * a.h; idx += nth) Sxp[(int64_t)vbase * a.h + idx] = R[idx];
   }
   if (wg) {
     __syncthreads();
     float2* dp = a.dphi + grp * (int64_t)a.Ws * a.Hs;
-    for (int idx = tid; idx < a.s * a.Hs; idx += nth) {
-      const int b = idx / fHs, u = idx - b * a.Hs;
-      dp[(int64_t)(v0 + b * a.w) * a.Hs + u] = acc[idx];
+    for (int idx = tid; idx < ncol * sH; idx += nth) {
+      const int cl = idx / fsH, r = idx - cl * sH;
+      const int b = r / fHs, u = r - b * a.Hs;
+      dp[(int64_t)(vbase + cl + b * a.w) * a.Hs + u] = acc[idx];
     }
   }
 }
 
 // Adjoint of the padding: dx[i][j] = sum of dy over the padded samples that copy source (i, j).
-__global__ void __launch_bounds__(256) k_pad_adj(const float* __restrict__ dy, int64_t P, int H, int W, int pad,
-                                                 int mode, float* __restrict__ dx) {
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= P * H * W) return;
-  const int64_t plane = e / ((int64_t)H * W);
-  const int rem = (int)(e - plane * H * W);
-  const int i = rem / W, j = rem - (rem / W) * W;
-  const int h = H + 2 * pad, w = W + 2 * pad;
-  int rows[16], cols[16];
-  int nr = 0, nc = 0;
-  rows[nr++] = i + pad;
-  cols[nc++] = j + pad;
-  for (int q = 0; q < 2 * pad && nr < 16; ++q) {  // border rows / columns: [0, pad) and [H + pad, h)
-    const int r = q < pad ? q : H + q;
-    if (pad_src(r, H, pad, mode) == i) rows[nr++] = r;
+// Grid (ceil(W / 256), ceil(H / kPadRows), planes).  Only samples within pad + 1 of an edge receive
+// border terms (in every mode); for those the 2 pad border rows / columns are scanned for the ones
+// whose padding source is i / j (no local arrays: runtime-indexed ones would live in scratch memory).
+__device__ __forceinline__ int border_idx(int q, int n, int pad) { return q < pad ? q : n + q; }
+
+constexpr int kPadRows = 8;  // rows per thread in k_pad_adj
+__global__ void __launch_bounds__(256) k_pad_adj(const float* __restrict__ dy, int H, int W, int pad, int mode,
+                                                 float* __restrict__ dx) {
+  extern __shared__ int psrc[];  // padding source of border row q: psrc[q]; of border column q: psrc[2 pad + q]
+  const int nb = (mode == CVN_PAD_ZEROS) ? 0 : 2 * pad;
+  for (int q = threadIdx.x; q < nb; q += blockDim.x) {
+    psrc[q] = pad_src(border_idx(q, H, pad), H, pad, mode);
+    psrc[nb + q] = pad_src(border_idx(q, W, pad), W, pad, mode);
   }
-  for (int q = 0; q < 2 * pad && nc < 16; ++q) {
-    const int c = q < pad ? q : W + q;
-    if (pad_src(c, W, pad, mode) == j) cols[nc++] = c;
+  __syncthreads();
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= W) return;
+  const int i0 = blockIdx.y * kPadRows;
+  const int64_t plane = blockIdx.z;
+  const int w = W + 2 * pad;
+  const float* p = dy + plane * (int64_t)(H + 2 * pad) * w;
+  float v[kPadRows];
+#pragma unroll
+  for (int k = 0; k < kPadRows; ++k) v[k] = (i0 + k < H) ? p[(int64_t)(i0 + k + pad) * w + j + pad] : 0.f;
+  const int nc = (nb > 0 && (j <= pad || j >= W - 1 - pad)) ? nb : 0;
+#pragma unroll
+  for (int k = 0; k < kPadRows; ++k) {
+    const int i = i0 + k;
+    if (i >= H) break;
+    float acc = v[k];
+    for (int qb = 0; qb < nc; ++qb)  // border columns of the interior row
+      if (psrc[nb + qb] == j) acc += p[(int64_t)(i + pad) * w + border_idx(qb, W, pad)];
+    if (nb > 0 && (i <= pad || i >= H - 1 - pad)) {
+      for (int qa = 0; qa < nb; ++qa) {  // border rows whose padding source is row i
+        if (psrc[qa] != i) continue;
+        const float* row = p + (int64_t)border_idx(qa, H, pad) * w;
+        acc += row[j + pad];
+        for (int qb = 0; qb < nc; ++qb)
+          if (psrc[nb + qb] == j) acc += row[border_idx(qb, W, pad)];
+      }
+    }
+    dx[(plane * H + i) * (int64_t)W + j] = acc;
   }
-  const float* p = dy + plane * (int64_t)h * w;
-  float acc = 0.f;
-  for (int a = 0; a < nr; ++a)
-    for (int b = 0; b < nc; ++b) acc += p[(int64_t)rows[a] * w + cols[b]];
-  dx[e] = acc;
 }
 
 // Per-class gradient of the transfer function: block = (psf plane, chunk of vc column classes
@@ -1490,8 +1548,6 @@ extern "C" int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int
   if (B == 0) return CVN_OK;
   if (g.P > 65535) return fail(CVN_ERR_UNSUPPORTED, "B*C = %lld planes exceeds 65535", (long long)g.P);
   if (wg && g.s > 4) return fail(CVN_ERR_UNSUPPORTED, "weight gradients support scale <= 4");
-  if (pad_mode == CVN_PAD_REPLICATE && pad > 15)
-    return fail(CVN_ERR_UNSUPPORTED, "replicate padding above 15 in the backward");
   PlanTabs t;
   if (!plan_tabs(g, &t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
   BwdWs ws;
@@ -1523,10 +1579,14 @@ extern "C" int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int
     a.h = g.h; a.w = g.w; a.s = g.s; a.Hs = g.Hs; a.Ws = g.Ws; a.NC = g.NC; a.NCs = g.NCs;
     a.plan_h = t.plan[kTabH]; a.plan_H = t.plan[kTabHs];
     a.tabs_h = tabs + t.off[kTabH]; a.tabs_H = tabs + t.off[kTabHs];
-    a.rad_off = (int)align_up(cols_bwd_lds(g.h, g.Hs, g.s, wg), 16);
-    const size_t lds = a.rad_off + rader_lds_bytes(a.plan_h) + rader_lds_bytes(a.plan_H);
+    // classes per block: up to 8, LDS within 80 KiB where possible (2 blocks per CU)
+    const size_t rad = rader_lds_bytes(a.plan_h) + rader_lds_bytes(a.plan_H);
+    a.cpb = std::max(1, std::min(8, g.NC));
+    while (a.cpb > 1 && align_up(cols_bwd_lds(g.h, g.Hs, g.s, a.cpb, wg), 16) + rad > 80 * 1024) --a.cpb;
+    a.rad_off = (int)align_up(cols_bwd_lds(g.h, g.Hs, g.s, a.cpb, wg), 16);
+    const size_t lds = a.rad_off + rad;
     if (lds > kLdsLimit) return fail(CVN_ERR_UNSUPPORTED, "plane too large for the backward column pass");
-    const dim3 grid((unsigned)g.NC, (unsigned)(a.psf_batch == 1 ? g.C : g.P));
+    const dim3 grid((unsigned)((g.NC + a.cpb - 1) / a.cpb), (unsigned)(a.psf_batch == 1 ? g.C : g.P));
     hipLaunchKernelGGL(k_cols_bwd, grid, dim3(kThreads), lds, st, a);
     if ((rc = check_launch("backward column pass")) != CVN_OK) return rc;
   }
@@ -1536,9 +1596,10 @@ extern "C" int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int
     gl.Hs = g.h; gl.Ws = g.w; gl.NCs = g.NC;
     float* dy = (float*)(base + ws.Sg);
     if ((rc = launch_rows_inv(Sx, gl, 0, g.h, 0, g.w, CVN_ACT_NONE, tabs + t.off[kTabW], dy, st)) != CVN_OK) return rc;
-    const int64_t n = g.P * g.H * g.W;
-    hipLaunchKernelGGL(k_pad_adj, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, dy, g.P, g.H, g.W, g.pad,
-                       pad_mode, grad_x);
+    if (g.H > 65535) return fail(CVN_ERR_UNSUPPORTED, "input height exceeds 65535");
+    hipLaunchKernelGGL(k_pad_adj, dim3((unsigned)((g.W + 255) / 256), (unsigned)((g.H + kPadRows - 1) / kPadRows),
+                                       (unsigned)g.P), dim3(256), (size_t)4 * 4 * std::max(1, g.pad), st, dy, g.H, g.W,
+                       g.pad, pad_mode, grad_x);
     if ((rc = check_launch("padding adjoint")) != CVN_OK) return rc;
   }
   if (!wg) return CVN_OK;

@@ -64,8 +64,6 @@ def _hip_grad_eligible(x, weight, bias, scale, padding, padding_mode) -> bool:
         return False
     if (weight.requires_grad or bias.requires_grad) and int(scale) > 4:
         return False
-    if padding_mode == "replicate" and int(padding) > 15:
-        return False
     if x.dim() != 4 or x.shape[0] * x.shape[1] > 65535:
         return False
     _lib.load()

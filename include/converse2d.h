@@ -86,7 +86,7 @@ int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, int64_t H, in
  * CompositeImplicitAutograd, converse2d.cpp:223-227; gradient checks in test/test_error.py:51-54).
  * grad_out: (B,C,H*scale,W*scale).  Outputs (each may be null when not wanted): grad_x (B,C,H,W),
  * grad_psf (psf_batch,C,kh,kw), grad_bias (C).  x is read only for grad_psf / grad_bias.  Weight
- * gradients support scale <= 4; replicate padding up to 15. */
+ * gradients support scale <= 4. */
 size_t cvn_converse2d_bwd_workspace(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch,
                                     int kh, int kw, int scale, int pad);
 int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int64_t B, int64_t C, int64_t H,

@@ -23,6 +23,8 @@ CASES = [
     (2, 3, 256, 256, 5, 1, 2, "circular", 1),   # cfg3 plane size (260^2)
     (1, 2, 256, 256, 7, 1, 6, "circular", 1),   # cfg4 plane size (268^2)
     (2, 2, 64, 64, 25, 4, 0, "circular", 2),    # ConvReverseDataNet data step (per-sample 25x25 psf)
+    (1, 2, 24, 26, 3, 1, 20, "replicate", 1),   # wide replicate border: many samples fold onto the edge
+    (1, 2, 21, 19, 5, 2, 9, "reflect", 1),
 ]
 
 
