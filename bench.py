@@ -256,6 +256,36 @@ def bench_layer(torch, Fh, dev, B, C, H, W, k, s, p, dist, iters):
             "Gpix*ch/s": B * C * H * s * W * s / t / 1e9, "GB/s": nbytes / t / 1e9, "frac_hbm": nbytes / t / HBM_PEAK}
 
 
+def bench_backward(torch, Fh, dev, x, w, bias, c, iters):
+    """Converse2D backward at the cfg3 shape (the reference trains through autograd of its composite
+    op, converse2d.cpp:223-227; test_speed.py:95-100 times forward + backward): the library's backward
+    alone (all three gradients, and grad_x only), forward + backward through the autograd Function, and
+    the same forward + backward through torch autograd of the reference op sequence (torch.fft on the
+    GPU) for comparison."""
+    from conversenet_amd import composite
+    g = torch.Generator(device=dev).manual_seed(4)
+    go = torch.randn(x.shape, device=dev, generator=g)
+    b4 = bias.reshape(1, -1, 1, 1)
+    s, p, mode, eps = c["scale"], c["padding"], c["mode"], c["eps"]
+    out = {"workload": "cfg3 Converse2D backward, B16 C64 256x256 k5 s1 p2 circular, fp32"}
+    out["hip_backward_all_ms"] = time_events(torch, lambda: Fh.converse2d_backward(go, x, w, b4, s, p, mode, eps),
+                                             iters) * 1e3
+    out["hip_backward_x_ms"] = time_events(
+        torch, lambda: Fh.converse2d_backward(go, x, w, b4, s, p, mode, eps, True, False, False), iters) * 1e3
+    xr, wr, br = (t.detach().clone().requires_grad_(True) for t in (x, w, b4))
+
+    def hip_step():
+        Fh.converse2d_train(xr, wr, br, s, p, mode, eps).backward(go)
+
+    def torch_step():
+        composite.converse2d_module(xr, wr, br, s, p, mode, eps).backward(go)
+
+    out["hip_forward_backward_ms"] = time_events(torch, hip_step, iters) * 1e3
+    out["torch_autograd_forward_backward_ms"] = time_events(torch, torch_step, max(2, iters // 2)) * 1e3
+    out["speedup_vs_torch_autograd"] = out["torch_autograd_forward_backward_ms"] / out["hip_forward_backward_ms"]
+    return out
+
+
 def bench_block_pointwise(torch, Fh, dev, iters):
     """The three channel-mixing kernels of one ConverseBlockAlphaVariant at the Converse-USRNet body
     shape (B4 C64 256x256, hidden 128): LN + 1x1 64->128 + GELU, 1x1 128->64 + alpha-scaled residual,
@@ -309,6 +339,12 @@ def only_kernel(torch, Fh, args, dev, x, step):
         m, xin = make_dncnn(torch, dev)
         torch.set_grad_enabled(False)
         fn = lambda: m(xin)
+    elif args.only == "backward":
+        g = torch.Generator(device=dev).manual_seed(4)
+        go = torch.randn(x.shape, device=dev, generator=g)
+        c, w, b = CFG3, step.w, step.b
+        fn = lambda: Fh.converse2d_backward(go, x, w, b.reshape(1, -1, 1, 1), c["scale"], c["padding"], c["mode"],
+                                            c["eps"])
     elif args.only == "usrnet":
         m, xin, kin = make_usrnet(torch, dev)
         torch.set_grad_enabled(False)
@@ -336,7 +372,7 @@ def main():
     ap.add_argument("--cpu-worker", action="store_true")
     ap.add_argument("--cpu-iters", type=int, default=3)
     ap.add_argument("--cpu-threads", type=int, default=16)
-    ap.add_argument("--only", choices=["converse2d", "layernorm", "conv1x1", "copy", "dncnn", "usrnet"],
+    ap.add_argument("--only", choices=["converse2d", "layernorm", "conv1x1", "copy", "dncnn", "usrnet", "backward"],
                     help="run one kernel family alone (for rocprofv3)")
     args = ap.parse_args()
 
@@ -360,6 +396,7 @@ def main():
 
     def step():
         return Fh.converse2d_fused(x, w, bias, c["scale"], c["padding"], c["mode"], c["eps"])
+    step.w, step.b = w, bias
 
     if args.only:
         return only_kernel(torch, Fh, args, dev, x, step)
@@ -399,6 +436,7 @@ def main():
                                 "frac_hbm": cv_bytes / t_cv / HBM_PEAK, "TFLOP/s": cv_flops / t_cv / 1e12,
                                 "frac_mfma": cv_flops / t_cv / FP32_MFMA_PEAK}
     extra["block_pointwise"] = bench_block_pointwise(torch, Fh, dev, max(10, args.steps // 2))
+    extra["converse2d_backward"] = bench_backward(torch, Fh, dev, x, w, bias, c, max(5, args.steps // 5))
     if not args.no_model:
         extra["converse_dncnn"] = bench_model(torch, dev)
         extra["converse_usrnet"] = bench_usrnet(torch, dev)
