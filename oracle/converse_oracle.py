@@ -22,8 +22,11 @@ How each function is pinned (checked by tests/test_oracle.py and tests/test_orac
                       autograd (fp64) of the reference op sequence restated in torch
   layernorm_cf        zero mean / unit biased variance closed form; torch F.layer_norm
   conv1x1, gelu       einsum definition; erf special values; torch F.conv2d / F.gelu
-  converse_block, converse_dncnn, conv_reverse_datanet, converse_usrnet
+  converse_block, converse_dncnn, conv_reverse_datanet, converse_usrnet, msrresnet,
+  converse_msrresnet, converse_up_msrresnet
                       compositions of the pinned pieces (structure follows the reference classes)
+  conv3x3, pixel_shuffle, bilinear_upsample
+                      torch F.conv2d / nn.PixelShuffle / F.interpolate(bilinear) on the CPU
 """
 from __future__ import annotations
 
@@ -396,6 +399,109 @@ def converse_usrnet(x, k, sf, sd, kernel_size, num_iterations=5, num_blocks=7, d
         x = conv_reverse_datanet(x, k_, sf if i == 0 else 1, sd["d.alpha"], 1e-3, dtype)
         x = body(x)
     return conv1x1(x, sd["conv2.weight"], sd["conv2.bias"], dtype)
+
+
+# ------------------------------------------------------------------------------------------------
+# SRResNet family (models/converse_srresnet.py) and the plain layers it uses
+# ------------------------------------------------------------------------------------------------
+def conv3x3(x, weight, bias, dtype=np.float64):
+    """nn.Conv2d(cin, cout, 3, 1, 1) (zero padding 1): y[b,o,i,j] = sum_{c,a,d} W[o,c,a,d] x[b,c,i+a-1,j+d-1]."""
+    x = x.astype(dtype)
+    B, C, H, W = x.shape
+    xp = np.zeros((B, C, H + 2, W + 2), dtype)
+    xp[:, :, 1:-1, 1:-1] = x
+    y = np.zeros((B, weight.shape[0], H, W), dtype)
+    for a in range(3):
+        for d in range(3):
+            y += np.einsum("oc,bchw->bohw", weight[:, :, a, d].astype(dtype), xp[:, :, a:a + H, d:d + W])
+    if bias is not None:
+        y += bias.astype(dtype)[None, :, None, None]
+    return y
+
+
+def pixel_shuffle(x, r):
+    """nn.PixelShuffle(r): out[b, c, h r + i, w r + j] = in[b, c r^2 + i r + j, h, w]."""
+    B, Cr, H, W = x.shape
+    C = Cr // (r * r)
+    return x.reshape(B, C, r, r, H, W).transpose(0, 1, 4, 2, 5, 3).reshape(B, C, H * r, W * r)
+
+
+def leaky_relu(x, slope=0.1):
+    return np.where(x >= 0, x, slope * x)
+
+
+def bilinear_upsample(x, s):
+    """F.interpolate(scale_factor=s, mode='bilinear', align_corners=False): source coordinate
+    (dst + 0.5) / s - 0.5 clamped at 0, linear weights between floor and floor + 1 (clamped to the
+    last sample), separably along rows and columns."""
+    def axis_weights(n):
+        dst = np.arange(n * s)
+        src = np.maximum((dst + 0.5) / s - 0.5, 0.0)
+        i0 = np.floor(src).astype(int)
+        i1 = np.minimum(i0 + 1, n - 1)
+        lam1 = src - i0
+        return i0, i1, lam1
+    H, W = x.shape[-2:]
+    r0, r1, lr = axis_weights(H)
+    c0, c1, lc = axis_weights(W)
+    rows = x[..., r0, :] * (1 - lr)[:, None] + x[..., r1, :] * lr[:, None]
+    return rows[..., c0] * (1 - lc) + rows[..., c1] * lc
+
+
+def residual_block(x, sd, prefix, dtype=np.float64):
+    """ResidualBlock (util_converse.py:328-342): x + conv2(relu(conv1(x)))."""
+    t = np.maximum(conv3x3(x, sd[prefix + "conv1.weight"], sd[prefix + "conv1.bias"], dtype), 0.0)
+    return x + conv3x3(t, sd[prefix + "conv2.weight"], sd[prefix + "conv2.bias"], dtype)
+
+
+def msrresnet(x, sd, num_blocks=16, upscale=4, dtype=np.float64):
+    """MSRResNet.forward (models/converse_srresnet.py:33-47)."""
+    x = x.astype(dtype)
+    x1 = leaky_relu(conv3x3(x, sd["conv_first.weight"], sd["conv_first.bias"], dtype))
+    for i in range(num_blocks):
+        x1 = residual_block(x1, sd, f"conv_body.{i}.", dtype)
+    if upscale == 4:
+        x1 = leaky_relu(pixel_shuffle(conv3x3(x1, sd["upconv1.weight"], sd["upconv1.bias"], dtype), 2))
+        x1 = leaky_relu(pixel_shuffle(conv3x3(x1, sd["upconv2.weight"], sd["upconv2.bias"], dtype), 2))
+    elif upscale in (2, 3):
+        x1 = leaky_relu(pixel_shuffle(conv3x3(x1, sd["upconv1.weight"], sd["upconv1.bias"], dtype), upscale))
+    x1 = conv3x3(leaky_relu(conv3x3(x1, sd["conv_hres.weight"], sd["conv_hres.bias"], dtype)),
+                 sd["conv_last.weight"], sd["conv_last.bias"], dtype)
+    return x1 + bilinear_upsample(x, upscale)
+
+
+def converse_msrresnet(x, sd, num_blocks=16, upscale=4, dtype=np.float64):
+    """ConverseMSRResNet.forward (models/converse_srresnet.py:72-82): 1x1 head + GELU, ConverseBlocks
+    (k5, padding 4, replicate), two ConverseBlock + Converse2D(k2, s2, padding 2, replicate, eps 1e-3)
+    + GELU upsamplers, ConverseBlock + GELU, 1x1 tail without bias, plus the bilinear-upsampled input."""
+    x = x.astype(dtype)
+    blk = lambda t, name: converse_block(t, sd, name + ".", 5, 1, 4, "replicate", 1e-5, False, dtype)  # noqa: E731
+    x1 = gelu(conv1x1(x, sd["conv_first.weight"], sd["conv_first.bias"], dtype))
+    for i in range(num_blocks):
+        x1 = blk(x1, f"conv_body.{i}")
+    for up in ("1", "2"):
+        x1 = blk(x1, "upconv" + up)
+        x1 = gelu(converse2d_module(x1, sd[f"up{up}.weight"], sd[f"up{up}.bias"], 2, 2, "replicate", 1e-3, dtype))
+    x1 = gelu(blk(x1, "conv_hres"))
+    x1 = conv1x1(x1, sd["conv_last.weight"], None, dtype)
+    return x1 + bilinear_upsample(x, upscale)
+
+
+def converse_up_msrresnet(x, sd, num_blocks=16, upscale=4, dtype=np.float64):
+    """ConverseUpMSRResNet.forward (models/converse_srresnet.py:107-119): 3x3 head + GELU, residual
+    blocks, two (3x3 conv -> Converse2D(k2, s2, padding 2, circular) -> GELU) upsamplers, 3x3 tail,
+    plus the bilinear-upsampled input."""
+    x = x.astype(dtype)
+    x1 = gelu(conv3x3(x, sd["conv_first.weight"], sd["conv_first.bias"], dtype))
+    for i in range(num_blocks):
+        x1 = residual_block(x1, sd, f"conv_body.{i}.", dtype)
+    for k in ("1", "2"):
+        x1 = conv3x3(x1, sd[f"conv{k}.weight"], sd[f"conv{k}.bias"], dtype)
+        x1 = gelu(converse2d_module(x1, sd[f"reverse{k}.weight"], sd[f"reverse{k}.bias"], 2, 2, "circular", 1e-5,
+                                    dtype))
+    x1 = conv3x3(gelu(conv3x3(x1, sd["conv_hres.weight"], sd["conv_hres.bias"], dtype)), sd["conv_last.weight"],
+                 sd["conv_last.bias"], dtype)
+    return x1 + bilinear_upsample(x, upscale)
 
 
 # ------------------------------------------------------------------------------------------------

@@ -168,6 +168,37 @@ def test_converse_usrnet():
     assert psnr(got, ref) >= 60
 
 
+def test_converse_msrresnet():
+    """ConverseMSRResNet (models/converse_srresnet.py:50-82) at its default width and depth: replicate
+    k5 p4 ConverseBlocks and the k2 s2 p2 replicate upsamplers (eps 1e-3) on HIP."""
+    from conversenet_amd.converse_srresnet import ConverseMSRResNet
+    torch.manual_seed(6)
+    m = ConverseMSRResNet().eval()
+    with torch.no_grad():
+        for mod in (m.up1, m.up2):
+            mod.bias.normal_(0, 0.5)
+    rng = seeded("msrresnet")
+    x = rng.random((1, 3, 16, 18)).astype(np.float32)
+    ref = O.converse_msrresnet(x, _sd(m))
+    with torch.no_grad():
+        got = _n(m.to(DEV)(_t(x)))
+    print(f"ConverseMSRResNet psnr {psnr(got, ref):.1f} dB")
+    assert psnr(got, ref) >= 60
+
+
+def test_converse_up_msrresnet():
+    from conversenet_amd.converse_srresnet import ConverseUpMSRResNet
+    torch.manual_seed(7)
+    m = ConverseUpMSRResNet(num_blocks=4).eval()
+    rng = seeded("upmsrresnet")
+    x = rng.random((2, 3, 12, 12)).astype(np.float32)
+    ref = O.converse_up_msrresnet(x, _sd(m), 4)
+    with torch.no_grad():
+        got = _n(m.to(DEV)(_t(x)))
+    print(f"ConverseUpMSRResNet psnr {psnr(got, ref):.1f} dB")
+    assert psnr(got, ref) >= 60
+
+
 # ------------------------------------------------------------------------------------------------
 # Full cfg3 size (B16 C64 256^2 k5 p2 circular): oracle on a plane sample, plus size-free identities
 # ------------------------------------------------------------------------------------------------
