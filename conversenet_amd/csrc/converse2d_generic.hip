@@ -1411,11 +1411,8 @@ extern "C" int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, in
   const char* tabs = (const char*)table + ws.tabs;
   float2* S = (float2*)(base + ws.S);
   float2* SH = (float2*)(base + ws.SH);
-  if (!fused_disabled() && pfa268_applies(g.h, g.w, g.s, t.plan[kTabW])) {
-    const char* rad = tabs + t.off[kTabW] + plan_tw_bytes(t.plan[kTabW]) + t.plan[kTabW].rad[0].off;
-    const float2* bh = (const float2*)(rad + 8 * (t.plan[kTabW].rad[0].R - 1));  // bf, then bi
-    return pfa268_forward(x, g.P, g.C, g.Cp / g.C, g.H, g.W, g.pad, pad_mode, act, phi, bh, S, out, st);
-  }
+  if (!fused_disabled() && pfa268_applies(g.h, g.w, g.s))
+    return pfa268_forward(x, g.P, g.C, g.Cp / g.C, g.H, g.W, g.pad, pad_mode, act, phi, S, out, st);
   if ((rc = launch_rows_fwd(x, g.P, g.H, g.W, g.pad, pad_mode, g.h, g.w, tabs + t.off[kTabW], S, st)) != CVN_OK)
     return rc;
   ColModArgs ca;

@@ -2,20 +2,17 @@
 //
 // Same three-pass data flow as the generic path (row transform -> column transform x Phi x inverse
 // -> inverse row transform, half spectra column-major in between), but every transform is the
-// in-place prime-factor FFT 268 = 4 * 67 (no twiddles): a row or column of 268 complex values sits
-// in LDS at "3-D natural" positions pos_in(n) = ((3 n) mod 4) * 67 + ((17 n) mod 67), pass A runs a
-// 67-point DFT along each contiguous segment of 67, pass B a 4-point DFT along stride 67, and
-// frequency v ends at fpos(v) = (v mod 4) * 67 + (v mod 67).  The inverse runs the same passes with
-// inverse DFTs in the opposite order, from fpos back to pos_in.
+// prime-factor FFT 268 = 4 * 67 (no twiddles) on one quad of lanes: each lane holds one PFA segment
+// of 67 complex values in registers, runs the 67-point DFT on it, and the 4-point DFT runs across
+// the quad through DPP permutes (layout and index maps at the quad helpers below).
 //
 // The 67-point DFT is one thread's work, entirely in registers, by Rader's algorithm (primitive
 // root 2): a_q = u[2^q mod 67], X_0 = u_0 + sum a, X[2^-q mod 67] = u_0 + (a (*) b)_q with the cyclic
 // convolution of length 66 done as an in-register prime-factor FFT 66 = 2 * 3 * 11, a product with
-// FFT(b)/66 (the generic path's Rader table for 67, built once per geometry) and the inverse FFT.
-// Slot s of the 66-register array holds the convolution input a[s]; after the forward 3-axis DFT it
-// holds the transform at k = kappa(s) (k = s mod 6, k = 2 s mod 11), and after the inverse 3-axis DFT
-// it holds the convolution output at s again.  (C. M. Rader, Proc. IEEE 56(6), 1968; I. J. Good,
-// J. R. Stat. Soc. B 20, 1958.)
+// FFT(b)/66 (compile-time constants) and the inverse FFT.  Slot s of the 66-register array holds the
+// convolution input a[s]; after the forward 3-axis DFT it holds the transform at k = kappa(s)
+// (k = s mod 6, k = 2 s mod 11), and after the inverse 3-axis DFT it holds the convolution output at
+// s again.  (C. M. Rader, Proc. IEEE 56(6), 1968; I. J. Good, J. R. Stat. Soc. B 20, 1958.)
 #include <math.h>
 
 #include <algorithm>
@@ -27,8 +24,6 @@ namespace pfa268 {
 
 constexpr int L = 268, P = 67, RM = 66, NC = L / 2 + 1;  // NC: half-spectrum bins
 
-__host__ __device__ constexpr int pos_in(int n) { return ((3 * n) % 4) * P + ((17 * n) % P); }
-__host__ __device__ constexpr int fpos(int v) { return (v % 4) * P + (v % P); }
 // Index tables, evaluated at compile time: gp[q] = 2^q mod 67, gq[q] = 2^-q mod 67 (34 = 2^-1), and
 // kap[s] = the k with k = s (mod 6), k = 2 s (mod 11).
 struct Tabs {
@@ -49,6 +44,59 @@ struct Tabs {
   }
 };
 constexpr Tabs kT{};
+
+// cos and sin of 2 pi m / n by Taylor series in double at compile time (|angle| <= pi after
+// reduction; 40 terms leave a truncation error far below double rounding).
+struct CosSin {
+  double c, s;
+};
+constexpr CosSin cos_sin_turn(int m, int n) {
+  m %= n;
+  if (2 * m >= n) m -= n;  // angle in [-pi, pi)
+  const double x = 2.0 * 3.14159265358979323846 * m / n;
+  double c = 0.0, s = 0.0, term = 1.0;  // term = x^k / k!
+  for (int k = 0; k < 40; ++k) {
+    const int r = k & 3;
+    if (r == 0) c += term;
+    if (r == 1) s += term;
+    if (r == 2) c -= term;
+    if (r == 3) s -= term;
+    term = term * x / (k + 1);
+  }
+  return CosSin{c, s};
+}
+// Rader tables of the 67-point DFT (primitive root 2): b_q = W67^(2^-q mod 67), bf = FFT66(b) / 66
+// (forward) and bi = FFT66(conj b) / 66 (inverse), evaluated in double at compile time and rounded
+// once.  Their indices are compile-time constants in dft67_reg, so the values become instruction
+// literals and occupy no registers.
+struct RaderTabs {
+  float bfr[RM], bfi[RM], bir[RM], bii[RM];
+  constexpr RaderTabs() : bfr(), bfi(), bir(), bii() {
+    double br[RM] = {}, bim[RM] = {}, wr[RM] = {}, wi[RM] = {};
+    for (int q = 0; q < RM; ++q) {
+      const CosSin b = cos_sin_turn(Tabs().gq[q], P), w = cos_sin_turn(q, RM);
+      br[q] = b.c;
+      bim[q] = -b.s;  // exp(-2 pi i gq / 67)
+      wr[q] = w.c;
+      wi[q] = -w.s;  // exp(-2 pi i q / 66)
+    }
+    for (int m = 0; m < RM; ++m) {
+      double fr = 0, fi = 0, ir = 0, ii = 0;
+      for (int q = 0; q < RM; ++q) {
+        const int e = (q * m) % RM;
+        fr += br[q] * wr[e] - bim[q] * wi[e];
+        fi += br[q] * wi[e] + bim[q] * wr[e];
+        ir += br[q] * wr[e] + bim[q] * wi[e];  // conj(b) w
+        ii += br[q] * wi[e] - bim[q] * wr[e];
+      }
+      bfr[m] = (float)(fr / RM);
+      bfi[m] = (float)(fi / RM);
+      bir[m] = (float)(ir / RM);
+      bii[m] = (float)(ii / RM);
+    }
+  }
+};
+constexpr RaderTabs kR{};
 
 // In-register 3-axis DFT of the 66 slots (axes of length 2, 3, 11; slot s has coordinates
 // (s mod 2, s mod 3, 2 s mod 11), i.e. s = 33 n1 + 22 n2 + 6 n3 mod 66).
@@ -89,46 +137,100 @@ __device__ __forceinline__ void dft66_axes(float2 (&a)[RM]) {
     }
 }
 
-// 67-point DFT (direction given by the table: bh = FFT(b)/66 forward or its inverse-direction
-// counterpart) of p[0], p[S], ..., p[66 S] in place.
-template <int S>
-__device__ __forceinline__ void dft67(float2* p, const float2* __restrict__ bh) {
+// 67-point DFT of the 67 registers x[0..66] in place (forward, or inverse without normalisation).
+template <bool INV>
+__device__ __forceinline__ void dft67_reg(float2 (&x)[P]) {
   float2 a[RM];
-  const float2 u0 = p[0];
+  const float2 u0 = x[0];
 #pragma unroll
-  for (int q = 0; q < RM; ++q) a[q] = p[kT.gp[q] * S];
+  for (int q = 0; q < RM; ++q) a[q] = x[kT.gp[q]];
   dft66_axes<false>(a);
   const float2 x0 = cadd(u0, a[0]);  // slot 0 holds bin 0: sum of the a's
 #pragma unroll
-  for (int s = 0; s < RM; ++s) a[s] = cmul(a[s], bh[kT.kap[s]]);
+  for (int s = 0; s < RM; ++s) {
+    const int k = kT.kap[s];
+    a[s] = cmul(a[s], INV ? make_float2(kR.bir[k], kR.bii[k]) : make_float2(kR.bfr[k], kR.bfi[k]));
+  }
   a[0] = cadd(a[0], u0);  // adds u_0 to every convolution output
   dft66_axes<true>(a);
-  p[0] = x0;
+  x[0] = x0;
 #pragma unroll
-  for (int q = 0; q < RM; ++q) p[kT.gq[q] * S] = a[q];
+  for (int q = 0; q < RM; ++q) x[kT.gq[q]] = a[q];
 }
 
-// pass A / pass B over `n` rows of 268 slots (row stride LD) held in LDS
+// Compiler scheduling fence.  The unrolled gather loops issue kLoadChunk global loads, fence, then
+// consume them: the loads of a chunk are in flight together (one memory latency per chunk), and the
+// compiler can neither hoist all 67 (or 134) loads up front, which would keep every address and
+// result live at once, nor serialise each load with its use to save registers.  The fence orders
+// generic and global-pointer accesses only (raw buffer loads are not held back by it).
+constexpr int kLoadChunk = 8;
+__device__ __forceinline__ void sched_fence() { asm volatile("" ::: "memory"); }
+
+// ---- quads: the 4 lanes 4 q .. 4 q + 3 of a wave share one complex row (or one column) ----
+// Lane s of a quad holds PFA segment s (samples n with 3 n = s mod 4).  It loads the samples in
+// column order c = 4 i + sig(s), sig(s) = 3 s mod 4, so the quad's loads cover 4 adjacent columns;
+// register i then holds segment element m = (i + dl(s)) mod 67, dl(s) = 17 sig(s) mod 67 (a cyclic
+// rotation, undone by the twiddle W67^(dl j) on the 67-point DFT's output).  The 4-point DFT across
+// the segments runs across the quad's lanes through DPP quad permutes; afterwards lane k holds the
+// bins v = (201 k + 68 j) mod 268 (v = k mod 4, v = j mod 67) in register j.
+__device__ __forceinline__ int quad_sig(int s) { return (3 * s) & 3; }
+__device__ __forceinline__ int quad_delta(int s) { return (17 * quad_sig(s)) % P; }
+
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ float2 dpp2(float2 v) {
+  return make_float2(dppf<CTRL>(v.x), dppf<CTRL>(v.y));
+}
+// quad_perm controls: broadcast lane 0 / 1 / 2 / 3 of the quad, and swap lanes 1 and 3
+constexpr int kQ0 = 0x00, kQ1 = 0x55, kQ2 = 0xAA, kQ3 = 0xFF, kSwap13 = 0x6C;
+
+// 4-point DFT across the quad for every register: lane k ends with sum_s W4^(+-k s) x_s.
 template <bool INV>
-__device__ __forceinline__ void pass_a(float2* buf, int n, int ld, const float2* bh, int tid, int nth) {
-  for (int w = tid; w < 4 * n; w += nth) {
-    const int m1 = w / n, t = w - m1 * n;  // row fastest across lanes
-    dft67<1>(buf + t * ld + m1 * P, bh);
+__device__ __forceinline__ void quad_dft4(float2 (&x)[P], int k) {
+  const bool odd = k & 1, hi = k & 2;
+#pragma unroll
+  for (int j = 0; j < P; ++j) {
+    const float2 a0 = dpp2<kQ0>(x[j]), a1 = dpp2<kQ1>(x[j]), a2 = dpp2<kQ2>(x[j]), a3 = dpp2<kQ3>(x[j]);
+    const float2 p = cadd(a0, a2), q = csub(a0, a2), r = cadd(a1, a3), w = csub(a1, a3);
+    const float2 rw = INV ? make_float2(-w.y, w.x) : make_float2(w.y, -w.x);  // +-i w
+    const float2 e = odd ? q : p, f = odd ? rw : r;
+    x[j] = hi ? csub(e, f) : cadd(e, f);
   }
 }
-template <bool INV>
-__device__ __forceinline__ void pass_b(float2* buf, int n, int ld, int tid, int nth) {
-  for (int w = tid; w < P * n; w += nth) {
-    const int t = w / P, m3 = w - t * P;
-    float2* b = buf + t * ld + m3;
-    float2 u[4] = {b[0], b[P], b[2 * P], b[3 * P]};
-    Dft<4, INV>::run(u);
-    b[0] = u[0];
-    b[P] = u[1];
-    b[2 * P] = u[2];
-    b[3 * P] = u[3];
+
+// x[j] *= W67^(+-dl j) (W67 = exp(-2 pi i / 67); tw holds W67^m)
+template <bool CONJ>
+__device__ __forceinline__ void quad_rotate(float2 (&x)[P], const float2* tw, int dl) {
+  int m = 0;
+#pragma unroll
+  for (int j = 0; j < P; ++j) {
+    const float2 t = tw[m];
+    x[j] = cmul(x[j], CONJ ? cconj(t) : t);
+    m += dl;
+    if (m >= P) m -= P;
+    if (j % kLoadChunk == kLoadChunk - 1) sched_fence();
   }
 }
+
+// Raw buffer stores: one wave-uniform resource per tensor and a 32-bit byte offset per lane.  A
+// store whose offset lies past the resource's size is dropped by the hardware, so the conditional
+// stores below need no branch (a divergent branch would make the compiler hoist the quad's DPP reads
+// above it and keep them all live).
+constexpr uint32_t kDrop = 0xFFFFFFF0u;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void bstore4(float4 v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, 0);
+}
+__device__ __forceinline__ void bstore1(float v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v), r, off, 0, 0);
+}
+
 
 __device__ __forceinline__ int pad_map(int i, int n, int p, int mode) {
   int j = i - p;
@@ -141,208 +243,218 @@ __device__ __forceinline__ int pad_map(int i, int n, int p, int mode) {
   }
 }
 
-constexpr int LD = L + 1;  // LDS row stride (odd: spreads the stride-67 pass over banks)
+// Shared per-block tables: W67^m and (row pass) the source column of every padded column.  The
+// Rader tables are read straight from global memory: their addresses are uniform, so they arrive
+// through scalar loads instead of occupying vector registers.
+struct QuadTabs {
+  float2 tw[P];
+  short csrc[L];
+};
+__device__ __forceinline__ void load_quad_tabs(QuadTabs& T, int W, int pad, int mode) {
+  for (int m = threadIdx.x; m < P; m += blockDim.x) {
+    double sn, cs;
+    sincospi(-2.0 * (double)m / (double)P, &sn, &cs);
+    T.tw[m] = make_float2((float)cs, (float)sn);
+  }
+  if (W > 0)
+    for (int n = threadIdx.x; n < L; n += blockDim.x) T.csrc[n] = (short)pad_map(n, W, pad, mode);
+  __syncthreads();
+}
 
-// Global-memory loops issue kBatch independent loads per thread before using any of them, so each
-// wave keeps many requests in flight (a plain loop would wait out the full HBM latency per element).
-constexpr int kBatch = 8;
-
-// ---- row forward: padded rows 2t, 2t + 1 of the plane as one complex row; half spectrum out ----
+// ---- row forward: padded rows 2t, 2t + 1 of a plane as one complex row; half spectrum out ----
+// quad index g = plane * 134 + t; S (P, NC, L): column v, row r.
 struct RowsArgs {
-  const float* x;   // (P, H, W)
-  float2* S;        // (P, NC, L): column v, row r
-  const float2* bh; // FFT(b)/66 forward, then inverse direction (2 x 66)
-  int H, W, pad, mode, nrp;
+  const float* x;  // (P, H, W)
+  float2* S;
+  int64_t nquad;
+  int H, W, pad, mode;
+  uint32_t s_bytes;  // size of S (< 2^31)
 };
 
 __global__ void __launch_bounds__(256) k_pfa_rows_fwd(RowsArgs a) {
-  extern __shared__ float2 sm[];
-  float2* bh = sm;            // 66
-  float2* buf = sm + 2 * RM;  // nrp rows of LD
-  const int tid = threadIdx.x, nth = blockDim.x;
-  const int64_t plane = blockIdx.y;
-  const int t0 = blockIdx.x * a.nrp;  // first row pair
-  const int nrp = min(a.nrp, L / 2 - t0);
-  for (int i = tid; i < RM; i += nth) bh[i] = a.bh[i];
-  // per-block index tables: source column and LDS position of each padded column, source row of
-  // each padded row of the block
-  short* csrc = (short*)(buf + a.nrp * LD);
-  short* cpos = csrc + L;
-  short* rsrc = cpos + L;
-  for (int n = tid; n < L; n += nth) {
-    csrc[n] = (short)pad_map(n, a.W, a.pad, a.mode);
-    cpos[n] = (short)pos_in(n);
-  }
-  for (int r = tid; r < 2 * nrp; r += nth) rsrc[r] = (short)pad_map(2 * t0 + r, a.H, a.pad, a.mode);
-  __syncthreads();
-  const float* xp = a.x + plane * (int64_t)a.H * a.W;
-  for (int i0 = tid; i0 < nrp * L; i0 += kBatch * nth) {
-    float2 v[kBatch];
+  __shared__ QuadTabs T;
+  load_quad_tabs(T, a.W, a.pad, a.mode);
+  const int k = threadIdx.x & 3;
+  const int64_t gq = (int64_t)blockIdx.x * (blockDim.x >> 2) + (threadIdx.x >> 2);
+  if (gq >= a.nquad) return;  // whole quads leave together
+  const int64_t plane = gq / (L / 2);
+  const int t = (int)(gq - plane * (L / 2));
+  const int ra = pad_map(2 * t, a.H, a.pad, a.mode), rb = pad_map(2 * t + 1, a.H, a.pad, a.mode);
+  const float* xa = a.x + (plane * a.H + (ra < 0 ? 0 : ra)) * (int64_t)a.W;
+  const float* xb = a.x + (plane * a.H + (rb < 0 ? 0 : rb)) * (int64_t)a.W;
+  const int sig = quad_sig(k);
+  float2 x[P];
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int idx = i0 + k * nth;
-      v[k] = make_float2(0.f, 0.f);
-      if (idx < nrp * L) {
-        const int t = idx / L, n = idx - t * L;
-        const int sc = csrc[n], ra = rsrc[2 * t], rb = rsrc[2 * t + 1];
-        if (sc >= 0) {
-          if (ra >= 0) v[k].x = xp[(int64_t)ra * a.W + sc];
-          if (rb >= 0) v[k].y = xp[(int64_t)rb * a.W + sc];
-        }
-      }
-    }
+  for (int i0 = 0; i0 < P; i0 += kLoadChunk) {
+    // a chunk of unconditional loads from clamped (in-range) addresses, then selects: no branches
+    float va[kLoadChunk], vb[kLoadChunk];
+    int sv[kLoadChunk];
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int idx = i0 + k * nth;
-      if (idx < nrp * L) {
-        const int t = idx / L, n = idx - t * L;
-        buf[t * LD + cpos[n]] = v[k];
-      }
+    for (int ii = 0; ii < kLoadChunk && i0 + ii < P; ++ii) {
+      const int sc = T.csrc[4 * (i0 + ii) + sig];
+      const int scc = sc < 0 ? 0 : sc;
+      va[ii] = xa[scc];
+      vb[ii] = xb[scc];
+      sv[ii] = sc;
     }
+    sched_fence();
+#pragma unroll
+    for (int ii = 0; ii < kLoadChunk && i0 + ii < P; ++ii)
+      x[i0 + ii] = make_float2((sv[ii] >= 0 && ra >= 0) ? va[ii] : 0.f, (sv[ii] >= 0 && rb >= 0) ? vb[ii] : 0.f);
   }
-  __syncthreads();
-  pass_a<false>(buf, nrp, LD, bh, tid, nth);
-  __syncthreads();
-  pass_b<false>(buf, nrp, LD, tid, nth);
-  __syncthreads();
-  // unpack two real rows: Ya = (Z[v] + conj Z[-v]) / 2, Yb = (Z[v] - conj Z[-v]) / (2i)
-  float2* Sp = a.S + plane * (int64_t)NC * L;
-  for (int idx = tid; idx < NC * 2 * nrp; idx += nth) {
-    const int v = idx / (2 * nrp), rl = idx - v * 2 * nrp;
-    const int t = rl >> 1;
-    const float2 z = buf[t * LD + fpos(v)];
-    const float2 zm = buf[t * LD + fpos(v == 0 ? 0 : L - v)];
-    const float2 o = (rl & 1) == 0 ? make_float2(0.5f * (z.x + zm.x), 0.5f * (z.y - zm.y))
-                                   : make_float2(0.5f * (z.y + zm.y), 0.5f * (zm.x - z.x));
-    Sp[(int64_t)v * L + 2 * t0 + rl] = o;
+  sched_fence();
+  dft67_reg<false>(x);
+  sched_fence();
+  quad_rotate<false>(x, T.tw, quad_delta(k));
+  sched_fence();
+  quad_dft4<false>(x, k);
+  sched_fence();
+  // two real rows: Ya = (Z[v] + conj Z[-v]) / 2, Yb = (Z[v] - conj Z[-v]) / (2i); Z[-v] sits in lane
+  // (4 - k) mod 4, register (67 - j) mod 67
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.S, a.s_bytes);
+  const uint32_t base = (uint32_t)((plane * NC * L + 2 * t) * 8);
+  int v = (201 * k) % L;
+#pragma unroll
+  for (int j = 0; j < P; ++j) {
+    const float2 z = x[j], zm = dpp2<kSwap13>(x[(P - j) % P]);
+    bstore4(make_float4(0.5f * (z.x + zm.x), 0.5f * (z.y - zm.y), 0.5f * (z.y + zm.y), 0.5f * (zm.x - z.x)), sr,
+            v <= L / 2 ? base + (uint32_t)(v * L * 8) : kDrop);
+    v += 68;
+    if (v >= L) v -= L;
+    if (j % kLoadChunk == kLoadChunk - 1) sched_fence();
   }
 }
 
 // ---- columns: forward transform, x Phi, inverse transform, in place on S ----
+// quad index g = plane * NC + column.
 struct ColsArgs {
-  float2* S;            // (P, NC, L)
-  const float2* phi;    // (Cp, NC, L) natural order, 1/(L L) folded in
-  const float2* bh;     // 2 x 66
-  int64_t C, psf_batch;
-  int ncb;              // columns per block
+  float2* S;          // (P, NC, L)
+  const float2* phi;  // (Cp, NC, L) natural order, 1/(L L) folded in
+  int64_t C, psf_batch, nquad;
 };
 
 __global__ void __launch_bounds__(256) k_pfa_cols(ColsArgs a) {
-  extern __shared__ float2 sm[];
-  float2* bhf = sm;
-  float2* bhi = sm + RM;
-  float2* buf = sm + 2 * RM;
-  const int tid = threadIdx.x, nth = blockDim.x;
-  const int64_t plane = blockIdx.y;
-  const int v0 = blockIdx.x * a.ncb;
-  const int ncol = min(a.ncb, NC - v0);
+  __shared__ QuadTabs T;
+  load_quad_tabs(T, 0, 0, 0);
+  const int k = threadIdx.x & 3;
+  const int64_t gq = (int64_t)blockIdx.x * (blockDim.x >> 2) + (threadIdx.x >> 2);
+  if (gq >= a.nquad) return;
+  const int64_t plane = gq / NC;
+  const int c = (int)(gq - plane * NC);
   const int64_t cp = a.psf_batch == 1 ? plane % a.C : plane;
-  for (int i = tid; i < 2 * RM; i += nth) sm[i] = a.bh[i];
-  float2* Sp = a.S + (plane * NC + v0) * (int64_t)L;
-  for (int u = tid; u < L; u += nth) {
-    const int pu = pos_in(u);
-    for (int cb = 0; cb < ncol; cb += kBatch) {
-      float2 v[kBatch];
+  float2* col = a.S + (plane * NC + c) * (int64_t)L + quad_sig(k);
+  float2 x[P];
 #pragma unroll
-      for (int k = 0; k < kBatch; ++k)
-        if (cb + k < ncol) v[k] = Sp[(int64_t)(cb + k) * L + u];
-#pragma unroll
-      for (int k = 0; k < kBatch; ++k)
-        if (cb + k < ncol) buf[(cb + k) * LD + pu] = v[k];
-    }
+  for (int i = 0; i < P; ++i) {
+    x[i] = col[4 * i];
+    if (i % kLoadChunk == kLoadChunk - 1) sched_fence();
   }
-  __syncthreads();
-  pass_a<false>(buf, ncol, LD, bhf, tid, nth);
-  __syncthreads();
-  pass_b<false>(buf, ncol, LD, tid, nth);
-  __syncthreads();
-  const float2* ph = a.phi + (cp * NC + v0) * (int64_t)L;
-  for (int u = tid; u < L; u += nth) {
-    const int fu = fpos(u);
-    for (int cb = 0; cb < ncol; cb += kBatch) {
-      float2 f[kBatch];
+  sched_fence();
+  const int dl = quad_delta(k);
+  dft67_reg<false>(x);
+  sched_fence();
+  quad_rotate<false>(x, T.tw, dl);
+  sched_fence();
+  quad_dft4<false>(x, k);
+  const float2* ph = a.phi + (cp * NC + c) * (int64_t)L;
+  int u = (201 * k) % L;
+  sched_fence();
 #pragma unroll
-      for (int k = 0; k < kBatch; ++k)
-        if (cb + k < ncol) f[k] = ph[(int64_t)(cb + k) * L + u];
+  for (int j0 = 0; j0 < P; j0 += kLoadChunk) {
+    float2 f[kLoadChunk];
 #pragma unroll
-      for (int k = 0; k < kBatch; ++k)
-        if (cb + k < ncol) {
-          float2* sl = buf + (cb + k) * LD + fu;
-          *sl = cmul(*sl, f[k]);
-        }
+    for (int jj = 0; jj < kLoadChunk && j0 + jj < P; ++jj) {
+      f[jj] = ph[u];
+      u += 68;
+      if (u >= L) u -= L;
     }
+    sched_fence();
+#pragma unroll
+    for (int jj = 0; jj < kLoadChunk && j0 + jj < P; ++jj) x[j0 + jj] = cmul(x[j0 + jj], f[jj]);
   }
-  __syncthreads();
-  pass_b<true>(buf, ncol, LD, tid, nth);
-  __syncthreads();
-  pass_a<true>(buf, ncol, LD, bhi, tid, nth);
-  __syncthreads();
-  for (int u = tid; u < L; u += nth) {
-    const int pu = pos_in(u);
-    for (int c = 0; c < ncol; ++c) Sp[(int64_t)c * L + u] = buf[c * LD + pu];
+  sched_fence();
+  quad_dft4<true>(x, k);
+  sched_fence();
+  int dl2 = dl;
+  asm volatile("" : "+v"(dl2));  // recompute the twiddle addresses instead of keeping the first pass's live
+  quad_rotate<true>(x, T.tw, dl2);
+  sched_fence();
+  dft67_reg<true>(x);
+  sched_fence();
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    col[4 * i] = x[i];
+    if (i % kLoadChunk == kLoadChunk - 1) sched_fence();
   }
 }
 
 // ---- row inverse: half spectra of rows 2t, 2t + 1 -> complex row -> inverse -> crop + store ----
 struct RowsInvArgs {
-  const float2* S;  // (P, NC, L)
-  float* out;       // (P, H, W)
-  const float2* bh; // 2 x 66 (the inverse-direction table is used)
-  int H, W, pad, act, nrp;
+  const float2* S;   // (P, NC, L)
+  float* out;        // (P, H, W)
+  int64_t nquad;
+  int H, W, pad;
+  uint32_t out_bytes;  // size of out (< 2^31)
 };
 
+template <bool GELU>
 __global__ void __launch_bounds__(256) k_pfa_rows_inv(RowsInvArgs a) {
-  extern __shared__ float2 sm[];
-  float2* bh = sm;
-  float2* buf = sm + 2 * RM;
-  const int tid = threadIdx.x, nth = blockDim.x;
-  const int64_t plane = blockIdx.y;
-  const int t0 = blockIdx.x * a.nrp;  // first row pair of the padded plane
-  const int nrp = min(a.nrp, L / 2 - t0);
-  for (int i = tid; i < RM; i += nth) bh[i] = a.bh[RM + i];
-  const float2* Sp = a.S + plane * (int64_t)NC * L;
-  // Z[v] = Ha[v] + i Hb[v] over the full row, with H[-v] = conj H[v]
-  for (int i0 = tid; i0 < nrp * L; i0 += kBatch * nth) {
-    float4 h[kBatch];  // (Ha, Hb) of rows 2t, 2t + 1 at bin |v|; row pair fastest across lanes
+  __shared__ QuadTabs T;
+  load_quad_tabs(T, 0, 0, 0);
+  const int k = threadIdx.x & 3;
+  const int64_t gq = (int64_t)blockIdx.x * (blockDim.x >> 2) + (threadIdx.x >> 2);
+  if (gq >= a.nquad) return;
+  const int64_t plane = gq / (L / 2);
+  const int t = (int)(gq - plane * (L / 2));
+  const float2* Sp = a.S + plane * (int64_t)NC * L + 2 * t;
+  // Z[v] = Ha[v] + i Hb[v] with H[-v] = conj H[v]
+  float2 x[P];
+  int v = (201 * k) % L;
+  // v = 0 or L/2 (real bins) only for j = 0 in lanes 0 and 2; lane 1 starts at v = 201 > L/2
+  const float sg0 = (k & 1) ? (k == 1 ? -1.f : 1.f) : 0.f;
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int idx = i0 + k * nth;
-      if (idx < nrp * L) {
-        const int v = idx / nrp, t = idx - v * nrp;
-        const int vv = v <= L / 2 ? v : L - v;
-        h[k] = *(const float4*)(Sp + (int64_t)vv * L + 2 * (t0 + t));
-      }
-    }
+  for (int j0 = 0; j0 < P; j0 += kLoadChunk) {
+    float4 h[kLoadChunk];
+    float sg[kLoadChunk];
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int idx = i0 + k * nth;
-      if (idx < nrp * L) {
-        const int v = idx / nrp, t = idx - v * nrp;
-        const bool lo = v <= L / 2;
-        const int vv = lo ? v : L - v;
-        float2 ha = make_float2(h[k].x, h[k].y), hb = make_float2(h[k].z, h[k].w);
-        if (vv == 0 || vv == L / 2) { ha.y = 0.f; hb.y = 0.f; }
-        if (!lo) { ha.y = -ha.y; hb.y = -hb.y; }
-        buf[t * LD + fpos(v)] = make_float2(ha.x - hb.y, ha.y + hb.x);
-      }
+    for (int jj = 0; jj < kLoadChunk && j0 + jj < P; ++jj) {
+      const bool lo = v <= L / 2;
+      h[jj] = *(const float4*)(Sp + (int64_t)(lo ? v : L - v) * L);
+      // imaginary parts: conjugated past L/2, zero at the real bins 0 and L/2
+      sg[jj] = j0 + jj == 0 ? sg0 : (lo ? 1.f : -1.f);
+      v += 68;
+      if (v >= L) v -= L;
     }
+    sched_fence();
+#pragma unroll
+    for (int jj = 0; jj < kLoadChunk && j0 + jj < P; ++jj)
+      x[j0 + jj] = make_float2(h[jj].x - sg[jj] * h[jj].w, sg[jj] * h[jj].y + h[jj].z);
   }
-  __syncthreads();
-  pass_b<true>(buf, nrp, LD, tid, nth);
-  __syncthreads();
-  pass_a<true>(buf, nrp, LD, bh, tid, nth);
-  __syncthreads();
-  float* op = a.out + plane * (int64_t)a.H * a.W;
-  for (int c = tid; c < a.W; c += nth) {
-    const int pc = pos_in(c + a.pad);
-    for (int rl = 0; rl < 2 * nrp; ++rl) {
-      const int row = 2 * t0 + rl - a.pad;
-      if (row < 0 || row >= a.H) continue;
-      const float2 z = buf[(rl >> 1) * LD + pc];
-      float v = (rl & 1) ? z.y : z.x;
-      if (a.act == CVN_ACT_GELU) v = gelu_fast(v);
-      op[(int64_t)row * a.W + c] = v;
+  sched_fence();
+  quad_dft4<true>(x, k);
+  sched_fence();
+  quad_rotate<true>(x, T.tw, quad_delta(k));
+  sched_fence();
+  dft67_reg<true>(x);
+  sched_fence();
+  const int sig = quad_sig(k);
+  const int r0 = 2 * t - a.pad, r1 = r0 + 1;
+  const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.out, a.out_bytes);
+  const bool wa = r0 >= 0 && r0 < a.H, wb = r1 >= 0 && r1 < a.H;
+  const uint32_t ba = (uint32_t)(((plane * a.H + r0) * a.W - a.pad + sig) * 4);
+  const uint32_t bb = ba + (uint32_t)(a.W * 4);
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int cc = 4 * i + sig - a.pad;
+    const bool in = cc >= 0 && cc < a.W;
+    float va = x[i].x, vb = x[i].y;
+    if (GELU) {
+      va = gelu_fast(va);
+      vb = gelu_fast(vb);
     }
+    bstore1(va, orr, in && wa ? ba + (uint32_t)(16 * i) : kDrop);
+    bstore1(vb, orr, in && wb ? bb + (uint32_t)(16 * i) : kDrop);
+    if (i % kLoadChunk == kLoadChunk - 1) sched_fence();
   }
 }
 
@@ -350,42 +462,33 @@ __global__ void __launch_bounds__(256) k_pfa_rows_inv(RowsInvArgs a) {
 
 // Host side --------------------------------------------------------------------------------------
 namespace {
-constexpr int kRowPairs = 16;  // row pairs (complex rows) per block: 4 x 16 = 64 DFT-67 items
-constexpr int kCols = 16;      // columns per block
-// Rader tables, the block's rows, and (row kernel) int16 column / row index tables
-size_t pfa_lds(int rows) {
-  return (size_t)(2 * pfa268::RM + rows * pfa268::LD) * sizeof(float2) + (2 * pfa268::L + 2 * rows) * sizeof(short);
-}
-bool g_pfa_attr = false;
+constexpr int kQuadsPerBlock = 64;  // 256 threads
 }  // namespace
 
-bool pfa268_applies(int h, int w, int s, const FftPlan& plan268) {
-  return h == pfa268::L && w == pfa268::L && s == 1 && plan268.nrad == 1 && plan268.rad[0].R == pfa268::P &&
-         plan268.rad[0].g == 2;
-}
+bool pfa268_applies(int h, int w, int s) { return h == pfa268::L && w == pfa268::L && s == 1; }
 
-// S: (P, NC, L) scratch; phi: (Cp, NC, L); bh: the 67-point Rader table pair (bf, bi) of the
-// plan tables of length 268.
+// S: (P, NC, L) scratch; phi: (Cp, NC, L).
 int pfa268_forward(const float* x, int64_t P, int64_t C, int64_t psf_batch, int H, int W, int pad, int mode, int act,
-                   const float2* phi, const float2* bh, float2* S, float* out, hipStream_t st) {
+                   const float2* phi, float2* S, float* out, hipStream_t st) {
   using namespace pfa268;
-  if (!g_pfa_attr) {
-    hipFuncSetAttribute((const void*)k_pfa_rows_fwd, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    hipFuncSetAttribute((const void*)k_pfa_cols, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    hipFuncSetAttribute((const void*)k_pfa_rows_inv, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    hipGetLastError();
-    g_pfa_attr = true;
-  }
-  const int nrb = (L / 2 + kRowPairs - 1) / kRowPairs;
-  RowsArgs ra{x, S, bh, H, W, pad, mode, kRowPairs};
-  hipLaunchKernelGGL(k_pfa_rows_fwd, dim3(nrb, (unsigned)P), dim3(4 * kRowPairs), pfa_lds(kRowPairs), st, ra);
+  const int64_t nrq = P * (L / 2), ncq = P * NC;
+  const int64_t nrb = (nrq + kQuadsPerBlock - 1) / kQuadsPerBlock, ncb = (ncq + kQuadsPerBlock - 1) / kQuadsPerBlock;
+  if (ncb > 0x7fffffff) return fail(CVN_ERR_UNSUPPORTED, "too many planes for the 268 path");
+  const int64_t s_bytes = P * NC * L * 8, o_bytes = P * (int64_t)H * W * 4;
+  if (s_bytes >= ((int64_t)1 << 31) || o_bytes >= ((int64_t)1 << 31))
+    return fail(CVN_ERR_UNSUPPORTED, "the 268 path addresses its buffers with 31-bit byte offsets");
+  RowsArgs ra{x, S, nrq, H, W, pad, mode, (uint32_t)s_bytes};
+  hipLaunchKernelGGL(k_pfa_rows_fwd, dim3((unsigned)nrb), dim3(4 * kQuadsPerBlock), 0, st, ra);
   int rc = check_launch("268 row pass");
   if (rc != CVN_OK) return rc;
-  ColsArgs ca{S, phi, bh, C, psf_batch, kCols};
-  hipLaunchKernelGGL(k_pfa_cols, dim3((NC + kCols - 1) / kCols, (unsigned)P), dim3(4 * kCols), pfa_lds(kCols), st, ca);
+  ColsArgs ca{S, phi, C, psf_batch, ncq};
+  hipLaunchKernelGGL(k_pfa_cols, dim3((unsigned)ncb), dim3(4 * kQuadsPerBlock), 0, st, ca);
   if ((rc = check_launch("268 column pass")) != CVN_OK) return rc;
-  RowsInvArgs ia{S, out, bh, H, W, pad, act, kRowPairs};
-  hipLaunchKernelGGL(k_pfa_rows_inv, dim3(nrb, (unsigned)P), dim3(4 * kRowPairs), pfa_lds(kRowPairs), st, ia);
+  RowsInvArgs ia{S, out, nrq, H, W, pad, (uint32_t)o_bytes};
+  if (act == CVN_ACT_GELU)
+    hipLaunchKernelGGL(k_pfa_rows_inv<true>, dim3((unsigned)nrb), dim3(4 * kQuadsPerBlock), 0, st, ia);
+  else
+    hipLaunchKernelGGL(k_pfa_rows_inv<false>, dim3((unsigned)nrb), dim3(4 * kQuadsPerBlock), 0, st, ia);
   return check_launch("268 inverse row pass");
 }
 

@@ -138,11 +138,10 @@ int fused_table(const float* psf, const float* bias, float eps, int64_t C, int64
 int fused_apply(const float* x, int64_t B, int64_t C, int H, int W, int64_t psf_batch, int pad, int mode, int act,
                 const void* table, float* out, hipStream_t st);
 // 268 x 268 planes at scale 1 (converse2d_pfa.hip): in-place prime-factor FFTs 268 = 4 * 67 with an
-// in-register Rader 67-point DFT.  plan268 is the generic plan of length 268 (its Rader table for 67
-// is reused); bh points at that table's forward / inverse FFT(b) / 66 pair.
-bool pfa268_applies(int h, int w, int s, const FftPlan& plan268);
+// in-register Rader 67-point DFT.
+bool pfa268_applies(int h, int w, int s);
 int pfa268_forward(const float* x, int64_t P, int64_t C, int64_t psf_batch, int H, int W, int pad, int mode, int act,
-                   const float2* phi, const float2* bh, float2* S, float* out, hipStream_t st);
+                   const float2* phi, float2* S, float* out, hipStream_t st);
 // CVN_DISABLE_FUSED=1 in the environment routes every call through the generic multi-pass path.
 bool fused_disabled();
 
