@@ -171,33 +171,51 @@ __device__ __forceinline__ void sched_fence() { asm volatile("" ::: "memory"); }
 // column order c = 4 i + sig(s), sig(s) = 3 s mod 4, so the quad's loads cover 4 adjacent columns;
 // register i then holds segment element m = (i + dl(s)) mod 67, dl(s) = 17 sig(s) mod 67 (a cyclic
 // rotation, undone by the twiddle W67^(dl j) on the 67-point DFT's output).  The 4-point DFT across
-// the segments runs across the quad's lanes through DPP quad permutes; afterwards lane k holds the
-// bins v = (201 k + 68 j) mod 268 (v = k mod 4, v = j mod 67) in register j.
+// the segments runs across the quad's lanes through DPP quad permutes, as a radix-2 decimation in
+// frequency, so its output is in bit-reversed lane order: afterwards lane k holds the bins
+// v = (201 br(k) + 68 j) mod 268 (v = br(k) mod 4, v = j mod 67) in register j, br = [0, 2, 1, 3].
+// The Hermitian partner -v of a bin then sits in lane [0, 1, 3, 2][k], register (67 - j) mod 67.
 __device__ __forceinline__ int quad_sig(int s) { return (3 * s) & 3; }
 __device__ __forceinline__ int quad_delta(int s) { return (17 * quad_sig(s)) % P; }
+__device__ __forceinline__ int quad_bin(int k) { return ((k & 1) << 1) | (k >> 1); }  // br(k)
 
 template <int CTRL>
 __device__ __forceinline__ float dppf(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 template <int CTRL>
 __device__ __forceinline__ float2 dpp2(float2 v) {
   return make_float2(dppf<CTRL>(v.x), dppf<CTRL>(v.y));
 }
-// quad_perm controls: broadcast lane 0 / 1 / 2 / 3 of the quad, and swap lanes 1 and 3
-constexpr int kQ0 = 0x00, kQ1 = 0x55, kQ2 = 0xAA, kQ3 = 0xFF, kSwap13 = 0x6C;
+// quad_perm controls: partner at distance 2 ([2, 3, 0, 1]), at distance 1 ([1, 0, 3, 2]), and the
+// Hermitian partner of the bit-reversed layout ([0, 1, 3, 2])
+constexpr int kX2 = 0x4E, kX1 = 0xB1, kHerm = 0xB4;
 
-// 4-point DFT across the quad for every register: lane k ends with sum_s W4^(+-k s) x_s.
+// y = (value of the partner lane) + sg * (own value): one multiply and one add with a DPP operand.
+template <int CTRL>
+__device__ __forceinline__ float2 quad_bfly(float2 v, float sg) {
+  return make_float2(dppf<CTRL>(v.x) + sg * v.x, dppf<CTRL>(v.y) + sg * v.y);
+}
+
+// 4-point DFT across the quad for every register, radix 2 in two steps.  Forward (decimation in
+// frequency, natural lane order in, bit-reversed out): a = x[s ^ 2] + (+-1) x[s] (minus in lanes 2,
+// 3), lane 3 times -i, then y = a[s ^ 1] + (+-1) a[s] (minus in lanes 1, 3).  Inverse (decimation in
+// time, bit-reversed in, natural out): the same steps in reverse order with +i.
 template <bool INV>
 __device__ __forceinline__ void quad_dft4(float2 (&x)[P], int k) {
-  const bool odd = k & 1, hi = k & 2;
+  const float s2 = (k & 2) ? -1.f : 1.f, s1 = (k & 1) ? -1.f : 1.f;
+  const bool l3 = k == 3;
 #pragma unroll
   for (int j = 0; j < P; ++j) {
-    const float2 a0 = dpp2<kQ0>(x[j]), a1 = dpp2<kQ1>(x[j]), a2 = dpp2<kQ2>(x[j]), a3 = dpp2<kQ3>(x[j]);
-    const float2 p = cadd(a0, a2), q = csub(a0, a2), r = cadd(a1, a3), w = csub(a1, a3);
-    const float2 rw = INV ? make_float2(-w.y, w.x) : make_float2(w.y, -w.x);  // +-i w
-    const float2 e = odd ? q : p, f = odd ? rw : r;
-    x[j] = hi ? csub(e, f) : cadd(e, f);
+    if (!INV) {
+      const float2 a = quad_bfly<kX2>(x[j], s2);
+      const float2 b = make_float2(l3 ? a.y : a.x, l3 ? -a.x : a.y);  // lane 3: -i a
+      x[j] = quad_bfly<kX1>(b, s1);
+    } else {
+      const float2 c = quad_bfly<kX1>(x[j], s1);
+      const float2 b = make_float2(l3 ? -c.y : c.x, l3 ? c.x : c.y);  // lane 3: +i c
+      x[j] = quad_bfly<kX2>(b, s2);
+    }
   }
 }
 
@@ -309,14 +327,13 @@ __global__ void __launch_bounds__(256) k_pfa_rows_fwd(RowsArgs a) {
   sched_fence();
   quad_dft4<false>(x, k);
   sched_fence();
-  // two real rows: Ya = (Z[v] + conj Z[-v]) / 2, Yb = (Z[v] - conj Z[-v]) / (2i); Z[-v] sits in lane
-  // (4 - k) mod 4, register (67 - j) mod 67
+  // two real rows: Ya = (Z[v] + conj Z[-v]) / 2, Yb = (Z[v] - conj Z[-v]) / (2i)
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.S, a.s_bytes);
   const uint32_t base = (uint32_t)((plane * NC * L + 2 * t) * 8);
-  int v = (201 * k) % L;
+  int v = (201 * quad_bin(k)) % L;
 #pragma unroll
   for (int j = 0; j < P; ++j) {
-    const float2 z = x[j], zm = dpp2<kSwap13>(x[(P - j) % P]);
+    const float2 z = x[j], zm = dpp2<kHerm>(x[(P - j) % P]);
     bstore4(make_float4(0.5f * (z.x + zm.x), 0.5f * (z.y - zm.y), 0.5f * (z.y + zm.y), 0.5f * (zm.x - z.x)), sr,
             v <= L / 2 ? base + (uint32_t)(v * L * 8) : kDrop);
     v += 68;
@@ -357,7 +374,7 @@ __global__ void __launch_bounds__(256) k_pfa_cols(ColsArgs a) {
   sched_fence();
   quad_dft4<false>(x, k);
   const float2* ph = a.phi + (cp * NC + c) * (int64_t)L;
-  int u = (201 * k) % L;
+  int u = (201 * quad_bin(k)) % L;
   sched_fence();
 #pragma unroll
   for (int j0 = 0; j0 < P; j0 += kLoadChunk) {
@@ -409,9 +426,10 @@ __global__ void __launch_bounds__(256) k_pfa_rows_inv(RowsInvArgs a) {
   const float2* Sp = a.S + plane * (int64_t)NC * L + 2 * t;
   // Z[v] = Ha[v] + i Hb[v] with H[-v] = conj H[v]
   float2 x[P];
-  int v = (201 * k) % L;
-  // v = 0 or L/2 (real bins) only for j = 0 in lanes 0 and 2; lane 1 starts at v = 201 > L/2
-  const float sg0 = (k & 1) ? (k == 1 ? -1.f : 1.f) : 0.f;
+  const int kb = quad_bin(k);
+  int v = (201 * kb) % L;
+  // v = 0 or L/2 (real bins) only for j = 0 with kb = 0 or 2; kb = 1 starts at v = 201 > L/2
+  const float sg0 = (kb & 1) ? (kb == 1 ? -1.f : 1.f) : 0.f;
 #pragma unroll
   for (int j0 = 0; j0 < P; j0 += kLoadChunk) {
     float4 h[kLoadChunk];
