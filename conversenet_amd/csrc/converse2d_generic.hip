@@ -69,6 +69,7 @@ struct PhiArgs {
   double eps;
   float2* phi;        // module: (Cp, NCs, Hs);  op: A (Cp, Ws, Hs)
   float2* kf;         // op only: K (Cp, Ws, Hs)
+  int q268;           // module at 268 x 268, scale 1: the 268 path's quad layout (pfa268_phi_index)
 };
 
 // P[b][i] = sum_j psf[i][j] exp(-2 pi i v_b (j - kw/2) / Ws), into LDS.
@@ -366,8 +367,8 @@ __global__ void __launch_bounds__(256) k_phi_tile(PhiArgs a, int op, int vc, int
         } else {
           const double2 hn = S > 1 ? dcmul(hH[u], hv) : make_double2(1.0, 0.0);
           const double2 t = dcmul(make_double2(k.x, -k.y), g);
-          a.phi[(cp * a.NCs + vb) * Hs + u] =
-              make_float2((float)((hn.x + t.x) * norm), (float)((hn.y + t.y) * norm));
+          const int64_t o = a.q268 ? pfa268_phi_index(cp, (int)vb, u) : (cp * a.NCs + vb) * Hs + u;
+          a.phi[o] = make_float2((float)((hn.x + t.x) * norm), (float)((hn.y + t.y) * norm));
         }
       }
     }
@@ -1194,11 +1195,12 @@ ModWs module_ws(const Geo& g, const PlanTabs& t) {
 }
 
 int launch_phi(const float* psf, const float* bias, float eps, const Geo& g, bool op, float2* phi,
-               float2* kf, hipStream_t st) {
+               float2* kf, hipStream_t st, bool q268 = false) {
   PhiArgs a;
   a.psf = psf; a.bias = bias; a.Cp = g.Cp; a.C = (int)g.C; a.kh = g.kh; a.kw = g.kw; a.s = g.s;
   a.h = g.h; a.w = g.w; a.Hs = g.Hs; a.Ws = g.Ws; a.NCs = g.NCs; a.eps = (double)eps;
   a.phi = phi; a.kf = kf;
+  a.q268 = q268 ? 1 : 0;
   a.nv0 = (!op && g.s == 1) ? g.NC : g.w;
   // tiled kernel (scales 1..4): about 2048 blocks, chunk size bounded by an LDS budget of 64 KiB
   if (g.s <= 4) {
@@ -1220,6 +1222,7 @@ int launch_phi(const float* psf, const float* bias, float eps, const Geo& g, boo
       return check_launch("transfer table");
     }
   }
+  if (q268) return fail(CVN_ERR_UNSUPPORTED, "268 transfer table needs the tiled kernel");
   const size_t lds = (size_t)g.s * g.kh * sizeof(double2);
   const int64_t blocks = g.Cp * a.nv0;
   if (blocks > 0x7fffffff) return fail(CVN_ERR_UNSUPPORTED, "too many transfer blocks");
@@ -1276,6 +1279,7 @@ namespace {
 // bias, eps and geometry, so callers may cache it across calls with unchanged weights.
 struct Route {
   bool fused;
+  bool pfa;  // 268 x 268 planes at scale 1: the 268 path (its table holds Phi in the quad layout)
   size_t table_bytes, scratch_bytes;
 };
 
@@ -1286,6 +1290,7 @@ int module_route(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, 
   size_t fws = 0;
   if (!fused_disabled() && kh <= 64 && fused_query(g->H, g->W, g->pad, g->s, g->Cp, &fws)) {
     r->fused = true;
+    r->pfa = false;
     r->table_bytes = fws;
     r->scratch_bytes = 0;
   } else {
@@ -1293,6 +1298,7 @@ int module_route(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, 
     if (!plan_tabs(*g, &t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
     const ModWs w = module_ws(*g, t);
     r->fused = false;
+    r->pfa = !fused_disabled() && pfa268_applies(g->h, g->w, g->s);
     r->table_bytes = w.S;
     r->scratch_bytes = w.total - w.S;
   }
@@ -1378,7 +1384,7 @@ extern "C" int cvn_converse2d_table_f32(const float* psf, int64_t psf_batch, int
   if (!plan_tabs(g, &t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
   const ModWs ws = module_ws(g, t);
   if ((rc = launch_plan_tabs(t, (char*)table + ws.tabs, st)) != CVN_OK) return rc;
-  return launch_phi(psf, bias, eps, g, false, (float2*)table, nullptr, st);
+  return launch_phi(psf, bias, eps, g, false, (float2*)table, nullptr, st, r.pfa);
 }
 
 extern "C" int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
@@ -1411,7 +1417,7 @@ extern "C" int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, in
   const char* tabs = (const char*)table + ws.tabs;
   float2* S = (float2*)(base + ws.S);
   float2* SH = (float2*)(base + ws.SH);
-  if (!fused_disabled() && pfa268_applies(g.h, g.w, g.s))
+  if (r.pfa)
     return pfa268_forward(x, g.P, g.C, g.Cp / g.C, g.H, g.W, g.pad, pad_mode, act, phi, S, out, st);
   if ((rc = launch_rows_fwd(x, g.P, g.H, g.W, g.pad, pad_mode, g.h, g.w, tabs + t.off[kTabW], S, st)) != CVN_OK)
     return rc;

@@ -346,7 +346,7 @@ __global__ void __launch_bounds__(256) k_pfa_rows_fwd(RowsArgs a) {
 // quad index g = plane * NC + column.
 struct ColsArgs {
   float2* S;          // (P, NC, L)
-  const float2* phi;  // (Cp, NC, L) natural order, 1/(L L) folded in
+  const float2* phi;  // (Cp, P, NC, 4) quad layout (pfa268_phi_index), 1/(L L) folded in
   int64_t C, psf_batch, nquad;
 };
 
@@ -373,18 +373,14 @@ __global__ void __launch_bounds__(256) k_pfa_cols(ColsArgs a) {
   quad_rotate<false>(x, T.tw, dl);
   sched_fence();
   quad_dft4<false>(x, k);
-  const float2* ph = a.phi + (cp * NC + c) * (int64_t)L;
-  int u = (201 * quad_bin(k)) % L;
+  // register j of lane k multiplies by Phi at u = 201 br(k) + 68 j, stored at [cp][j][c][k]
+  const float2* ph = a.phi + (cp * P * NC + c) * 4 + k;
   sched_fence();
 #pragma unroll
   for (int j0 = 0; j0 < P; j0 += kLoadChunk) {
     float2 f[kLoadChunk];
 #pragma unroll
-    for (int jj = 0; jj < kLoadChunk && j0 + jj < P; ++jj) {
-      f[jj] = ph[u];
-      u += 68;
-      if (u >= L) u -= L;
-    }
+    for (int jj = 0; jj < kLoadChunk && j0 + jj < P; ++jj) f[jj] = ph[(j0 + jj) * NC * 4];
     sched_fence();
 #pragma unroll
     for (int jj = 0; jj < kLoadChunk && j0 + jj < P; ++jj) x[j0 + jj] = cmul(x[j0 + jj], f[jj]);

@@ -140,6 +140,14 @@ int fused_apply(const float* x, int64_t B, int64_t C, int H, int W, int64_t psf_
 // 268 x 268 planes at scale 1 (converse2d_pfa.hip): in-place prime-factor FFTs 268 = 4 * 67 with an
 // in-register Rader 67-point DFT.
 bool pfa268_applies(int h, int w, int s);
+// Index of Phi(u, v) (row frequency u, half-spectrum column v) in the 268 path's transfer table:
+// (Cp, 67, 135, 4) = [psf plane][u mod 67][v][lane of the quad that holds bin u], so that the 16
+// quads of a wave read 512 contiguous bytes per register.  The lane holding u is br(u mod 4) with
+// br = [0, 2, 1, 3] (the bit-reversed output order of the quad's 4-point DFT).
+__host__ __device__ inline int64_t pfa268_phi_index(int64_t cp, int v, int u) {
+  const int r = u & 3;
+  return ((cp * 67 + u % 67) * 135 + v) * 4 + (((r & 1) << 1) | (r >> 1));
+}
 int pfa268_forward(const float* x, int64_t P, int64_t C, int64_t psf_batch, int H, int W, int pad, int mode, int act,
                    const float2* phi, float2* S, float* out, hipStream_t st);
 // CVN_DISABLE_FUSED=1 in the environment routes every call through the generic multi-pass path.
