@@ -68,6 +68,9 @@ int cvn_converse2d_fwd_f32(const float* x, int64_t B, int64_t C, int64_t H, int6
  * while weight and bias are unchanged, as the reference caches its OTF (converse2d.cpp:52-102).
  * cvn_converse2d_table_f32 writes the table; cvn_converse2d_apply_f32 runs the solve with it.  The
  * table depends on (psf, psf_batch, bias, eps, C, H, W, scale, pad) and, for psf_batch = B, on B.
+ * Its layout follows the kernels chosen for the geometry (fused single-kernel path, 268 path or
+ * generic passes; CVN_DISABLE_FUSED=1 in the environment selects the generic passes), so a table is
+ * applied under the same environment it was written in.
  * cvn_converse2d_fwd_f32 == table into workspace[0, align256(table_bytes)) + apply with the rest. */
 size_t cvn_converse2d_table_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch,
                                   int kh, int kw, int scale, int pad);
