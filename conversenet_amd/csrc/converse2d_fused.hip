@@ -616,12 +616,12 @@ int fused_table_run(const float* psf, const float* bias, float eps, int64_t C, i
 template <class P>
 int fused_apply_run(const float* x, int64_t B, int64_t C, int H, int W, int64_t psf_batch, int pad, int mode,
                     int act, const void* table, float* out, hipStream_t st) {
-  static bool attr = false;
-  if (!attr) {
-    hipFuncSetAttribute((const void*)k_converse2d_fused<P>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)P::LDS_BYTES);
-    attr = true;
-  }
+  static std::atomic<uint64_t> attr{0};
+  once_per_device(attr, [] {
+    (void)hipFuncSetAttribute((const void*)k_converse2d_fused<P>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)P::LDS_BYTES);
+    (void)hipGetLastError();
+  });
   const int64_t Cp = psf_batch * C;
   const float4* t4 = (const float4*)table;
   FusedArgs fa{x, t4, out, B, C, psf_batch, H, W, pad, mode, act};

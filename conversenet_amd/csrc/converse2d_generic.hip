@@ -1078,22 +1078,22 @@ namespace {
 constexpr int kThreads = 256;
 constexpr size_t kLdsLimit = 160 * 1024;
 
-bool g_attr_done = false;
+std::atomic<uint64_t> g_attr_done{0};
 void set_lds_attrs() {
-  if (g_attr_done) return;
-  hipFuncSetAttribute((const void*)k_rows_fwd, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
-  hipFuncSetAttribute((const void*)k_cols_module, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
-  hipFuncSetAttribute((const void*)k_cols_op, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
-  hipFuncSetAttribute((const void*)k_rows_inv, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
-  hipFuncSetAttribute((const void*)k_cols_bwd, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
-  hipFuncSetAttribute((const void*)k_phi_grad<1>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
-  hipFuncSetAttribute((const void*)k_phi_grad<2>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
-  hipFuncSetAttribute((const void*)k_phi_grad<3>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
-  hipFuncSetAttribute((const void*)k_phi_grad<4>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
-  hipFuncSetAttribute((const void*)k_psf_grad_a, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
-  hipFuncSetAttribute((const void*)k_psf_grad_b, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
-  hipGetLastError();
-  g_attr_done = true;
+  once_per_device(g_attr_done, [] {
+    (void)hipFuncSetAttribute((const void*)k_rows_fwd, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+    (void)hipFuncSetAttribute((const void*)k_cols_module, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+    (void)hipFuncSetAttribute((const void*)k_cols_op, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+    (void)hipFuncSetAttribute((const void*)k_rows_inv, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+    (void)hipFuncSetAttribute((const void*)k_cols_bwd, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+    (void)hipFuncSetAttribute((const void*)k_phi_grad<1>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+    (void)hipFuncSetAttribute((const void*)k_phi_grad<2>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+    (void)hipFuncSetAttribute((const void*)k_phi_grad<3>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+    (void)hipFuncSetAttribute((const void*)k_phi_grad<4>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+    (void)hipFuncSetAttribute((const void*)k_psf_grad_a, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+    (void)hipFuncSetAttribute((const void*)k_psf_grad_b, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+    (void)hipGetLastError();
+  });
 }
 
 // rows per block (even) for a row pass of length L

@@ -6,6 +6,7 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <atomic>
 #include <string>
 
 #include "../../include/converse2d.h"
@@ -152,5 +153,21 @@ int pfa268_forward(const float* x, int64_t P, int64_t C, int64_t psf_batch, int 
                    const float2* phi, float2* S, float* out, hipStream_t st);
 // CVN_DISABLE_FUSED=1 in the environment routes every call through the generic multi-pass path.
 bool fused_disabled();
+
+// Index of the current HIP device (0 if the query fails).
+inline int current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  return dev;
+}
+// Runs fn once per device for devices 0..63 (per-device launch attributes and occupancy queries).
+// Thread-safe; concurrent first calls on one device may both run fn, so fn must be idempotent.
+template <class F>
+void once_per_device(std::atomic<uint64_t>& done, F fn) {
+  const uint64_t bit = 1ull << (current_device() & 63);
+  if (done.load(std::memory_order_acquire) & bit) return;
+  fn();
+  done.fetch_or(bit, std::memory_order_release);
+}
 
 }  // namespace cvn

@@ -444,20 +444,22 @@ struct MlpTile {
   static constexpr int Q = 1, NW = 16;
 };
 
-// Persistent grid: as many blocks as fit on the device at once (occupancy query, cached per kernel),
-// at most one per tile.
+// Persistent grid: as many blocks as fit on the device at once (occupancy query, cached per kernel
+// and device), at most one per tile.
 template <typename K>
 unsigned persistent_grid(K kernel, int threads, int64_t ntiles) {
-  static int resident = 0;
-  if (resident == 0) {
-    int dev = 0, cus = 0, per_cu = 0;
-    hipGetDevice(&dev);
-    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kernel, threads, 0);
-    hipGetLastError();
-    resident = std::max(1, cus) * std::max(1, per_cu);
+  static std::atomic<int> resident[64];
+  const int dev = current_device() & 63;
+  int r = resident[dev].load(std::memory_order_relaxed);
+  if (r == 0) {
+    int cus = 0, per_cu = 0;
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, current_device());
+    (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kernel, threads, 0);
+    (void)hipGetLastError();
+    r = std::max(1, cus) * std::max(1, per_cu);
+    resident[dev].store(r, std::memory_order_relaxed);
   }
-  return (unsigned)std::min<int64_t>(ntiles, resident);
+  return (unsigned)std::min<int64_t>(ntiles, r);
 }
 
 template <int CIN, int COUT, bool LN>
