@@ -30,20 +30,21 @@ __device__ __forceinline__ float2 twid(float2 w) {  // table entry -> direction-
 
 // Exact-form GELU 0.5 x (1 + erf(x / sqrt 2)) with erf from Abramowitz & Stegun, Handbook of
 // Mathematical Functions, eq. 7.1.26: erf(z) = 1 - t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^{-z^2},
-// t = 1 / (1 + p z) for z >= 0 (odd extension), |error| <= 1.5e-7.  The GELU error is therefore
-// below 0.75e-7 |x|, under fp32 rounding of the surrounding arithmetic at the magnitudes seen here,
-// at about half the instructions of the library erff.
+// t = 1 / (1 + p z) for z >= 0 (odd extension), |error| <= 1.5e-7.  With z = |x| / sqrt 2 and
+// h = 0.5 |x| t P(t) e^{-x^2 / 2} this is GELU(x) = max(x, 0) - h for either sign of x (for x < 0,
+// 0.5 x (1 - (1 - 2h/|x|)) = -h), so the 0.5 folds into the coefficients and no 1 - erf
+// cancellation occurs.  Measured against the exact GELU in fp64 over [-12, 12]: |error| <= 3.3e-7,
+// at about 13 instructions (two of them the hardware reciprocal and exp2).
 __device__ __forceinline__ float gelu_fast(float x) {
-  const float z = fabsf(x) * 0.70710678118654752f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
-  float p = fmaf(1.061405429f, t, -1.453152027f);
-  p = fmaf(p, t, 1.421413741f);
-  p = fmaf(p, t, -0.284496736f);
-  p = fmaf(p, t, 0.254829592f);
+  const float a = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f * 0.70710678118654752f, a, 1.0f));
+  float p = fmaf(0.5f * 1.061405429f, t, 0.5f * -1.453152027f);
+  p = fmaf(p, t, 0.5f * 1.421413741f);
+  p = fmaf(p, t, 0.5f * -0.284496736f);
+  p = fmaf(p, t, 0.5f * 0.254829592f);
   p *= t;
-  const float e = __builtin_amdgcn_exp2f(-z * z * 1.4426950408889634f);
-  const float erf_abs = fmaf(-p, e, 1.0f);
-  return 0.5f * x * (1.0f + copysignf(erf_abs, x));
+  const float e = __builtin_amdgcn_exp2f((a * (-0.5f * 1.4426950408889634f)) * a);
+  return __builtin_amdgcn_fmed3f(x, 0.0f, __builtin_inff()) - (a * p) * e;
 }
 
 // Division by a block-uniform divisor d through a multiply-high with m = ceil(2^32 / d): exact for
