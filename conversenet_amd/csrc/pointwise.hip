@@ -381,6 +381,178 @@ __global__ void __launch_bounds__(64 * NW) k_ln_mlp_mfma(const float* x, int64_t
   }
 }
 
+// ConverseBlock tail in one kernel: y' = x + s1 (W0 t + b0) (the first branch's last 1x1 and its
+// residual), then  out = y' + s2 (W2 GELU(W1 LN(y') + b1) + b2)  (the second branch).  y' stays in
+// registers in the accumulator layout (lane group g holds channels 16 rb + 4 g + r of pixel block
+// j), which is the B-operand layout of the next layer's k-steps, so neither y' nor LN(y') reaches
+// memory.  out may alias x: every pixel's x is read by the lanes that later write it.
+template <int CIN, int C, int CM, int Q, int NW>
+__global__ void __launch_bounds__(64 * NW) k_conv_ln_mlp_mfma(const float* __restrict__ t, const float* x, int64_t HW,
+                                                          int64_t tpb, int64_t ntiles,
+                                                          const float* __restrict__ W0, const float* __restrict__ b0,
+                                                          const float* __restrict__ s1,
+                                                          const float* __restrict__ lw, const float* __restrict__ lb,
+                                                          float eps, const float* __restrict__ W1,
+                                                          const float* __restrict__ b1, const float* __restrict__ W2,
+                                                          const float* __restrict__ b2,
+                                                          const float* __restrict__ s2, float* y) {
+  constexpr int LD0 = C + 16;  // W0t[k][i], k < CIN, i < C; read at (4 ks + g) LD0 + 16 rb + j
+  constexpr int LD1 = CM + 4;  // W1t[k][i], k < C, i < CM; read at (16 rb + 4 g + r) LD1 + 16 ob + j
+  constexpr int LD2 = C + 4;   // W2t[k][i], k < CM, i < C; read at (16 rb + 4 g + r) LD2 + 16 ob + j
+  __shared__ float W0t[CIN * LD0];
+  __shared__ float W1t[C * LD1];
+  __shared__ float W2t[CM * LD2];
+  __shared__ float prm[6 * C + CM];  // b0, s1, LN weight, LN bias, b2, s2, b1
+  stage_wt<C, CIN, LD0>(W0, W0t);
+  stage_wt<CM, C, LD1>(W1, W1t);
+  stage_wt<C, CM, LD2>(W2, W2t);
+  stage_vec<C>(b0, 0.f, prm);
+  stage_vec<C>(s1, 1.f, prm + C);
+  stage_vec<C>(lw, 1.f, prm + 2 * C);
+  stage_vec<C>(lb, 0.f, prm + 3 * C);
+  stage_vec<C>(b2, 0.f, prm + 4 * C);
+  stage_vec<C>(s2, 1.f, prm + 5 * C);
+  stage_vec<CM>(b1, 0.f, prm + 6 * C);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, j = lane & 15;
+  const uint32_t xoff = (uint32_t)(((int64_t)g * HW + Q * j) * 4);
+  const uint32_t yoff = (uint32_t)(((int64_t)4 * g * HW + Q * j) * 4);
+  const float inv = 1.0f / (float)C;
+  for (int64_t tt = blockIdx.x; tt < ntiles; tt += gridDim.x) {
+    mem_fence_sched();
+    const int64_t hw = opaque_stride(HW);
+    int64_t b;
+    const int64_t pw = tile_px(tt, tpb, Q, NW, wave, &b);
+    const bool inb = pw + Q * j < hw;
+    // first branch's last layer: acc = W0 t
+    v4f acc[C / 16][Q];
+    {
+      float tv[CIN / 4][Q];
+      load_tile<CIN, Q>(t + b * CIN * hw + pw, hw, inb, xoff, tv);
+      zero_acc<C, Q>(acc);
+      gemm_tile<CIN, C, Q>(tv, W0t, LD0, g, j, acc);
+    }
+    // y' = x + s1 (acc + b0), channel 16 rb + 4 g + r; x read in the same layout
+    const float* xw = x + b * C * hw + pw;
+#pragma unroll
+    for (int rb = 0; rb < C / 16; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int o = 16 * rb + 4 * g + r;
+        float rr[Q];
+        if (inb) {
+          ldq<Q>(at_off(xw + (int64_t)(16 * rb + r) * hw, yoff), rr);
+        } else {
+#pragma unroll
+          for (int q = 0; q < Q; ++q) rr[q] = 0.f;
+        }
+        const float bo = prm[o], sc = prm[C + o];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) acc[rb][q][r] = fmaf(sc, acc[rb][q][r] + bo, rr[q]);
+      }
+    // LayerNorm of y' over its C channels (16 per lane, the rest in lanes j + 16, j + 32, j + 48)
+    v4f xn[C / 16][Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      float su = 0.f;
+#pragma unroll
+      for (int rb = 0; rb < C / 16; ++rb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) su += acc[rb][q][r];
+      su += __shfl_xor(su, 16);
+      su += __shfl_xor(su, 32);
+      const float u = su * inv;
+      float va = 0.f;
+#pragma unroll
+      for (int rb = 0; rb < C / 16; ++rb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float d = acc[rb][q][r] - u;
+          va = fmaf(d, d, va);
+        }
+      va += __shfl_xor(va, 16);
+      va += __shfl_xor(va, 32);
+      const float rs = 1.0f / sqrtf(va * inv + eps);
+#pragma unroll
+      for (int rb = 0; rb < C / 16; ++rb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int o = 16 * rb + 4 * g + r;
+          xn[rb][q][r] = fmaf(prm[2 * C + o] * rs, acc[rb][q][r] - u, prm[3 * C + o]);
+        }
+    }
+    // hidden = GELU(W1 xn + b1): k-step kk = 4 rb + r, lane group g supplies channel 16 rb + 4 g + r
+    v4f h[CM / 16][Q];
+    zero_acc<CM, Q>(h);
+    {
+      float a[2][CM / 16];
+#pragma unroll
+      for (int ob = 0; ob < CM / 16; ++ob) a[0][ob] = W1t[(4 * g) * LD1 + j + 16 * ob];
+#pragma unroll
+      for (int kk = 0; kk < C / 4; ++kk) {
+        const int rb = kk >> 2, r = kk & 3;
+        if (kk + 1 < C / 4) {
+          const int rn = (kk + 1) >> 2, sn = (kk + 1) & 3;
+          const float* wk = W1t + (16 * rn + 4 * g + sn) * LD1 + j;
+#pragma unroll
+          for (int ob = 0; ob < CM / 16; ++ob) a[(kk + 1) & 1][ob] = wk[16 * ob];
+        }
+#pragma unroll
+        for (int ob = 0; ob < CM / 16; ++ob)
+#pragma unroll
+          for (int q = 0; q < Q; ++q) h[ob][q] = mfma4(a[kk & 1][ob], xn[rb][q][r], h[ob][q]);
+        mem_fence_sched();
+      }
+    }
+#pragma unroll
+    for (int rb = 0; rb < CM / 16; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float bo = prm[6 * C + 16 * rb + 4 * g + r];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) h[rb][q][r] = gelu_f(h[rb][q][r] + bo);
+      }
+    // out = y' + s2 (W2 hidden + b2)
+    v4f acc2[C / 16][Q];
+    zero_acc<C, Q>(acc2);
+    {
+      float a[2][C / 16];
+#pragma unroll
+      for (int ob = 0; ob < C / 16; ++ob) a[0][ob] = W2t[(4 * g) * LD2 + j + 16 * ob];
+#pragma unroll
+      for (int kk = 0; kk < CM / 4; ++kk) {
+        const int rb = kk >> 2, r = kk & 3;
+        if (kk + 1 < CM / 4) {
+          const int rn = (kk + 1) >> 2, sn = (kk + 1) & 3;
+          const float* wk = W2t + (16 * rn + 4 * g + sn) * LD2 + j;
+#pragma unroll
+          for (int ob = 0; ob < C / 16; ++ob) a[(kk + 1) & 1][ob] = wk[16 * ob];
+        }
+#pragma unroll
+        for (int ob = 0; ob < C / 16; ++ob)
+#pragma unroll
+          for (int q = 0; q < Q; ++q) acc2[ob][q] = mfma4(a[kk & 1][ob], h[rb][q][r], acc2[ob][q]);
+        mem_fence_sched();
+      }
+    }
+    if (inb) {
+      float* yw = y + b * C * hw + pw;
+#pragma unroll
+      for (int rb = 0; rb < C / 16; ++rb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int o = 16 * rb + 4 * g + r;
+          const float bo = prm[4 * C + o], sc = prm[5 * C + o];
+          float v[Q];
+#pragma unroll
+          for (int q = 0; q < Q; ++q) v[q] = fmaf(sc, acc2[rb][q][r] + bo, acc[rb][q][r]);
+          stq<Q>(at_off(yw + (int64_t)(16 * rb + r) * hw, yoff), v);
+        }
+    }
+  }
+}
+
 // Plain VALU 1x1 conv for channel counts / sizes the MFMA tiles do not cover (e.g. 1 or 3 channels,
 // or pixel counts that are not a multiple of 4).  Thread = one pixel and a group of kOutGroup
 // output channels (grid z); each input channel value is loaded once and feeds the whole group.
@@ -486,6 +658,18 @@ int launch_mlp(const float* x, int64_t B, int64_t HW, const float* ln_w, const f
   return check_launch("fused LN-MLP branch");
 }
 
+template <int CIN, int C, int CM>
+int launch_tail(const float* t, const float* x, int64_t B, int64_t HW, const float* w0, const float* b0,
+                const float* s1, const float* ln_w, const float* ln_b, float ln_eps, const float* w1, const float* b1,
+                const float* w2, const float* b2, const float* s2, float* y, hipStream_t st) {
+  constexpr int Q = 1, NW = 16;
+  const int64_t tpb = (HW + 16 * NW * Q - 1) / (16 * NW * Q), ntiles = B * tpb;
+  auto kern = k_conv_ln_mlp_mfma<CIN, C, CM, Q, NW>;
+  hipLaunchKernelGGL(kern, dim3(persistent_grid(kern, 64 * NW, ntiles)), dim3(64 * NW), 0, st, t, x, HW, tpb,
+                     ntiles, w0, b0, s1, ln_w, ln_b, ln_eps, w1, b1, w2, b2, s2, y);
+  return check_launch("fused block tail");
+}
+
 template <bool LN>
 int dispatch_mfma(int64_t Cin, int64_t Cout, const float* x, int64_t B, int64_t HW, const float* W,
                   const float* bias, const float* lw, const float* lb, float eps, int act, const float* residual,
@@ -588,4 +772,24 @@ extern "C" int cvn_ln_mlp_residual_f32(const float* x, int64_t B, int64_t C, int
   if (C == 32 && Cmid == 64)
     return launch_mlp<32, 64>(x, B, HW, ln_w, ln_b, ln_eps, w1, b1, w2, b2, res_scale, y, st);
   return fail(CVN_ERR_UNSUPPORTED, "fused branch supports (C, Cmid) in {(64,128), (32,64)}");
+}
+
+extern "C" int cvn_conv_ln_mlp_residual_f32(const float* t, int64_t B, int64_t Ct, int64_t HW, const float* w0,
+                                            const float* b0, const float* res_scale1, const float* x, int64_t C,
+                                            const float* ln_w, const float* ln_b, float ln_eps, const float* w1,
+                                            const float* b1, int64_t Cmid, const float* w2, const float* b2,
+                                            const float* res_scale2, float* y, cvn_stream_t stream) {
+  if (!t || !w0 || !b0 || !x || !ln_w || !ln_b || !w1 || !b1 || !w2 || !b2 || !y)
+    return fail(CVN_ERR_ARG, "null pointer");
+  if (B < 0 || HW < 0) return fail(CVN_ERR_ARG, "bad shape");
+  if (B > 65535) return fail(CVN_ERR_UNSUPPORTED, "batch exceeds 65535");
+  if (t == y) return fail(CVN_ERR_ARG, "the output may alias x, not t");
+  if (B == 0 || HW == 0) return CVN_OK;
+  if (HW % 4 != 0 || HW > kMaxMfmaHW || !aligned16(t) || !aligned16(x) || !aligned16(y))
+    return fail(CVN_ERR_UNSUPPORTED, "fused tail needs HW %% 4 == 0, HW <= 2^26 and 16-byte aligned buffers");
+  hipStream_t st = (hipStream_t)stream;
+  if (Ct == 128 && C == 64 && Cmid == 128)
+    return launch_tail<128, 64, 128>(t, x, B, HW, w0, b0, res_scale1, ln_w, ln_b, ln_eps, w1, b1, w2, b2,
+                                     res_scale2, y, st);
+  return fail(CVN_ERR_UNSUPPORTED, "fused tail supports (Ct, C, Cmid) = (128, 64, 128)");
 }

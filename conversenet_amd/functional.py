@@ -303,6 +303,30 @@ def ln_mlp_residual(x, ln_w, ln_b, ln_eps, w1, b1, w2, b2, res_scale=None, out=N
     return y
 
 
+TAIL_SHAPES = {(128, 64, 128)}  # (Ct, C, Cmid) of cvn_conv_ln_mlp_residual_f32
+
+
+def conv_ln_mlp_residual(t, x, w0, b0, ln_w, ln_b, ln_eps, w1, b1, w2, b2, res_scale1=None, res_scale2=None,
+                         out=None):
+    """ConverseBlock tail: y' = x + res_scale1 (W0 t + b0); y' + res_scale2 (W2 GELU(W1 LN(y') + b1) + b2)."""
+    lib = _lib.load()
+    _need_hip(t, x, w0, b0, w1, b1, w2, b2, res_scale1, res_scale2)
+    t = t.contiguous()
+    x = x.contiguous()
+    B, Ct, H, W = t.shape
+    C = x.shape[1]
+    W0, W1, W2 = _wmat(w0), _wmat(w1), _wmat(w2)
+    y = out if out is not None else torch.empty_like(x)
+    rc = lib.cvn_conv_ln_mlp_residual_f32(
+        t.data_ptr(), B, Ct, H * W, W0.data_ptr(), b0.contiguous().data_ptr(),
+        res_scale1.contiguous().data_ptr() if res_scale1 is not None else None, x.data_ptr(), C,
+        ln_w.contiguous().data_ptr(), ln_b.contiguous().data_ptr(), float(ln_eps), W1.data_ptr(),
+        b1.contiguous().data_ptr(), W1.shape[0], W2.data_ptr(), b2.contiguous().data_ptr(),
+        res_scale2.contiguous().data_ptr() if res_scale2 is not None else None, y.data_ptr(), _stream(x.device))
+    _lib.check(rc, "conv_ln_mlp_residual")
+    return y
+
+
 def copy_(dst, src):
     """Plain device copy through the library (HBM calibration kernel)."""
     lib = _lib.load()

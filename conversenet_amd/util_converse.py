@@ -230,10 +230,15 @@ def _fused_block_forward(blk, x, alpha1=None, alpha2=None):
     cv.biaseps = None  # read lazily from the current bias
     t = functional.converse2d_fused(t, cv.weight, cv.bias.reshape(-1), cv.scale, cv.padding, cv.padding_mode,
                                     cv.eps, act="gelu")
-    x = functional.conv1x1(t, c15.weight, c15.bias, residual=x,
-                           res_scale=alpha1.reshape(-1) if alpha1 is not None else None)
+    s1 = alpha1.reshape(-1) if alpha1 is not None else None
+    s2 = alpha2.reshape(-1) if alpha2 is not None else None
+    if (mid, C, c21.out_channels) in functional.TAIL_SHAPES and t.data_ptr() % 16 == 0 and x.data_ptr() % 16 == 0:
+        # last 1x1 + residual and the LN-MLP branch in one kernel (the intermediate stays on chip)
+        return functional.conv_ln_mlp_residual(t, x, c15.weight, c15.bias, ln2.weight, ln2.bias, ln2.eps,
+                                               c21.weight, c21.bias, c23.weight, c23.bias, s1, s2)
+    x = functional.conv1x1(t, c15.weight, c15.bias, residual=x, res_scale=s1)
     return functional.ln_mlp_residual(x, ln2.weight, ln2.bias, ln2.eps, c21.weight, c21.bias, c23.weight, c23.bias,
-                                      res_scale=alpha2.reshape(-1) if alpha2 is not None else None, out=x)
+                                      res_scale=s2, out=x)
 
 
 def _block_params(blk):

@@ -105,6 +105,40 @@ def test_ln_mlp_residual(C, mid, alpha):
     assert np.abs(got - ref).max() <= TOL
 
 
+@pytest.mark.parametrize("alpha", [False, True])
+@pytest.mark.parametrize("inplace", [False, True])
+def test_conv_ln_mlp_residual_tail(alpha, inplace):
+    """ConverseBlock tail in one kernel: x + s1 (W0 t + b0), then its LN-MLP branch and residual
+    (util_converse.py:279-293, :309-323); against the oracle and the two-kernel sequence."""
+    from conversenet_amd import functional as Fh
+    rng = seeded("tail", alpha, inplace)
+    B, C, Ct, mid, H, W = 2, 64, 128, 128, 20, 26  # 520 pixels: a partial last tile
+    t = rng.standard_normal((B, Ct, H, W)).astype(np.float32)
+    x = rng.standard_normal((B, C, H, W)).astype(np.float32)
+    w0 = (rng.standard_normal((C, Ct, 1, 1)) / np.sqrt(Ct)).astype(np.float32)
+    b0 = rng.standard_normal(C).astype(np.float32)
+    lw, lb = rng.standard_normal(C).astype(np.float32), rng.standard_normal(C).astype(np.float32)
+    w1 = (rng.standard_normal((mid, C, 1, 1)) / np.sqrt(C)).astype(np.float32)
+    b1 = rng.standard_normal(mid).astype(np.float32)
+    w2 = (rng.standard_normal((C, mid, 1, 1)) / np.sqrt(mid)).astype(np.float32)
+    b2 = rng.standard_normal(C).astype(np.float32)
+    s1 = rng.standard_normal(C).astype(np.float32) if alpha else None
+    s2 = rng.standard_normal(C).astype(np.float32) if alpha else None
+    xt = _t(x)
+    got = _n(Fh.conv_ln_mlp_residual(_t(t), xt, _t(w0), _t(b0), _t(lw), _t(lb), 1e-5, _t(w1), _t(b1), _t(w2),
+                                     _t(b2), _t(s1) if alpha else None, _t(s2) if alpha else None,
+                                     out=xt if inplace else None))
+    u = O.conv1x1(t, w0, b0)
+    y1 = (s1[None, :, None, None] * u if alpha else u) + x
+    v = O.conv1x1(O.gelu(O.conv1x1(O.layernorm_cf(y1, lw, lb, 1e-5), w1, b1)), w2, b2)
+    ref = (s2[None, :, None, None] * v if alpha else v) + y1
+    assert np.abs(got - ref).max() <= TOL
+    two = Fh.conv1x1(_t(t), _t(w0), _t(b0), residual=_t(x), res_scale=_t(s1) if alpha else None)
+    two = _n(Fh.ln_mlp_residual(two, _t(lw), _t(lb), 1e-5, _t(w1), _t(b1), _t(w2), _t(b2),
+                                res_scale=_t(s2) if alpha else None))
+    assert np.abs(got - two).max() <= TOL
+
+
 # ------------------------------------------------------------------------------------------------
 # a15 ConverseBlock / ConverseBlockAlphaVariant (fused block path on the GPU)
 # ------------------------------------------------------------------------------------------------
