@@ -287,9 +287,10 @@ def bench_backward(torch, Fh, dev, x, w, bias, c, iters):
 
 
 def bench_block_pointwise(torch, Fh, dev, iters):
-    """The three channel-mixing kernels of one ConverseBlockAlphaVariant at the Converse-USRNet body
-    shape (B4 C64 256x256, hidden 128): LN + 1x1 64->128 + GELU, 1x1 128->64 + alpha-scaled residual,
-    and the fused LN -> 1x1 -> GELU -> 1x1 -> residual branch.  Bytes are the algorithmic HBM bytes
+    """The channel-mixing kernels of one ConverseBlockAlphaVariant at the Converse-USRNet body shape
+    (B4 C64 256x256, hidden 128): LN + 1x1 64->128 + GELU, 1x1 128->64 + alpha-scaled residual, the
+    fused LN -> 1x1 -> GELU -> 1x1 -> residual branch, and the last two as the one tail kernel the
+    blocks run.  Bytes are the algorithmic HBM bytes
     (each activation read or written once), FLOPs the 1x1 products (2 per multiply-add)."""
     B, C, H, W = 4, 64, 256, 256
     npx = B * H * W
@@ -310,6 +311,10 @@ def bench_block_pointwise(torch, Fh, dev, iters):
                                     4 * npx * (2 * C + C + C), 2 * npx * C * 2 * C),
         "ln_mlp_64_128_residual": (lambda: Fh.ln_mlp_residual(x, lw, lb, 1e-5, w1, b1, w2, b2, res_scale=al, out=y),
                                    4 * npx * 2 * C, 4 * npx * C * 2 * C),
+        # the last two in one kernel (what the blocks run): reads h and x, writes the block output
+        "tail_conv1x1_128_64_ln_mlp": (lambda: Fh.conv_ln_mlp_residual(h, x, w2, b2, lw, lb, 1e-5, w1, b1, w2, b2,
+                                                                       al, al, out=y),
+                                       4 * npx * (2 * C + C + C), 6 * npx * C * 2 * C),
     }
     out = {"workload": "ConverseBlockAlphaVariant channel mixing, B4 C64 256x256, hidden 128, fp32"}
     for name, (fn, nbytes, flops) in cases.items():
