@@ -7,7 +7,7 @@ checkpoints load with strict=True.  The 1x1 head (1->64) and tail (64->1) run on
 import torch.nn as nn
 
 from . import functional
-from .util_converse import ConverseBlock, _hip_eligible
+from .util_converse import ConverseBlock, _hip_eligible, run_blocks
 
 
 class ConverseDnCNN(nn.Module):
@@ -31,7 +31,7 @@ class ConverseDnCNN(nn.Module):
         h, t = self.m_head[0], self.m_tail[0]
         if _hip_eligible(x, h.weight, h.bias, t.weight, t.bias):
             x = functional.conv1x1(x, h.weight, h.bias)
-            x = self.m_body(x)
+            x = run_blocks(self.m_body, x)
             return functional.conv1x1(x, t.weight, t.bias)
         x = self.m_head(x)
         x = self.m_body(x)

@@ -10,7 +10,8 @@ import torch
 import torch.nn as nn
 
 from . import composite, functional
-from .util_converse import _hip_grad_eligible, ConverseBlock, ConverseBlockAlphaVariant, _hip_eligible, sequential
+from .util_converse import (_hip_grad_eligible, ConverseBlock, ConverseBlockAlphaVariant, _hip_eligible, run_blocks,
+                            sequential)
 
 
 class MultiConverseBlock(nn.Module):
@@ -20,7 +21,7 @@ class MultiConverseBlock(nn.Module):
                                    for _ in range(num_blocks)])
 
     def forward(self, x):
-        return self.m_body(x)
+        return run_blocks(self.m_body, x)
 
 
 class MultiConverseBlockAlphaVariant(nn.Module):
@@ -30,7 +31,7 @@ class MultiConverseBlockAlphaVariant(nn.Module):
                                                              padding_mode) for _ in range(num_blocks)])
 
     def forward(self, x):
-        return self.m_body(x)
+        return run_blocks(self.m_body, x)
 
 
 class ConvReverseDataNet(nn.Module):

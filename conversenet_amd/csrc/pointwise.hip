@@ -385,56 +385,147 @@ __global__ void __launch_bounds__(64 * NW) k_ln_mlp_mfma(const float* x, int64_t
 // residual), then  out = y' + s2 (W2 GELU(W1 LN(y') + b1) + b2)  (the second branch).  y' stays in
 // registers in the accumulator layout (lane group g holds channels 16 rb + 4 g + r of pixel block
 // j), which is the B-operand layout of the next layer's k-steps, so neither y' nor LN(y') reaches
-// memory.  out may alias x: every pixel's x is read by the lanes that later write it.
-template <int CIN, int C, int CM, int Q, int NW>
-__global__ void __launch_bounds__(64 * NW) k_conv_ln_mlp_mfma(const float* __restrict__ t, const float* x, int64_t HW,
-                                                          int64_t tpb, int64_t ntiles,
-                                                          const float* __restrict__ W0, const float* __restrict__ b0,
-                                                          const float* __restrict__ s1,
-                                                          const float* __restrict__ lw, const float* __restrict__ lb,
-                                                          float eps, const float* __restrict__ W1,
-                                                          const float* __restrict__ b1, const float* __restrict__ W2,
-                                                          const float* __restrict__ b2,
-                                                          const float* __restrict__ s2, float* y) {
-  constexpr int LD0 = C + 16;  // W0t[k][i], k < CIN, i < C; read at (4 ks + g) LD0 + 16 rb + j
-  constexpr int LD1 = CM + 4;  // W1t[k][i], k < C, i < CM; read at (16 rb + 4 g + r) LD1 + 16 ob + j
-  constexpr int LD2 = C + 4;   // W2t[k][i], k < CM, i < C; read at (16 rb + 4 g + r) LD2 + 16 ob + j
+// memory.  out may alias x: every pixel's x is read by the lanes that later write it.  With HEAD,
+// the next block's first layer follows on the same registers: th = GELU(Wh LNh(out) + bh)
+// (CIN channels), so the next block does not read `out` again before its Converse2D.
+struct TailArgs {
+  const float* t;  // (B, CIN, HW)
+  const float* x;  // (B, C, HW)
+  int64_t HW, tpb, ntiles;
+  const float *W0, *b0, *s1, *lw, *lb, *W1, *b1, *W2, *b2, *s2;
+  float eps;
+  float* y;  // (B, C, HW)
+  const float *hlw, *hlb, *Wh, *bh;  // HEAD: next block's LayerNorm and 1x1 (CIN x C)
+  float heps;
+  float* th;  // HEAD: (B, CIN, HW)
+};
+
+// acc[ob][q] += W[16 ob + j][k] * v[k] over the k-steps kk = 4 rb + r whose B operand is register r of
+// row block rb of v (lane group g supplies channel 16 rb + 4 g + r): the first layer's accumulator
+// layout fed to the next layer.  Wt[k * LD + i] = W[i][k].
+template <int K, int N, int Q>
+__device__ __forceinline__ void gemm_from_acc(const v4f (&v)[K / 16][Q], const float* Wt, int ld, int g, int j,
+                                              v4f (&acc)[N / 16][Q]) {
+  float a[2][N / 16];
+#pragma unroll
+  for (int ob = 0; ob < N / 16; ++ob) a[0][ob] = Wt[(4 * g) * ld + j + 16 * ob];
+#pragma unroll
+  for (int kk = 0; kk < K / 4; ++kk) {
+    const int rb = kk >> 2, r = kk & 3;
+    if (kk + 1 < K / 4) {
+      const int rn = (kk + 1) >> 2, sn = (kk + 1) & 3;
+      const float* wk = Wt + (16 * rn + 4 * g + sn) * ld + j;
+#pragma unroll
+      for (int ob = 0; ob < N / 16; ++ob) a[(kk + 1) & 1][ob] = wk[16 * ob];
+    }
+#pragma unroll
+    for (int ob = 0; ob < N / 16; ++ob)
+#pragma unroll
+      for (int q = 0; q < Q; ++q) acc[ob][q] = mfma4(a[kk & 1][ob], v[rb][q][r], acc[ob][q]);
+    mem_fence_sched();
+  }
+}
+
+// LayerNorm over the C channels of v, held in the accumulator layout (16 per lane for C = 64; the
+// other lane groups of the same pixel block are lanes j + 16, j + 32, j + 48).
+template <int C, int Q>
+__device__ __forceinline__ void ln_acc(const v4f (&v)[C / 16][Q], const float* w, const float* bb, float eps, int g,
+                                       v4f (&out)[C / 16][Q]) {
+  const float inv = 1.0f / (float)C;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    float su = 0.f;
+#pragma unroll
+    for (int rb = 0; rb < C / 16; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) su += v[rb][q][r];
+    su += __shfl_xor(su, 16);
+    su += __shfl_xor(su, 32);
+    const float u = su * inv;
+    float va = 0.f;
+#pragma unroll
+    for (int rb = 0; rb < C / 16; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float d = v[rb][q][r] - u;
+        va = fmaf(d, d, va);
+      }
+    va += __shfl_xor(va, 16);
+    va += __shfl_xor(va, 32);
+    const float rs = 1.0f / sqrtf(va * inv + eps);
+#pragma unroll
+    for (int rb = 0; rb < C / 16; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int o = 16 * rb + 4 * g + r;
+        out[rb][q][r] = fmaf(w[o] * rs, v[rb][q][r] - u, bb[o]);
+      }
+  }
+}
+
+// Stores an accumulator-layout tile (channel 16 rb + 4 g + r, Q consecutive pixels per lane).
+template <int N, int Q>
+__device__ __forceinline__ void store_acc(const v4f (&v)[N / 16][Q], float* yw, int64_t hw, uint32_t yoff) {
+#pragma unroll
+  for (int rb = 0; rb < N / 16; ++rb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float o[Q];
+#pragma unroll
+      for (int q = 0; q < Q; ++q) o[q] = v[rb][q][r];
+      stq<Q>(at_off(yw + (int64_t)(16 * rb + r) * hw, yoff), o);
+    }
+}
+
+template <int CIN, int C, int CM, int Q, int NW, bool HEAD>
+__global__ void __launch_bounds__(64 * NW) k_conv_ln_mlp_mfma(TailArgs a) {
+  constexpr int LD0 = C + 16;   // W0t[k][i], k < CIN, i < C; read at (4 ks + g) LD0 + 16 rb + j
+  constexpr int LD1 = CM + 4;   // W1t[k][i], k < C, i < CM; read at (16 rb + 4 g + r) LD1 + 16 ob + j
+  constexpr int LD2 = C + 4;    // W2t[k][i], k < CM, i < C
+  constexpr int LDH = CIN + 4;  // Wht[k][i], k < C, i < CIN
+  constexpr int NP = 6 * C + CM + (HEAD ? 2 * C + CIN : 0);
   __shared__ float W0t[CIN * LD0];
   __shared__ float W1t[C * LD1];
   __shared__ float W2t[CM * LD2];
-  __shared__ float prm[6 * C + CM];  // b0, s1, LN weight, LN bias, b2, s2, b1
-  stage_wt<C, CIN, LD0>(W0, W0t);
-  stage_wt<CM, C, LD1>(W1, W1t);
-  stage_wt<C, CM, LD2>(W2, W2t);
-  stage_vec<C>(b0, 0.f, prm);
-  stage_vec<C>(s1, 1.f, prm + C);
-  stage_vec<C>(lw, 1.f, prm + 2 * C);
-  stage_vec<C>(lb, 0.f, prm + 3 * C);
-  stage_vec<C>(b2, 0.f, prm + 4 * C);
-  stage_vec<C>(s2, 1.f, prm + 5 * C);
-  stage_vec<CM>(b1, 0.f, prm + 6 * C);
+  __shared__ float Wht[HEAD ? C * LDH : 1];
+  __shared__ float prm[NP];  // b0, s1, LN weight, LN bias, b2, s2, b1 [, head LN weight, bias, head bias]
+  stage_wt<C, CIN, LD0>(a.W0, W0t);
+  stage_wt<CM, C, LD1>(a.W1, W1t);
+  stage_wt<C, CM, LD2>(a.W2, W2t);
+  stage_vec<C>(a.b0, 0.f, prm);
+  stage_vec<C>(a.s1, 1.f, prm + C);
+  stage_vec<C>(a.lw, 1.f, prm + 2 * C);
+  stage_vec<C>(a.lb, 0.f, prm + 3 * C);
+  stage_vec<C>(a.b2, 0.f, prm + 4 * C);
+  stage_vec<C>(a.s2, 1.f, prm + 5 * C);
+  stage_vec<CM>(a.b1, 0.f, prm + 6 * C);
+  if (HEAD) {
+    stage_wt<CIN, C, LDH>(a.Wh, Wht);
+    stage_vec<C>(a.hlw, 1.f, prm + 6 * C + CM);
+    stage_vec<C>(a.hlb, 0.f, prm + 7 * C + CM);
+    stage_vec<CIN>(a.bh, 0.f, prm + 8 * C + CM);
+  }
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, j = lane & 15;
-  const uint32_t xoff = (uint32_t)(((int64_t)g * HW + Q * j) * 4);
-  const uint32_t yoff = (uint32_t)(((int64_t)4 * g * HW + Q * j) * 4);
-  const float inv = 1.0f / (float)C;
-  for (int64_t tt = blockIdx.x; tt < ntiles; tt += gridDim.x) {
+  const uint32_t xoff = (uint32_t)(((int64_t)g * a.HW + Q * j) * 4);
+  const uint32_t yoff = (uint32_t)(((int64_t)4 * g * a.HW + Q * j) * 4);
+  for (int64_t tt = blockIdx.x; tt < a.ntiles; tt += gridDim.x) {
     mem_fence_sched();
-    const int64_t hw = opaque_stride(HW);
+    const int64_t hw = opaque_stride(a.HW);
     int64_t b;
-    const int64_t pw = tile_px(tt, tpb, Q, NW, wave, &b);
+    const int64_t pw = tile_px(tt, a.tpb, Q, NW, wave, &b);
     const bool inb = pw + Q * j < hw;
     // first branch's last layer: acc = W0 t
     v4f acc[C / 16][Q];
     {
       float tv[CIN / 4][Q];
-      load_tile<CIN, Q>(t + b * CIN * hw + pw, hw, inb, xoff, tv);
+      load_tile<CIN, Q>(a.t + b * CIN * hw + pw, hw, inb, xoff, tv);
       zero_acc<C, Q>(acc);
       gemm_tile<CIN, C, Q>(tv, W0t, LD0, g, j, acc);
     }
     // y' = x + s1 (acc + b0), channel 16 rb + 4 g + r; x read in the same layout
-    const float* xw = x + b * C * hw + pw;
+    const float* xw = a.x + b * C * hw + pw;
 #pragma unroll
     for (int rb = 0; rb < C / 16; ++rb)
 #pragma unroll
@@ -451,104 +542,55 @@ __global__ void __launch_bounds__(64 * NW) k_conv_ln_mlp_mfma(const float* __res
 #pragma unroll
         for (int q = 0; q < Q; ++q) acc[rb][q][r] = fmaf(sc, acc[rb][q][r] + bo, rr[q]);
       }
-    // LayerNorm of y' over its C channels (16 per lane, the rest in lanes j + 16, j + 32, j + 48)
-    v4f xn[C / 16][Q];
-#pragma unroll
-    for (int q = 0; q < Q; ++q) {
-      float su = 0.f;
-#pragma unroll
-      for (int rb = 0; rb < C / 16; ++rb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) su += acc[rb][q][r];
-      su += __shfl_xor(su, 16);
-      su += __shfl_xor(su, 32);
-      const float u = su * inv;
-      float va = 0.f;
-#pragma unroll
-      for (int rb = 0; rb < C / 16; ++rb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float d = acc[rb][q][r] - u;
-          va = fmaf(d, d, va);
-        }
-      va += __shfl_xor(va, 16);
-      va += __shfl_xor(va, 32);
-      const float rs = 1.0f / sqrtf(va * inv + eps);
-#pragma unroll
-      for (int rb = 0; rb < C / 16; ++rb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int o = 16 * rb + 4 * g + r;
-          xn[rb][q][r] = fmaf(prm[2 * C + o] * rs, acc[rb][q][r] - u, prm[3 * C + o]);
-        }
-    }
-    // hidden = GELU(W1 xn + b1): k-step kk = 4 rb + r, lane group g supplies channel 16 rb + 4 g + r
-    v4f h[CM / 16][Q];
-    zero_acc<CM, Q>(h);
+    // out = y' + s2 (W2 GELU(W1 LN(y') + b1) + b2)
+    v4f acc2[C / 16][Q];
     {
-      float a[2][CM / 16];
-#pragma unroll
-      for (int ob = 0; ob < CM / 16; ++ob) a[0][ob] = W1t[(4 * g) * LD1 + j + 16 * ob];
-#pragma unroll
-      for (int kk = 0; kk < C / 4; ++kk) {
-        const int rb = kk >> 2, r = kk & 3;
-        if (kk + 1 < C / 4) {
-          const int rn = (kk + 1) >> 2, sn = (kk + 1) & 3;
-          const float* wk = W1t + (16 * rn + 4 * g + sn) * LD1 + j;
-#pragma unroll
-          for (int ob = 0; ob < CM / 16; ++ob) a[(kk + 1) & 1][ob] = wk[16 * ob];
-        }
-#pragma unroll
-        for (int ob = 0; ob < CM / 16; ++ob)
-#pragma unroll
-          for (int q = 0; q < Q; ++q) h[ob][q] = mfma4(a[kk & 1][ob], xn[rb][q][r], h[ob][q]);
-        mem_fence_sched();
+      v4f h[CM / 16][Q];
+      {
+        v4f xn[C / 16][Q];
+        ln_acc<C, Q>(acc, prm + 2 * C, prm + 3 * C, a.eps, g, xn);
+        zero_acc<CM, Q>(h);
+        gemm_from_acc<C, CM, Q>(xn, W1t, LD1, g, j, h);
       }
+#pragma unroll
+      for (int rb = 0; rb < CM / 16; ++rb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float bo = prm[6 * C + 16 * rb + 4 * g + r];
+#pragma unroll
+          for (int q = 0; q < Q; ++q) h[rb][q][r] = gelu_f(h[rb][q][r] + bo);
+        }
+      zero_acc<C, Q>(acc2);
+      gemm_from_acc<CM, C, Q>(h, W2t, LD2, g, j, acc2);
     }
 #pragma unroll
-    for (int rb = 0; rb < CM / 16; ++rb)
+    for (int rb = 0; rb < C / 16; ++rb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float bo = prm[6 * C + 16 * rb + 4 * g + r];
+        const int o = 16 * rb + 4 * g + r;
+        const float bo = prm[4 * C + o], sc = prm[5 * C + o];
 #pragma unroll
-        for (int q = 0; q < Q; ++q) h[rb][q][r] = gelu_f(h[rb][q][r] + bo);
+        for (int q = 0; q < Q; ++q) acc2[rb][q][r] = fmaf(sc, acc2[rb][q][r] + bo, acc[rb][q][r]);
       }
-    // out = y' + s2 (W2 hidden + b2)
-    v4f acc2[C / 16][Q];
-    zero_acc<C, Q>(acc2);
-    {
-      float a[2][C / 16];
-#pragma unroll
-      for (int ob = 0; ob < C / 16; ++ob) a[0][ob] = W2t[(4 * g) * LD2 + j + 16 * ob];
-#pragma unroll
-      for (int kk = 0; kk < CM / 4; ++kk) {
-        const int rb = kk >> 2, r = kk & 3;
-        if (kk + 1 < CM / 4) {
-          const int rn = (kk + 1) >> 2, sn = (kk + 1) & 3;
-          const float* wk = W2t + (16 * rn + 4 * g + sn) * LD2 + j;
-#pragma unroll
-          for (int ob = 0; ob < C / 16; ++ob) a[(kk + 1) & 1][ob] = wk[16 * ob];
-        }
-#pragma unroll
-        for (int ob = 0; ob < C / 16; ++ob)
-#pragma unroll
-          for (int q = 0; q < Q; ++q) acc2[ob][q] = mfma4(a[kk & 1][ob], h[rb][q][r], acc2[ob][q]);
-        mem_fence_sched();
+    if (inb) store_acc<C, Q>(acc2, a.y + b * C * hw + pw, hw, yoff);
+    if (HEAD) {
+      // next block: th = GELU(Wh LNh(out) + bh)
+      v4f hh[CIN / 16][Q];
+      {
+        v4f xn[C / 16][Q];
+        ln_acc<C, Q>(acc2, prm + 6 * C + CM, prm + 7 * C + CM, a.heps, g, xn);
+        zero_acc<CIN, Q>(hh);
+        gemm_from_acc<C, CIN, Q>(xn, Wht, LDH, g, j, hh);
       }
-    }
-    if (inb) {
-      float* yw = y + b * C * hw + pw;
 #pragma unroll
-      for (int rb = 0; rb < C / 16; ++rb)
+      for (int rb = 0; rb < CIN / 16; ++rb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int o = 16 * rb + 4 * g + r;
-          const float bo = prm[4 * C + o], sc = prm[5 * C + o];
-          float v[Q];
+          const float bo = prm[8 * C + CM + 16 * rb + 4 * g + r];
 #pragma unroll
-          for (int q = 0; q < Q; ++q) v[q] = fmaf(sc, acc2[rb][q][r] + bo, acc[rb][q][r]);
-          stq<Q>(at_off(yw + (int64_t)(16 * rb + r) * hw, yoff), v);
+          for (int q = 0; q < Q; ++q) hh[rb][q][r] = gelu_f(hh[rb][q][r] + bo);
         }
+      if (inb) store_acc<CIN, Q>(hh, a.th + b * CIN * hw + pw, hw, yoff);
     }
   }
 }
@@ -659,14 +701,17 @@ int launch_mlp(const float* x, int64_t B, int64_t HW, const float* ln_w, const f
 }
 
 template <int CIN, int C, int CM>
-int launch_tail(const float* t, const float* x, int64_t B, int64_t HW, const float* w0, const float* b0,
-                const float* s1, const float* ln_w, const float* ln_b, float ln_eps, const float* w1, const float* b1,
-                const float* w2, const float* b2, const float* s2, float* y, hipStream_t st) {
+int launch_tail(TailArgs a, int64_t B, hipStream_t st) {
   constexpr int Q = 1, NW = 16;
-  const int64_t tpb = (HW + 16 * NW * Q - 1) / (16 * NW * Q), ntiles = B * tpb;
-  auto kern = k_conv_ln_mlp_mfma<CIN, C, CM, Q, NW>;
-  hipLaunchKernelGGL(kern, dim3(persistent_grid(kern, 64 * NW, ntiles)), dim3(64 * NW), 0, st, t, x, HW, tpb,
-                     ntiles, w0, b0, s1, ln_w, ln_b, ln_eps, w1, b1, w2, b2, s2, y);
+  a.tpb = (a.HW + 16 * NW * Q - 1) / (16 * NW * Q);
+  a.ntiles = B * a.tpb;
+  if (a.th) {
+    auto kern = k_conv_ln_mlp_mfma<CIN, C, CM, Q, NW, true>;
+    hipLaunchKernelGGL(kern, dim3(persistent_grid(kern, 64 * NW, a.ntiles)), dim3(64 * NW), 0, st, a);
+  } else {
+    auto kern = k_conv_ln_mlp_mfma<CIN, C, CM, Q, NW, false>;
+    hipLaunchKernelGGL(kern, dim3(persistent_grid(kern, 64 * NW, a.ntiles)), dim3(64 * NW), 0, st, a);
+  }
   return check_launch("fused block tail");
 }
 
@@ -774,22 +819,41 @@ extern "C" int cvn_ln_mlp_residual_f32(const float* x, int64_t B, int64_t C, int
   return fail(CVN_ERR_UNSUPPORTED, "fused branch supports (C, Cmid) in {(64,128), (32,64)}");
 }
 
+static int tail_impl(TailArgs a, int64_t B, int64_t Ct, int64_t C, int64_t Cmid, hipStream_t st) {
+  if (!a.t || !a.W0 || !a.b0 || !a.x || !a.lw || !a.lb || !a.W1 || !a.b1 || !a.W2 || !a.b2 || !a.y)
+    return fail(CVN_ERR_ARG, "null pointer");
+  if (a.th && (!a.hlw || !a.hlb || !a.Wh || !a.bh)) return fail(CVN_ERR_ARG, "null pointer");
+  if (B < 0 || a.HW < 0) return fail(CVN_ERR_ARG, "bad shape");
+  if (B > 65535) return fail(CVN_ERR_UNSUPPORTED, "batch exceeds 65535");
+  if (a.t == a.y || (a.th && (a.th == a.x || a.th == a.y)))
+    return fail(CVN_ERR_ARG, "the output may alias x only; the next block's input must be a separate buffer");
+  if (B == 0 || a.HW == 0) return CVN_OK;
+  if (a.HW % 4 != 0 || a.HW > kMaxMfmaHW || !aligned16(a.t) || !aligned16(a.x) || !aligned16(a.y) ||
+      (a.th && !aligned16(a.th)))
+    return fail(CVN_ERR_UNSUPPORTED, "fused tail needs HW %% 4 == 0, HW <= 2^26 and 16-byte aligned buffers");
+  if (Ct == 128 && C == 64 && Cmid == 128) return launch_tail<128, 64, 128>(a, B, st);
+  return fail(CVN_ERR_UNSUPPORTED, "fused tail supports (Ct, C, Cmid) = (128, 64, 128)");
+}
+
 extern "C" int cvn_conv_ln_mlp_residual_f32(const float* t, int64_t B, int64_t Ct, int64_t HW, const float* w0,
                                             const float* b0, const float* res_scale1, const float* x, int64_t C,
                                             const float* ln_w, const float* ln_b, float ln_eps, const float* w1,
                                             const float* b1, int64_t Cmid, const float* w2, const float* b2,
                                             const float* res_scale2, float* y, cvn_stream_t stream) {
-  if (!t || !w0 || !b0 || !x || !ln_w || !ln_b || !w1 || !b1 || !w2 || !b2 || !y)
-    return fail(CVN_ERR_ARG, "null pointer");
-  if (B < 0 || HW < 0) return fail(CVN_ERR_ARG, "bad shape");
-  if (B > 65535) return fail(CVN_ERR_UNSUPPORTED, "batch exceeds 65535");
-  if (t == y) return fail(CVN_ERR_ARG, "the output may alias x, not t");
-  if (B == 0 || HW == 0) return CVN_OK;
-  if (HW % 4 != 0 || HW > kMaxMfmaHW || !aligned16(t) || !aligned16(x) || !aligned16(y))
-    return fail(CVN_ERR_UNSUPPORTED, "fused tail needs HW %% 4 == 0, HW <= 2^26 and 16-byte aligned buffers");
-  hipStream_t st = (hipStream_t)stream;
-  if (Ct == 128 && C == 64 && Cmid == 128)
-    return launch_tail<128, 64, 128>(t, x, B, HW, w0, b0, res_scale1, ln_w, ln_b, ln_eps, w1, b1, w2, b2,
-                                     res_scale2, y, st);
-  return fail(CVN_ERR_UNSUPPORTED, "fused tail supports (Ct, C, Cmid) = (128, 64, 128)");
+  TailArgs a{t, x, HW, 0, 0, w0, b0, res_scale1, ln_w, ln_b, w1, b1, w2, b2, res_scale2, ln_eps, y,
+             nullptr, nullptr, nullptr, nullptr, 0.f, nullptr};
+  return tail_impl(a, B, Ct, C, Cmid, (hipStream_t)stream);
+}
+
+extern "C" int cvn_conv_ln_mlp_head_f32(const float* t, int64_t B, int64_t Ct, int64_t HW, const float* w0,
+                                        const float* b0, const float* res_scale1, const float* x, int64_t C,
+                                        const float* ln_w, const float* ln_b, float ln_eps, const float* w1,
+                                        const float* b1, int64_t Cmid, const float* w2, const float* b2,
+                                        const float* res_scale2, float* y, const float* head_ln_w,
+                                        const float* head_ln_b, float head_ln_eps, const float* head_w,
+                                        const float* head_b, float* t_next, cvn_stream_t stream) {
+  TailArgs a{t, x, HW, 0, 0, w0, b0, res_scale1, ln_w, ln_b, w1, b1, w2, b2, res_scale2, ln_eps, y,
+             head_ln_w, head_ln_b, head_w, head_b, head_ln_eps, t_next};
+  if (!t_next) return fail(CVN_ERR_ARG, "null pointer");
+  return tail_impl(a, B, Ct, C, Cmid, (hipStream_t)stream);
 }

@@ -307,8 +307,10 @@ TAIL_SHAPES = {(128, 64, 128)}  # (Ct, C, Cmid) of cvn_conv_ln_mlp_residual_f32
 
 
 def conv_ln_mlp_residual(t, x, w0, b0, ln_w, ln_b, ln_eps, w1, b1, w2, b2, res_scale1=None, res_scale2=None,
-                         out=None):
-    """ConverseBlock tail: y' = x + res_scale1 (W0 t + b0); y' + res_scale2 (W2 GELU(W1 LN(y') + b1) + b2)."""
+                         out=None, head=None):
+    """ConverseBlock tail: y' = x + res_scale1 (W0 t + b0); y = y' + res_scale2 (W2 GELU(W1 LN(y') + b1) + b2).
+    With head = (ln_w, ln_b, ln_eps, w, b) of the next block, also returns its Converse2D input
+    GELU(w LN(y) + b): (y, t_next); otherwise y."""
     lib = _lib.load()
     _need_hip(t, x, w0, b0, w1, b1, w2, b2, res_scale1, res_scale2)
     t = t.contiguous()
@@ -317,14 +319,20 @@ def conv_ln_mlp_residual(t, x, w0, b0, ln_w, ln_b, ln_eps, w1, b1, w2, b2, res_s
     C = x.shape[1]
     W0, W1, W2 = _wmat(w0), _wmat(w1), _wmat(w2)
     y = out if out is not None else torch.empty_like(x)
-    rc = lib.cvn_conv_ln_mlp_residual_f32(
-        t.data_ptr(), B, Ct, H * W, W0.data_ptr(), b0.contiguous().data_ptr(),
-        res_scale1.contiguous().data_ptr() if res_scale1 is not None else None, x.data_ptr(), C,
-        ln_w.contiguous().data_ptr(), ln_b.contiguous().data_ptr(), float(ln_eps), W1.data_ptr(),
-        b1.contiguous().data_ptr(), W1.shape[0], W2.data_ptr(), b2.contiguous().data_ptr(),
-        res_scale2.contiguous().data_ptr() if res_scale2 is not None else None, y.data_ptr(), _stream(x.device))
-    _lib.check(rc, "conv_ln_mlp_residual")
-    return y
+    ptr = lambda v: v.contiguous().data_ptr() if v is not None else None
+    common = (t.data_ptr(), B, Ct, H * W, W0.data_ptr(), ptr(b0), ptr(res_scale1), x.data_ptr(), C, ptr(ln_w),
+              ptr(ln_b), float(ln_eps), W1.data_ptr(), ptr(b1), W1.shape[0], W2.data_ptr(), ptr(b2), ptr(res_scale2),
+              y.data_ptr())
+    if head is None:
+        _lib.check(lib.cvn_conv_ln_mlp_residual_f32(*common, _stream(x.device)), "conv_ln_mlp_residual")
+        return y
+    hw, hb, heps, wh, bh = head
+    _need_hip(wh, bh)
+    Wh = _wmat(wh)
+    tn = torch.empty((B, Wh.shape[0], H, W), device=x.device, dtype=x.dtype)
+    _lib.check(lib.cvn_conv_ln_mlp_head_f32(*common, ptr(hw), ptr(hb), float(heps), Wh.data_ptr(), ptr(bh),
+                                            tn.data_ptr(), _stream(x.device)), "conv_ln_mlp_head")
+    return y, tn
 
 
 def copy_(dst, src):

@@ -215,30 +215,83 @@ class Converse2D(nn.Module):
 """
 
 
-def _fused_block_forward(blk, x, alpha1=None, alpha2=None):
-    """LN+1x1+GELU -> Converse2D+GELU -> 1x1+residual -> fused LN-MLP branch + residual.
-    Returns None when a shape is outside the instantiated HIP tiles."""
+def _block_parts(blk):
+    """The layers of a ConverseBlock(AlphaVariant) the fused path needs, or None when a shape is
+    outside the instantiated HIP tiles."""
     ln1, c11, _, cv, _, c15 = blk.conv1
     ln2, c21, _, c23 = blk.conv2
-    C = x.shape[1]
+    C = c11.in_channels
     mid = c11.out_channels
     if (C, mid) not in MFMA_SHAPES or (mid, C) not in MFMA_SHAPES or (C, c21.out_channels) not in MLP_SHAPES:
         return None
-    if (x.shape[2] * x.shape[3]) % 4 != 0 or not isinstance(cv, Converse2D) or _backend(cv.backend) == "pytorch":
+    if not isinstance(cv, Converse2D) or _backend(cv.backend) == "pytorch" or cv.scale != 1:
         return None
-    t = functional.conv1x1(x, c11.weight, c11.bias, act="gelu", ln=(ln1.weight, ln1.bias, ln1.eps))
+    alphas = (blk.alpha1.reshape(-1), blk.alpha2.reshape(-1)) if hasattr(blk, "alpha1") else (None, None)
+    return ln1, c11, cv, c15, ln2, c21, c23, alphas
+
+
+def _block_head(parts, x):
+    """LN -> 1x1 -> GELU (the first branch's first layer)."""
+    ln1, c11 = parts[0], parts[1]
+    return functional.conv1x1(x, c11.weight, c11.bias, act="gelu", ln=(ln1.weight, ln1.bias, ln1.eps))
+
+
+def _block_converse(parts, t):
+    cv = parts[2]
     cv.biaseps = None  # read lazily from the current bias
-    t = functional.converse2d_fused(t, cv.weight, cv.bias.reshape(-1), cv.scale, cv.padding, cv.padding_mode,
-                                    cv.eps, act="gelu")
-    s1 = alpha1.reshape(-1) if alpha1 is not None else None
-    s2 = alpha2.reshape(-1) if alpha2 is not None else None
-    if (mid, C, c21.out_channels) in functional.TAIL_SHAPES and t.data_ptr() % 16 == 0 and x.data_ptr() % 16 == 0:
-        # last 1x1 + residual and the LN-MLP branch in one kernel (the intermediate stays on chip)
-        return functional.conv_ln_mlp_residual(t, x, c15.weight, c15.bias, ln2.weight, ln2.bias, ln2.eps,
-                                               c21.weight, c21.bias, c23.weight, c23.bias, s1, s2)
+    return functional.converse2d_fused(t, cv.weight, cv.bias.reshape(-1), cv.scale, cv.padding, cv.padding_mode,
+                                       cv.eps, act="gelu")
+
+
+def _block_tail(parts, t, x, next_parts=None):
+    """1x1 + residual and the LN-MLP branch + residual; with next_parts also the next block's head.
+    Returns (block output, next block's Converse2D input or None)."""
+    _, _, _, c15, ln2, c21, c23, (s1, s2) = parts
+    mid, C = c15.in_channels, c15.out_channels
+    aligned = t.data_ptr() % 16 == 0 and x.data_ptr() % 16 == 0
+    if (mid, C, c21.out_channels) in functional.TAIL_SHAPES and aligned:
+        if next_parts is not None and next_parts[1].out_channels == mid:
+            nln, nc11 = next_parts[0], next_parts[1]
+            return functional.conv_ln_mlp_residual(t, x, c15.weight, c15.bias, ln2.weight, ln2.bias, ln2.eps,
+                                                   c21.weight, c21.bias, c23.weight, c23.bias, s1, s2,
+                                                   head=(nln.weight, nln.bias, nln.eps, nc11.weight, nc11.bias))
+        y = functional.conv_ln_mlp_residual(t, x, c15.weight, c15.bias, ln2.weight, ln2.bias, ln2.eps,
+                                            c21.weight, c21.bias, c23.weight, c23.bias, s1, s2)
+        return y, None
     x = functional.conv1x1(t, c15.weight, c15.bias, residual=x, res_scale=s1)
-    return functional.ln_mlp_residual(x, ln2.weight, ln2.bias, ln2.eps, c21.weight, c21.bias, c23.weight, c23.bias,
-                                      res_scale=s2, out=x)
+    y = functional.ln_mlp_residual(x, ln2.weight, ln2.bias, ln2.eps, c21.weight, c21.bias, c23.weight, c23.bias,
+                                   res_scale=s2, out=x)
+    return y, None
+
+
+def _fused_block_forward(blk, x, alpha1=None, alpha2=None):
+    """LN+1x1+GELU -> Converse2D+GELU -> 1x1+residual and the LN-MLP branch + residual.
+    Returns None when a shape is outside the instantiated HIP tiles."""
+    parts = _block_parts(blk)
+    if parts is None or (x.shape[2] * x.shape[3]) % 4 != 0:
+        return None
+    return _block_tail(parts, _block_converse(parts, _block_head(parts, x)), x)[0]
+
+
+def run_blocks(blocks, x):
+    """A chain of ConverseBlocks (util_converse.py:253-323 applied in sequence, as in the bodies of
+    converse_dncnn.py:24 and converse_usrnet.py:19-33).  On the HIP path each block's tail kernel
+    also computes the next block's LN -> 1x1 -> GELU, so a block's output is read once; otherwise the
+    blocks run one by one."""
+    blocks = list(blocks)
+    if not blocks:
+        return x
+    parts = [_block_parts(b) if _hip_eligible(x, *_block_params(b)) else None for b in blocks]
+    if any(p is None for p in parts) or (x.shape[2] * x.shape[3]) % 4 != 0:
+        for b in blocks:
+            x = b(x)
+        return x
+    t = _block_head(parts[0], x)
+    for i, p in enumerate(parts):
+        t = _block_converse(p, t)
+        x, t_next = _block_tail(p, t, x, parts[i + 1] if i + 1 < len(parts) else None)
+        t = t_next if t_next is not None else (_block_head(parts[i + 1], x) if i + 1 < len(parts) else None)
+    return x
 
 
 def _block_params(blk):

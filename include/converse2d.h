@@ -153,6 +153,17 @@ int cvn_conv_ln_mlp_residual_f32(const float* t, int64_t B, int64_t Ct, int64_t 
                                  const float* ln_w, const float* ln_b, float ln_eps, const float* w1,
                                  const float* b1, int64_t Cmid, const float* w2, const float* b2,
                                  const float* res_scale2, float* y, cvn_stream_t stream);
+/* The same tail followed by the next block's first layer (util_converse.py:278-280, LN -> 1x1 -> GELU),
+ * for chains of blocks (converse_dncnn.py:24, converse_usrnet.py:19-33): additionally
+ * t_next = GELU(head_w LN_head(y) + head_b), (B,Ct,HW), head_w: (Ct,C).  t_next may alias
+ * neither x nor y. */
+int cvn_conv_ln_mlp_head_f32(const float* t, int64_t B, int64_t Ct, int64_t HW, const float* w0,
+                             const float* b0, const float* res_scale1, const float* x, int64_t C,
+                             const float* ln_w, const float* ln_b, float ln_eps, const float* w1,
+                             const float* b1, int64_t Cmid, const float* w2, const float* b2,
+                             const float* res_scale2, float* y, const float* head_ln_w,
+                             const float* head_ln_b, float head_ln_eps, const float* head_w,
+                             const float* head_b, float* t_next, cvn_stream_t stream);
 
 /* Plain device copy of n floats (bandwidth calibration). */
 int cvn_copy_f32(const float* src, float* dst, int64_t n, cvn_stream_t stream);
