@@ -239,6 +239,11 @@ def _device():
     return torch.device("cuda" if torch.cuda.is_available() else "cpu")
 
 
+def _model_device(model):
+    p = next(model.parameters(), None)
+    return p.device if p is not None else _device()
+
+
 def _load(model, path):
     if path:
         model.load_state_dict(torch.load(path, map_location="cpu", weights_only=True), strict=True)
@@ -258,7 +263,7 @@ def eval_dncnn(paths, model, noise_level, out_dir=None):
         np.random.seed(seed=0)
         img_l = img_l + np.random.normal(0, noise_level / 255., img_l.shape)
         with torch.no_grad():
-            img_e = tensor2uint(model(single2tensor4(img_l).to(_device())))
+            img_e = tensor2uint(model(single2tensor4(img_l).to(_model_device(model))))
         h = img_h.squeeze()
         res.append((os.path.basename(p), calculate_psnr(img_e, h), calculate_ssim(img_e, h)))
         if out_dir:
@@ -274,7 +279,7 @@ def eval_srresnet(paths, model, sf, out_dir=None):
         img_h = modcrop(imread_uint(p, 3), sf)
         img_l = imresize_np(uint2single(img_h), 1.0 / sf, True)
         with torch.no_grad():
-            img_e = tensor2uint(model(single2tensor4(img_l).to(_device())))
+            img_e = tensor2uint(model(single2tensor4(img_l).to(_model_device(model))))
         psnr, ssim = calculate_psnr(img_e, img_h, sf), calculate_ssim(img_e, img_h, sf)
         ey, hy = rgb2ycbcr(img_e, True), rgb2ycbcr(img_h, True)
         res.append((os.path.basename(p), psnr, ssim, calculate_psnr(ey, hy, sf), calculate_ssim(ey, hy, sf)))
@@ -296,7 +301,7 @@ def eval_usrnet(paths, model, kernel, sf, noise_level=2.55, out_dir=None):
         np.random.seed(seed=0)
         img_l = img_l + np.random.normal(0, noise_level / 255., img_l.shape)
         with torch.no_grad():
-            img_e = tensor2uint(model(single2tensor4(img_l).to(_device())))
+            img_e = tensor2uint(model(single2tensor4(img_l).to(_model_device(model))))
         res.append((os.path.basename(p), calculate_psnr(img_e, img_h, sf * sf)))
         if out_dir:
             imsave(img_e, os.path.join(out_dir, os.path.splitext(os.path.basename(p))[0] + f"_x{sf}.png"))

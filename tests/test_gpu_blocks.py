@@ -343,3 +343,24 @@ def test_module_non_contiguous_input():
     ref = O.converse2d_module(x.cpu().numpy(), m.weight.detach().cpu().numpy(), m.bias.detach().cpu().numpy(), 1,
                               2, "circular", 1e-5)
     assert np.abs(got - ref).max() <= TOL
+
+
+def test_evaluate_dncnn_loop_on_hip_matches_cpu(tmp_path):
+    """The evaluation loop (main_test_converse_dncnn.py:110-171) through the HIP model gives the same
+    PSNR / SSIM as through the CPU composition (random-init Converse-DnCNN, synthetic 64x64 image)."""
+    from PIL import Image
+    from conversenet_amd import evaluate as E
+    from conversenet_amd.converse_dncnn import ConverseDnCNN
+    rng = seeded("eval")
+    yy, xx = np.mgrid[0:64, 0:64]
+    img = (127 + 60 * np.sin(xx / 5.0) * np.cos(yy / 7.0) + rng.normal(0, 5, (64, 64))).clip(0, 255)
+    Image.fromarray(img.astype(np.uint8)).save(str(tmp_path / "a.png"))
+    paths = E.get_image_paths(str(tmp_path))
+    torch.manual_seed(5)
+    m = ConverseDnCNN().eval()
+    for p in m.parameters():
+        p.requires_grad_(False)
+    _, p_cpu, s_cpu = E.eval_dncnn(paths, m, 25)[0]  # inputs follow the model's device
+    m = m.to(DEV)
+    _, p_hip, s_hip = E.eval_dncnn(paths, m, 25)[0]
+    assert abs(p_hip - p_cpu) < 0.05 and abs(s_hip - s_cpu) < 1e-3
