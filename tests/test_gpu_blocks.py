@@ -345,6 +345,33 @@ def test_module_non_contiguous_input():
     assert np.abs(got - ref).max() <= TOL
 
 
+def test_block_chain_matches_block_by_block():
+    """run_blocks (each tail kernel also computing the next block's head) against the same blocks
+    called one by one, and against the fp64 oracle, for a chain of alpha-variant blocks."""
+    from conversenet_amd import util_converse as U
+    torch.manual_seed(21)
+    blocks = [U.ConverseBlockAlphaVariant(64, 64, kernel_size=3, padding=2, padding_mode="circular")
+              for _ in range(3)]
+    with torch.no_grad():
+        for b in blocks:
+            b.alpha1.normal_(0, 0.5)
+            b.alpha2.normal_(0, 0.5)
+    rng = seeded("chain")
+    x = rng.standard_normal((2, 64, 28, 36)).astype(np.float32)
+    ref = x.astype(np.float64)
+    for b in blocks:
+        ref = O.converse_block(ref, _sd(b), "", 3, 1, 2, "circular", 1e-5, True)
+    blocks = [b.to(DEV).eval() for b in blocks]
+    with torch.no_grad():
+        chain = _n(U.run_blocks(blocks, _t(x)))
+        one = _t(x)
+        for b in blocks:
+            one = b(one)
+        one = _n(one)
+    assert np.abs(chain - one).max() <= 1e-4
+    assert np.abs(chain - ref).max() <= 1e-3 and psnr(chain, ref) >= 60
+
+
 def test_evaluate_dncnn_loop_on_hip_matches_cpu(tmp_path):
     """The evaluation loop (main_test_converse_dncnn.py:110-171) through the HIP model gives the same
     PSNR / SSIM as through the CPU composition (random-init Converse-DnCNN, synthetic 64x64 image)."""

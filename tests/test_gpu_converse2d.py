@@ -235,6 +235,20 @@ def test_pfa268_vs_oracle(mode, k):
     assert err <= TOL, err
 
 
+@pytest.mark.parametrize("H,p,k,mode", [(268, 0, 3, "constant"), (266, 1, 3, "reflect"), (264, 2, 5, "replicate")])
+def test_pfa268_other_paddings(H, p, k, mode):
+    """268-point planes reached with padding 0, 1, 2 (every padded column and row index map of the
+    quad loads), 7 planes so the row pass's last block is partial."""
+    rng = seeded("pfa268-pad", H, p, k, mode)
+    B, C = 1, 7
+    x = rng.standard_normal((B, C, H, H)).astype(np.float32)
+    w = softmax_psf(rng, C, k)
+    b = (0.4 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    ref = O.converse2d_module(x, w, b, 1, p, mode, 1e-5)
+    got = _run_fused(x, w, b, 1, p, mode, 1e-5)
+    assert np.abs(got - ref).max() <= TOL
+
+
 def test_pfa268_per_sample_psf_gelu_and_generic_agreement(monkeypatch):
     from conversenet_amd import functional as Fh
     rng = seeded("pfa268-ps")
