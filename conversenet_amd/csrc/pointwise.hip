@@ -309,6 +309,32 @@ __global__ void __launch_bounds__(64 * NW) k_conv1x1_mfma(const float* __restric
   }
 }
 
+// acc[ob][q] += W[16 ob + j][k] * v[k] over the k-steps kk = 4 rb + r whose B operand is register r of
+// row block rb of v (lane group g supplies channel 16 rb + 4 g + r): the first layer's accumulator
+// layout fed to the next layer.  Wt[k * LD + i] = W[i][k].
+template <int K, int N, int Q>
+__device__ __forceinline__ void gemm_from_acc(const v4f (&v)[K / 16][Q], const float* Wt, int ld, int g, int j,
+                                              v4f (&acc)[N / 16][Q]) {
+  float a[2][N / 16];
+#pragma unroll
+  for (int ob = 0; ob < N / 16; ++ob) a[0][ob] = Wt[(4 * g) * ld + j + 16 * ob];
+#pragma unroll
+  for (int kk = 0; kk < K / 4; ++kk) {
+    const int rb = kk >> 2, r = kk & 3;
+    if (kk + 1 < K / 4) {
+      const int rn = (kk + 1) >> 2, sn = (kk + 1) & 3;
+      const float* wk = Wt + (16 * rn + 4 * g + sn) * ld + j;
+#pragma unroll
+      for (int ob = 0; ob < N / 16; ++ob) a[(kk + 1) & 1][ob] = wk[16 * ob];
+    }
+#pragma unroll
+    for (int ob = 0; ob < N / 16; ++ob)
+#pragma unroll
+      for (int q = 0; q < Q; ++q) acc[ob][q] = mfma4(a[kk & 1][ob], v[rb][q][r], acc[ob][q]);
+    mem_fence_sched();
+  }
+}
+
 // ConverseBlock conv2 branch: y = x + res_scale * (W2 GELU(W1 LN(x) + b1) + b2)
 template <int C, int CM, int Q, int NW>
 __global__ void __launch_bounds__(64 * NW) k_ln_mlp_mfma(const float* x, int64_t HW, int64_t tpb, int64_t ntiles,
@@ -358,25 +384,7 @@ __global__ void __launch_bounds__(64 * NW) k_ln_mlp_mfma(const float* x, int64_t
       }
     v4f acc[C / 16][Q];
     zero_acc<C, Q>(acc);
-    // k-step kk = 4 rb + r: lane group g supplies hidden channel 16 rb + 4 g + r
-    float a[2][C / 16];
-#pragma unroll
-    for (int ob = 0; ob < C / 16; ++ob) a[0][ob] = W2t[(4 * g) * LD2 + j + 16 * ob];
-#pragma unroll
-    for (int kk = 0; kk < CM / 4; ++kk) {
-      const int rb = kk >> 2, r = kk & 3;
-      if (kk + 1 < CM / 4) {
-        const int rn = (kk + 1) >> 2, sn = (kk + 1) & 3;
-        const float* wk = W2t + (16 * rn + 4 * g + sn) * LD2 + j;
-#pragma unroll
-        for (int ob = 0; ob < C / 16; ++ob) a[(kk + 1) & 1][ob] = wk[16 * ob];
-      }
-#pragma unroll
-      for (int ob = 0; ob < C / 16; ++ob)
-#pragma unroll
-        for (int q = 0; q < Q; ++q) acc[ob][q] = mfma4(a[kk & 1][ob], h[rb][q][r], acc[ob][q]);
-      mem_fence_sched();
-    }
+    gemm_from_acc<CM, C, Q>(h, W2t, LD2, g, j, acc);  // k-step 4 rb + r: hidden channel 16 rb + 4 g + r
     store_tile<C, Q>(acc, y + b * C * hw + pw, xw, hw, inb, yoff, g, prm + CM, CVN_ACT_NONE, prm + CM + C);
   }
 }
@@ -399,32 +407,6 @@ struct TailArgs {
   float heps;
   float* th;  // HEAD: (B, CIN, HW)
 };
-
-// acc[ob][q] += W[16 ob + j][k] * v[k] over the k-steps kk = 4 rb + r whose B operand is register r of
-// row block rb of v (lane group g supplies channel 16 rb + 4 g + r): the first layer's accumulator
-// layout fed to the next layer.  Wt[k * LD + i] = W[i][k].
-template <int K, int N, int Q>
-__device__ __forceinline__ void gemm_from_acc(const v4f (&v)[K / 16][Q], const float* Wt, int ld, int g, int j,
-                                              v4f (&acc)[N / 16][Q]) {
-  float a[2][N / 16];
-#pragma unroll
-  for (int ob = 0; ob < N / 16; ++ob) a[0][ob] = Wt[(4 * g) * ld + j + 16 * ob];
-#pragma unroll
-  for (int kk = 0; kk < K / 4; ++kk) {
-    const int rb = kk >> 2, r = kk & 3;
-    if (kk + 1 < K / 4) {
-      const int rn = (kk + 1) >> 2, sn = (kk + 1) & 3;
-      const float* wk = Wt + (16 * rn + 4 * g + sn) * ld + j;
-#pragma unroll
-      for (int ob = 0; ob < N / 16; ++ob) a[(kk + 1) & 1][ob] = wk[16 * ob];
-    }
-#pragma unroll
-    for (int ob = 0; ob < N / 16; ++ob)
-#pragma unroll
-      for (int q = 0; q < Q; ++q) acc[ob][q] = mfma4(a[kk & 1][ob], v[rb][q][r], acc[ob][q]);
-    mem_fence_sched();
-  }
-}
 
 // LayerNorm over the C channels of v, held in the accumulator layout (16 per lane for C = 64; the
 // other lane groups of the same pixel block are lanes j + 16, j + 32, j + 48).
