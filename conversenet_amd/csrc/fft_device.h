@@ -293,7 +293,7 @@ __device__ __forceinline__ RaderTab rader_tab(char* base, const RaderPlan& rp) {
 // p is the product of the radices already applied.  Output position of butterfly i, leg j is
 // (i - k) * R + k + j * p with k = i mod p; leg j is pre-multiplied by exp(-+2 pi i j k / (p R)).
 template <int R, bool INV>
-__device__ void stockham_pass(const float2* __restrict__ src, float2* __restrict__ dst, int L, int p,
+__device__ __forceinline__ void stockham_pass(const float2* __restrict__ src, float2* __restrict__ dst, int L, int p,
                               int ntr, const float2* __restrict__ tw, int tid, int nth) {
   const int T = L / R;
   const int twstep = L / (p * R);
@@ -321,7 +321,7 @@ __device__ void stockham_pass(const float2* __restrict__ src, float2* __restrict
 
 // Same pass for any radix R (runtime), O(R^2) per butterfly; used for prime factors > 13.
 template <bool INV>
-__device__ void stockham_pass_generic(const float2* __restrict__ src, float2* __restrict__ dst, int L,
+__device__ __forceinline__ void stockham_pass_generic(const float2* __restrict__ src, float2* __restrict__ dst, int L,
                                       int R, int p, int ntr, const float2* __restrict__ tw, int tid,
                                       int nth) {
   const int T = L / R;
@@ -355,7 +355,7 @@ __device__ void stockham_pass_generic(const float2* __restrict__ src, float2* __
 
 // A fixed-radix-only plan (the inner transforms of a Rader stage) on `ntr` transforms in a / b.
 template <bool INV>
-__device__ float2* fft_fixed(const int* radix, int nst, int L, float2* a, float2* b, int ntr, const float2* tw,
+__device__ __forceinline__ float2* fft_fixed(const int* radix, int nst, int L, float2* a, float2* b, int ntr, const float2* tw,
                              int tid, int nth) {
   int p = 1;
   float2* src = a;
@@ -388,7 +388,7 @@ __device__ float2* fft_fixed(const int* radix, int nst, int L, float2* a, float2
 // passes each way the convolution always ends in dst, whose tail was never touched, so the
 // outputs are scattered into src.  Returns src (the pass does not swap buffers).
 template <bool INV>
-__device__ float2* rader_pass(float2* src, float2* dst, int L, int p, int ntr, const float2* tw,
+__device__ __forceinline__ float2* rader_pass(float2* src, float2* dst, int L, int p, int ntr, const float2* tw,
                               const RaderPlan& rp, const RaderTab& rt, int tid, int nth) {
   const int R = rp.R, Rm = R - 1, T = L / R, NB = T * ntr;
   const int twstep = L / (p * R);
@@ -509,7 +509,7 @@ __device__ __forceinline__ void load_plan_tabs(const FftPlan& plan, const char* 
 // the buffer holding the result.  All threads of the block must call it; it synchronises.
 // `rader` is the plan's Rader LDS area (filled by load_plan_tabs), or null when plan.nrad == 0.
 template <bool INV>
-__device__ float2* fft_lds(const FftPlan& plan, float2* a, float2* b, int ntr, const float2* tw,
+__device__ __forceinline__ float2* fft_lds(const FftPlan& plan, float2* a, float2* b, int ntr, const float2* tw,
                            int tid, int nth, char* rader = nullptr) {
   int p = 1;
   float2* src = a;
