@@ -724,7 +724,10 @@ __host__ __device__ inline size_t cols_bwd_lds(int h, int Hs, int s, int cpb, bo
   return (size_t)(h + Hs + 3 * cpb * h + 2 * cpb * s * Hs + (wg ? cpb * s * Hs : 0)) * sizeof(float2);
 }
 
-__global__ void __launch_bounds__(256) k_cols_bwd(ColBwdArgs a) {
+constexpr int kColsBwdThreads = 512;  // 2 blocks of 8 waves per CU at the cfg3 LDS size
+constexpr int kColRegs = 4;           // per-thread register slots of the scale-1 path
+
+__global__ void __launch_bounds__(kColsBwdThreads) k_cols_bwd(ColBwdArgs a) {
   extern __shared__ float2 sm[];
   const int tid = threadIdx.x, nth = blockDim.x;
   const bool wg = a.dphi != nullptr;
@@ -751,6 +754,20 @@ __global__ void __launch_bounds__(256) k_cols_bwd(ColBwdArgs a) {
   const float norm = 1.0f / ((float)a.Hs * (float)a.Ws);
   if (wg)
     for (int i = tid; i < cpb * sH; i += nth) acc[i] = make_float2(0.f, 0.f);
+  // Scale 1 with at most kColRegs elements per thread: every class has one member column (vb =
+  // vbase + cl <= Ws / 2) and one row per bin, so element idx = cl h + u of this thread is the same
+  // in every plane; its conj(Phi') is read from HBM once and the dPhi sum stays in registers.
+  const bool regs = a.s == 1 && cpb * a.h <= kColRegs * nth;
+  float2 fr[kColRegs], ar[kColRegs];
+  if (regs) {
+#pragma unroll
+    for (int k = 0; k < kColRegs; ++k) {
+      const int idx = tid + k * nth;
+      const int cl = idx / fh;
+      fr[k] = (cl < ncol) ? cconj(ph[(int64_t)(vbase + cl) * a.Hs + (idx - cl * a.h)]) : make_float2(0.f, 0.f);
+      ar[k] = make_float2(0.f, 0.f);
+    }
+  }
   const int64_t nplanes = (a.psf_batch == 1) ? a.B : 1;
   for (int64_t ib = 0; ib < nplanes; ++ib) {
     const int64_t plane = (a.psf_batch == 1) ? ib * a.C + grp : grp;
@@ -797,39 +814,65 @@ __global__ void __launch_bounds__(256) k_cols_bwd(ColBwdArgs a) {
     }
     __syncthreads();
     const float2* dZ = fft_lds<false>(a.plan_H, Xa, Xb, cpb * a.s, tH, tid, nth, radH);
-    if (wg) {
-      const float2* Y = fft_lds<false>(a.plan_h, Ya, Yb, cpb, twh, tid, nth, radh);
-      for (int idx = tid; idx < cpb * sH; idx += nth) {
-        const int cl = idx / fsH, r = idx - cl * sH;
-        const int u = r - (r / fHs) * a.Hs;
-        const float2 t = cmul(cconj(Y[cl * a.h + u - (u / fh) * a.h]), dZ[idx]);
-        acc[idx].x = fmaf(t.x, norm, acc[idx].x);
-        acc[idx].y = fmaf(t.y, norm, acc[idx].y);
-      }
-    }
-    for (int idx = tid; idx < cpb * a.h; idx += nth) {
-      const int cl = idx / fh, u0 = idx - cl * a.h;
-      float2 m = make_float2(0.f, 0.f);
-      if (cl < ncol) {
-        for (int b = 0; b < a.s; ++b) {
-          const int vb = vbase + cl + b * a.w;
-          for (int aa = 0; aa < a.s; ++aa) {
-            const int u = u0 + aa * a.h;
-            const float2 f = vb <= a.Ws / 2 ? ph[(int64_t)vb * a.Hs + u]
-                                            : cconj(ph[(int64_t)(a.Ws - vb) * a.Hs + (u == 0 ? 0 : a.Hs - u)]);
-            const float2 t = cmul(cconj(f), dZ[cl * sH + b * a.Hs + u]);
-            m.x += t.x;
-            m.y += t.y;
+    const float2* Y = wg ? fft_lds<false>(a.plan_h, Ya, Yb, cpb, twh, tid, nth, radh) : nullptr;
+    if (regs) {
+#pragma unroll
+      for (int k = 0; k < kColRegs; ++k) {
+        const int idx = tid + k * nth;
+        if (idx < cpb * a.h) {
+          const float2 z = dZ[idx];
+          if (wg) {
+            const float2 t = cmul(cconj(Y[idx]), z);
+            ar[k].x = fmaf(t.x, norm, ar[k].x);
+            ar[k].y = fmaf(t.y, norm, ar[k].y);
           }
+          Yc[idx] = cmul(fr[k], z);
         }
       }
-      Yc[idx] = m;
+    } else {
+      if (wg) {
+        for (int idx = tid; idx < cpb * sH; idx += nth) {
+          const int cl = idx / fsH, r = idx - cl * sH;
+          const int u = r - (r / fHs) * a.Hs;
+          const float2 t = cmul(cconj(Y[cl * a.h + u - (u / fh) * a.h]), dZ[idx]);
+          acc[idx].x = fmaf(t.x, norm, acc[idx].x);
+          acc[idx].y = fmaf(t.y, norm, acc[idx].y);
+        }
+      }
+      for (int idx = tid; idx < cpb * a.h; idx += nth) {
+        const int cl = idx / fh, u0 = idx - cl * a.h;
+        float2 m = make_float2(0.f, 0.f);
+        if (cl < ncol) {
+          for (int b = 0; b < a.s; ++b) {
+            const int vb = vbase + cl + b * a.w;
+            for (int aa = 0; aa < a.s; ++aa) {
+              const int u = u0 + aa * a.h;
+              const float2 f = vb <= a.Ws / 2 ? ph[(int64_t)vb * a.Hs + u]
+                                              : cconj(ph[(int64_t)(a.Ws - vb) * a.Hs + (u == 0 ? 0 : a.Hs - u)]);
+              const float2 t = cmul(cconj(f), dZ[cl * sH + b * a.Hs + u]);
+              m.x += t.x;
+              m.y += t.y;
+            }
+          }
+        }
+        Yc[idx] = m;
+      }
     }
     __syncthreads();
     const float2* R = fft_lds<true>(a.plan_h, Yc, Ya, cpb, twh, tid, nth, radh);
     for (int idx = tid; idx < ncol * a.h; idx += nth) Sxp[(int64_t)vbase * a.h + idx] = R[idx];
   }
-  if (wg) {
+  if (wg && regs) {
+    float2* dp = a.dphi + grp * (int64_t)a.Ws * a.Hs;
+#pragma unroll
+    for (int k = 0; k < kColRegs; ++k) {
+      const int idx = tid + k * nth;
+      if (idx < ncol * a.h) {
+        const int cl = idx / fh;
+        dp[(int64_t)(vbase + cl) * a.Hs + (idx - cl * a.h)] = ar[k];
+      }
+    }
+  } else if (wg) {
     __syncthreads();
     float2* dp = a.dphi + grp * (int64_t)a.Ws * a.Hs;
     for (int idx = tid; idx < ncol * sH; idx += nth) {
@@ -846,7 +889,7 @@ __global__ void __launch_bounds__(256) k_cols_bwd(ColBwdArgs a) {
 // whose padding source is i / j (no local arrays: runtime-indexed ones would live in scratch memory).
 __device__ __forceinline__ int border_idx(int q, int n, int pad) { return q < pad ? q : n + q; }
 
-constexpr int kPadRows = 8;  // rows per thread in k_pad_adj
+constexpr int kPadRows = 16;  // rows per thread in k_pad_adj
 __global__ void __launch_bounds__(256) k_pad_adj(const float* __restrict__ dy, int H, int W, int pad, int mode,
                                                  float* __restrict__ dx) {
   extern __shared__ int psrc[];  // padding source of border row q: psrc[q]; of border column q: psrc[2 pad + q]
@@ -1590,7 +1633,7 @@ extern "C" int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int
     const size_t lds = a.rad_off + rad;
     if (lds > kLdsLimit) return fail(CVN_ERR_UNSUPPORTED, "plane too large for the backward column pass");
     const dim3 grid((unsigned)((g.NC + a.cpb - 1) / a.cpb), (unsigned)(a.psf_batch == 1 ? g.C : g.P));
-    hipLaunchKernelGGL(k_cols_bwd, grid, dim3(kThreads), lds, st, a);
+    hipLaunchKernelGGL(k_cols_bwd, grid, dim3(kColsBwdThreads), lds, st, a);
     if ((rc = check_launch("backward column pass")) != CVN_OK) return rc;
   }
   // dy = C2R rows of dS (LR grid, uncropped), then the padding adjoint
