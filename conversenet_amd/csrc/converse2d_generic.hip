@@ -1019,21 +1019,26 @@ __global__ void __launch_bounds__(256) k_phi_grad(PhiArgs a, PhiGradArgs gr, int
 }
 
 // Transposed DFT along the columns: T[cp][u][j] = sum_v dK[cp][v][u] exp(+2 pi i v (j - cw) / Ws),
-// fp64 accumulation; thread = row u, kJ taps j at a time.
-constexpr int kJ = 8;
+// fp64 accumulation.  Block = (kGaU rows u, psf plane); its kGaV thread slices take the columns
+// v = slice mod kGaV, kGaUnroll loads in flight per thread, and the slice sums are reduced in LDS.
+constexpr int kJ = 8;          // taps j per accumulation round
+constexpr int kGaU = 32;       // rows u per block (lanes of a slice)
+constexpr int kGaV = 8;        // column slices per block (kGaU * kGaV = 256 threads)
+constexpr int kGaUnroll = 4;   // column loads batched per thread
 __global__ void __launch_bounds__(256) k_psf_grad_a(const float2* __restrict__ dK, int Hs, int Ws, int kw,
                                                     double2* __restrict__ T) {
-  extern __shared__ double2 twW[];  // exp(+2 pi i m / Ws)
+  extern __shared__ double2 twW[];  // exp(+2 pi i m / Ws), then kGaV * kGaU * kJ slice sums
+  double2* part = twW + Ws;
   const int tid = threadIdx.x;
+  const int ul = tid % kGaU, vs = tid / kGaU;
   const int64_t cp = blockIdx.y;
   for (int m = tid; m < Ws; m += blockDim.x) {
     const double2 e = dexpi((double)m, (double)Ws);
     twW[m] = make_double2(e.x, -e.y);
   }
-  __syncthreads();
-  const int u = blockIdx.x * blockDim.x + tid;
-  if (u >= Hs) return;
-  const float2* col = dK + cp * (int64_t)Ws * Hs + u;
+  const int u = blockIdx.x * kGaU + ul;
+  const bool live = u < Hs;
+  const float2* col = dK + cp * (int64_t)Ws * Hs + (live ? u : 0);
   const int cw = kw / 2;
   for (int j0 = 0; j0 < kw; j0 += kJ) {
     double2 acc[kJ];
@@ -1041,25 +1046,48 @@ __global__ void __launch_bounds__(256) k_psf_grad_a(const float2* __restrict__ d
 #pragma unroll
     for (int q = 0; q < kJ; ++q) {
       acc[q] = make_double2(0.0, 0.0);
-      idx[q] = 0;
-      const int d = (j0 + q - cw) % Ws;
-      step[q] = d < 0 ? d + Ws : d;
+      int d = (j0 + q - cw) % Ws;
+      d = d < 0 ? d + Ws : d;
+      idx[q] = (int)(((int64_t)vs * d) % Ws);  // exponent index of column v = vs
+      step[q] = (int)(((int64_t)kGaV * d) % Ws);
     }
-    for (int v = 0; v < Ws; ++v) {
-      const float2 gf = col[(int64_t)v * Hs];
-      const double2 gd = make_double2((double)gf.x, (double)gf.y);
+    __syncthreads();  // twW written; the previous round's slice sums consumed
+    for (int v0 = vs; v0 < Ws; v0 += kGaV * kGaUnroll) {
+      float2 g[kGaUnroll];
 #pragma unroll
-      for (int q = 0; q < kJ; ++q) {
-        const double2 e = twW[idx[q]];
-        acc[q].x = fma(gd.x, e.x, fma(-gd.y, e.y, acc[q].x));
-        acc[q].y = fma(gd.x, e.y, fma(gd.y, e.x, acc[q].y));
-        idx[q] += step[q];
-        if (idx[q] >= Ws) idx[q] -= Ws;
+      for (int r = 0; r < kGaUnroll; ++r) {
+        const int v = v0 + r * kGaV;
+        g[r] = (live && v < Ws) ? col[(int64_t)v * Hs] : make_float2(0.f, 0.f);
+      }
+#pragma unroll
+      for (int r = 0; r < kGaUnroll; ++r) {
+        const double2 gd = make_double2((double)g[r].x, (double)g[r].y);
+#pragma unroll
+        for (int q = 0; q < kJ; ++q) {
+          const double2 e = twW[idx[q]];
+          acc[q].x = fma(gd.x, e.x, fma(-gd.y, e.y, acc[q].x));
+          acc[q].y = fma(gd.x, e.y, fma(gd.y, e.x, acc[q].y));
+          idx[q] += step[q];
+          if (idx[q] >= Ws) idx[q] -= Ws;
+        }
       }
     }
 #pragma unroll
-    for (int q = 0; q < kJ; ++q)
-      if (j0 + q < kw) T[(cp * Hs + u) * kw + j0 + q] = acc[q];
+    for (int q = 0; q < kJ; ++q) part[(vs * kGaU + ul) * kJ + q] = acc[q];
+    __syncthreads();
+    if (vs == 0 && live) {
+#pragma unroll
+      for (int q = 0; q < kJ; ++q) {
+        if (j0 + q >= kw) break;
+        double2 t = part[ul * kJ + q];
+        for (int sl = 1; sl < kGaV; ++sl) {
+          const double2 o = part[(sl * kGaU + ul) * kJ + q];
+          t.x += o.x;
+          t.y += o.y;
+        }
+        T[(cp * Hs + u) * kw + j0 + q] = t;
+      }
+    }
   }
 }
 
@@ -1082,7 +1110,33 @@ __global__ void __launch_bounds__(256) k_psf_grad_b(const double2* __restrict__ 
   double lsum = 0.0;
   for (int64_t pb = 0; pb < psf_batch; ++pb) {
     const int64_t cp = pb * C + c;
-    if (dpsf) {
+    if (dpsf && kh * kw <= nth) {
+      // S threads per tap, each summing the rows u = slice mod S; slice sums reduced in LDS
+      const int ne = kh * kw, S = nth / ne, e = tid % ne, sl = tid / ne;
+      double acc = 0.0;
+      if (sl < S) {
+        const int i = e / kw, j = e - i * kw;
+        int d = (i - ch) % Hs;
+        if (d < 0) d += Hs;
+        const int dS = (int)(((int64_t)d * S) % Hs);
+        int idx = (int)(((int64_t)d * sl) % Hs);
+        const double2* Tc = T + cp * (int64_t)Hs * kw + j;
+        for (int u = sl; u < Hs; u += S) {
+          const double2 t = Tc[(int64_t)u * kw], e2 = twH[idx];
+          acc = fma(t.x, e2.x, fma(-t.y, e2.y, acc));
+          idx += dS;
+          if (idx >= Hs) idx -= Hs;
+        }
+      }
+      red[tid] = acc;
+      __syncthreads();
+      if (tid < ne) {
+        double t = 0.0;
+        for (int k = 0; k < S; ++k) t += red[tid + k * ne];
+        dpsf[cp * ne + tid] = (float)t;
+      }
+      __syncthreads();  // red is reused
+    } else if (dpsf) {
       for (int e = tid; e < kh * kw; e += nth) {
         const int i = e / kw, j = e - i * kw;
         int d = (i - ch) % Hs;
@@ -1671,9 +1725,9 @@ extern "C" int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int
   }
   double2* T = (double2*)(base + ws.T);
   if (grad_psf) {
-    const dim3 grid((unsigned)((g.Hs + 255) / 256), (unsigned)g.Cp);
+    const dim3 grid((unsigned)((g.Hs + kGaU - 1) / kGaU), (unsigned)g.Cp);
     if (g.Cp > 65535) return fail(CVN_ERR_UNSUPPORTED, "too many psf planes");
-    hipLaunchKernelGGL(k_psf_grad_a, grid, dim3(256), (size_t)g.Ws * sizeof(double2), st,
+    hipLaunchKernelGGL(k_psf_grad_a, grid, dim3(kGaU * kGaV), ((size_t)g.Ws + kGaU * kGaV * kJ) * sizeof(double2), st,
                        (const float2*)(base + ws.dK), g.Hs, g.Ws, g.kw, T);
     if ((rc = check_launch("psf gradient (columns)")) != CVN_OK) return rc;
   }
