@@ -43,6 +43,10 @@ __device__ __forceinline__ int pad_src(int i, int n, int p, int mode) {
 
 __device__ __forceinline__ float gelu_exact(float v) { return gelu_fast(v); }
 
+// Border sample q in [0, 2 pad) of a padded axis with n interior samples: padded index q (q < pad)
+// or n + q (the far border).
+__device__ __forceinline__ int border_idx(int q, int n, int pad) { return q < pad ? q : n + q; }
+
 // Global-memory loops issue kBatch independent loads per thread before using any of them, so each
 // wave keeps many requests in flight (a plain loop waits out the full memory latency per element).
 constexpr int kBatch = 8;
@@ -628,6 +632,13 @@ struct RowInvArgs {
   int Hs, Ws, NCs;
   int row0, nrows, col0, ncols;  // crop window
   int rpb, act;
+  // Padding adjoint on the store (pad >= 0; crop window = the whole padded grid): row r of the
+  // padded grid, its border columns folded into their padding sources, goes to out row r - pad
+  // (interior rows, out is (P, nrows - 2 pad, ncols - 2 pad)) or to side row q (border row q,
+  // side is (P, 2 pad, ncols - 2 pad)); k_pad_rows_fold then adds the side rows to their sources.
+  int pad, pmode;
+  float* side;
+  int csrc_off;      // byte offset in LDS of the 2 pad column padding sources (pad >= 0)
   FftPlan plan;      // length Ws
   const char* tabs;  // the plan's tables (build_plan_tabs)
   int rad_off;       // byte offset of the plan's Rader tables in LDS
@@ -644,6 +655,10 @@ __global__ void __launch_bounds__(256) k_rows_inv(RowInvArgs a) {
   const int r0 = blockIdx.x * a.rpb;  // local output row
   char* rad = (char*)sm + a.rad_off;
   load_plan_tabs(a.plan, a.tabs, tw, rad, tid, nth);
+  int* csrc = (int*)((char*)sm + a.csrc_off);
+  if (a.pad >= 0 && a.pmode != CVN_PAD_ZEROS)
+    for (int q = tid; q < 2 * a.pad; q += nth)
+      csrc[q] = pad_src(border_idx(q, a.ncols - 2 * a.pad, a.pad), a.ncols - 2 * a.pad, a.pad, a.pmode);
   const float2* SHp = a.SH + plane * (int64_t)a.NCs * a.Hs;
   const FastDiv fL = fast_div(L), frpb = fast_div(a.rpb), fnc = fast_div(a.ncols);
   // stage the half spectra: Bf[rl * NCs + v]
@@ -679,6 +694,44 @@ __global__ void __launch_bounds__(256) k_rows_inv(RowInvArgs a) {
   }
   __syncthreads();
   const float2* Z = fft_lds<true>(a.plan, A, Bf, ntr, tw, tid, nth, rad);
+  if (a.pad >= 0) {
+    const int pad = a.pad, Hd = a.nrows - 2 * pad, Wd = a.ncols - 2 * pad;
+    const int nb = (a.pmode == CVN_PAD_ZEROS) ? 0 : 2 * pad;
+    // edge columns j <= pad or j >= Wd - 1 - pad are the only padding sources of border columns
+    const bool all_edge = nb > 0 && Wd <= 2 * pad + 2;
+    const int ne = nb == 0 ? 0 : (all_edge ? Wd : 2 * pad + 2);
+    auto put = [&](int rl, int j, float v) {
+      const int r = r0 + rl;
+      if (r >= pad && r < pad + Hd)
+        a.out[(plane * Hd + (r - pad)) * (int64_t)Wd + j] = v;
+      else if (nb > 0)
+        a.side[(plane * nb + (r < pad ? r : r - Hd)) * (int64_t)Wd + j] = v;
+    };
+    if (!all_edge) {
+      const FastDiv fW = fast_div(Wd);
+      for (int idx = tid; idx < a.rpb * Wd; idx += nth) {
+        const int rl = idx / fW, j = idx - rl * Wd;
+        if (r0 + rl >= a.nrows || (nb > 0 && (j <= pad || j >= Wd - 1 - pad))) continue;
+        const float2 z = Z[(rl >> 1) * L + j + pad];
+        put(rl, j, (rl & 1) ? z.y : z.x);
+      }
+    }
+    for (int idx = tid; idx < a.rpb * ne; idx += nth) {
+      const int rl = idx / ne, e = idx - rl * ne;
+      if (r0 + rl >= a.nrows) continue;
+      const int j = (all_edge || e <= pad) ? e : Wd - 1 - pad + (e - pad - 1);
+      const float2* zr = Z + (rl >> 1) * L;
+      const bool odd = rl & 1;
+      float v = odd ? zr[j + pad].y : zr[j + pad].x;
+      for (int qb = 0; qb < nb; ++qb)
+        if (csrc[qb] == j) {
+          const float2 z = zr[border_idx(qb, Wd, pad)];
+          v += odd ? z.y : z.x;
+        }
+      put(rl, j, v);
+    }
+    return;
+  }
   float* op = a.out + plane * (int64_t)a.nrows * a.ncols;
   for (int idx = tid; idx < a.rpb * a.ncols; idx += nth) {
     const int rl = idx / fnc, cc = idx - rl * a.ncols;
@@ -883,49 +936,19 @@ __global__ void __launch_bounds__(kColsBwdThreads) k_cols_bwd(ColBwdArgs a) {
   }
 }
 
-// Adjoint of the padding: dx[i][j] = sum of dy over the padded samples that copy source (i, j).
-// Grid (ceil(W / 256), ceil(H / kPadRows), planes).  Only samples within pad + 1 of an edge receive
-// border terms (in every mode); for those the 2 pad border rows / columns are scanned for the ones
-// whose padding source is i / j (no local arrays: runtime-indexed ones would live in scratch memory).
-__device__ __forceinline__ int border_idx(int q, int n, int pad) { return q < pad ? q : n + q; }
-
-constexpr int kPadRows = 16;  // rows per thread in k_pad_adj
-__global__ void __launch_bounds__(256) k_pad_adj(const float* __restrict__ dy, int H, int W, int pad, int mode,
-                                                 float* __restrict__ dx) {
-  extern __shared__ int psrc[];  // padding source of border row q: psrc[q]; of border column q: psrc[2 pad + q]
-  const int nb = (mode == CVN_PAD_ZEROS) ? 0 : 2 * pad;
-  for (int q = threadIdx.x; q < nb; q += blockDim.x) {
-    psrc[q] = pad_src(border_idx(q, H, pad), H, pad, mode);
-    psrc[nb + q] = pad_src(border_idx(q, W, pad), W, pad, mode);
-  }
-  __syncthreads();
+// Second half of the padding adjoint (the first is k_rows_inv's store): border row q of every
+// plane, already folded along its columns, is added to its padding source row.  Thread = (plane,
+// column j); the 2 pad border rows are added in order by that one thread, so rows that share a
+// source (replicate, wide reflect) need no atomics.
+__global__ void __launch_bounds__(256) k_pad_rows_fold(const float* __restrict__ side, int H, int W, int pad, int mode,
+                                                       float* __restrict__ dx) {
   const int j = blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= W) return;
-  const int i0 = blockIdx.y * kPadRows;
-  const int64_t plane = blockIdx.z;
-  const int w = W + 2 * pad;
-  const float* p = dy + plane * (int64_t)(H + 2 * pad) * w;
-  float v[kPadRows];
-#pragma unroll
-  for (int k = 0; k < kPadRows; ++k) v[k] = (i0 + k < H) ? p[(int64_t)(i0 + k + pad) * w + j + pad] : 0.f;
-  const int nc = (nb > 0 && (j <= pad || j >= W - 1 - pad)) ? nb : 0;
-#pragma unroll
-  for (int k = 0; k < kPadRows; ++k) {
-    const int i = i0 + k;
-    if (i >= H) break;
-    float acc = v[k];
-    for (int qb = 0; qb < nc; ++qb)  // border columns of the interior row
-      if (psrc[nb + qb] == j) acc += p[(int64_t)(i + pad) * w + border_idx(qb, W, pad)];
-    if (nb > 0 && (i <= pad || i >= H - 1 - pad)) {
-      for (int qa = 0; qa < nb; ++qa) {  // border rows whose padding source is row i
-        if (psrc[qa] != i) continue;
-        const float* row = p + (int64_t)border_idx(qa, H, pad) * w;
-        acc += row[j + pad];
-        for (int qb = 0; qb < nc; ++qb)
-          if (psrc[nb + qb] == j) acc += row[border_idx(qb, W, pad)];
-      }
-    }
-    dx[(plane * H + i) * (int64_t)W + j] = acc;
+  const int64_t plane = blockIdx.y;
+  const int nb = 2 * pad;
+  for (int q = 0; q < nb; ++q) {
+    const int i = pad_src(border_idx(q, H, pad), H, pad, mode);
+    dx[(plane * H + i) * (int64_t)W + j] += side[(plane * nb + q) * (int64_t)W + j];
   }
 }
 
@@ -1346,16 +1369,19 @@ int launch_rows_fwd(const float* x, int64_t P, int Hin, int Win, int pad, int mo
 }
 
 int launch_rows_inv(const float2* SH, const Geo& g, int row0, int nrows, int col0, int ncols,
-                    int act, const char* tabs, float* out, hipStream_t st) {
+                    int act, const char* tabs, float* out, hipStream_t st, int pad = -1, int pmode = 0,
+                    float* side = nullptr) {
   RowInvArgs a;
   a.SH = SH; a.out = out; a.Hs = g.Hs; a.Ws = g.Ws; a.NCs = g.NCs;
   a.row0 = row0; a.nrows = nrows; a.col0 = col0; a.ncols = ncols; a.act = act;
+  a.pad = pad; a.pmode = pmode; a.side = side;
   a.rpb = rows_per_block(g.Ws, nrows);
   if (!make_plan(g.Ws, &a.plan)) return fail(CVN_ERR_UNSUPPORTED, "no plan for length %d", g.Ws);
   a.rad_off = (int)align_up(rows_lds(g.Ws, a.rpb), 16);
+  a.csrc_off = (int)(a.rad_off + rader_lds_bytes(a.plan));
   a.tabs = tabs;
   dim3 grid((nrows + a.rpb - 1) / a.rpb, (unsigned)g.P);
-  hipLaunchKernelGGL(k_rows_inv, grid, dim3(kThreads), a.rad_off + rader_lds_bytes(a.plan), st, a);
+  hipLaunchKernelGGL(k_rows_inv, grid, dim3(kThreads), a.csrc_off + sizeof(int) * 2 * std::max(pad, 0), st, a);
   return check_launch("row inverse pass");
 }
 
@@ -1690,17 +1716,21 @@ extern "C" int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int
     hipLaunchKernelGGL(k_cols_bwd, grid, dim3(kColsBwdThreads), lds, st, a);
     if ((rc = check_launch("backward column pass")) != CVN_OK) return rc;
   }
-  // dy = C2R rows of dS (LR grid, uncropped), then the padding adjoint
+  // dx = pad^T(C2R rows of dS): interior rows and the column folds on the row pass's store, the
+  // border rows (in the Sg scratch, free after the column pass) folded in afterwards
   if (grad_x) {
     Geo gl = g;
     gl.Hs = g.h; gl.Ws = g.w; gl.NCs = g.NC;
-    float* dy = (float*)(base + ws.Sg);
-    if ((rc = launch_rows_inv(Sx, gl, 0, g.h, 0, g.w, CVN_ACT_NONE, tabs + t.off[kTabW], dy, st)) != CVN_OK) return rc;
-    if (g.H > 65535) return fail(CVN_ERR_UNSUPPORTED, "input height exceeds 65535");
-    hipLaunchKernelGGL(k_pad_adj, dim3((unsigned)((g.W + 255) / 256), (unsigned)((g.H + kPadRows - 1) / kPadRows),
-                                       (unsigned)g.P), dim3(256), (size_t)4 * 4 * std::max(1, g.pad), st, dy, g.H, g.W,
-                       g.pad, pad_mode, grad_x);
-    if ((rc = check_launch("padding adjoint")) != CVN_OK) return rc;
+    float* side = (float*)(base + ws.Sg);
+    if ((rc = launch_rows_inv(Sx, gl, 0, g.h, 0, g.w, CVN_ACT_NONE, tabs + t.off[kTabW], grad_x, st, g.pad, pad_mode,
+                              side)) != CVN_OK)
+      return rc;
+    if (pad_mode != CVN_PAD_ZEROS && g.pad > 0) {
+      if (g.P > 65535) return fail(CVN_ERR_UNSUPPORTED, "too many planes for the padding adjoint");
+      hipLaunchKernelGGL(k_pad_rows_fold, dim3((unsigned)((g.W + 255) / 256), (unsigned)g.P), dim3(256), 0, st, side,
+                         g.H, g.W, g.pad, pad_mode, grad_x);
+      if ((rc = check_launch("padding adjoint")) != CVN_OK) return rc;
+    }
   }
   if (!wg) return CVN_OK;
   {
