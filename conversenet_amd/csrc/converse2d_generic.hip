@@ -779,6 +779,7 @@ __host__ __device__ inline size_t cols_bwd_lds(int h, int Hs, int s, int cpb, bo
 
 constexpr int kColsBwdThreads = 512;  // 2 blocks of 8 waves per CU at the cfg3 LDS size
 constexpr int kColRegs = 4;           // per-thread register slots of the scale-1 path
+constexpr int kColLoad = 4;           // column elements per array loaded per thread and batch
 
 __global__ void __launch_bounds__(kColsBwdThreads) k_cols_bwd(ColBwdArgs a) {
   extern __shared__ float2 sm[];
@@ -827,42 +828,32 @@ __global__ void __launch_bounds__(kColsBwdThreads) k_cols_bwd(ColBwdArgs a) {
     const float2* Sgp = a.Sg + plane * (int64_t)a.NCs * a.Hs;
     float2* Sxp = a.Sx + plane * (int64_t)a.NC * a.h;
     __syncthreads();  // the previous plane's LDS reads are done
-    // member columns vb = v0 + b w of each class (row spectra of real rows are Hermitian in the column)
-    for (int i0 = tid; i0 < cpb * sH; i0 += kBatch * nth) {
-      float2 val[kBatch];
+    // member columns vb = v0 + b w of each class (row spectra of real rows are Hermitian in the
+    // column); the Sg and Sx loads of a batch are all issued before the first LDS store, so a
+    // plane waits for one HBM round trip, not two
+    const int nG = cpb * sH, nX = wg ? cpb * a.h : 0;
+    for (int i0 = tid; i0 < max(nG, nX); i0 += kColLoad * nth) {
+      float2 vg[kColLoad], vx[kColLoad];
 #pragma unroll
-      for (int k = 0; k < kBatch; ++k) {
+      for (int k = 0; k < kColLoad; ++k) {
         const int idx = i0 + k * nth;
-        val[k] = make_float2(0.f, 0.f);
-        if (idx < cpb * sH) {
+        vg[k] = make_float2(0.f, 0.f);
+        vx[k] = make_float2(0.f, 0.f);
+        if (idx < nG) {
           const int cl = idx / fsH, r = idx - cl * sH;
           const int b = r / fHs, u = r - b * a.Hs;
           if (cl < ncol) {
             const int vb = vbase + cl + b * a.w;
-            val[k] = vb <= a.Ws / 2 ? Sgp[(int64_t)vb * a.Hs + u] : cconj(Sgp[(int64_t)(a.Ws - vb) * a.Hs + u]);
+            vg[k] = vb <= a.Ws / 2 ? Sgp[(int64_t)vb * a.Hs + u] : cconj(Sgp[(int64_t)(a.Ws - vb) * a.Hs + u]);
           }
         }
+        if (idx < nX && idx < ncol * a.h) vx[k] = Sxp[(int64_t)vbase * a.h + idx];  // columns vbase.. are contiguous
       }
 #pragma unroll
-      for (int k = 0; k < kBatch; ++k) {
+      for (int k = 0; k < kColLoad; ++k) {
         const int idx = i0 + k * nth;
-        if (idx < cpb * sH) Xa[idx] = val[k];
-      }
-    }
-    if (wg) {
-      for (int i0 = tid; i0 < cpb * a.h; i0 += kBatch * nth) {
-        float2 val[kBatch];
-#pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-          const int idx = i0 + k * nth;
-          val[k] = make_float2(0.f, 0.f);
-          if (idx < ncol * a.h) val[k] = Sxp[(int64_t)vbase * a.h + idx];  // columns vbase.. are contiguous
-        }
-#pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-          const int idx = i0 + k * nth;
-          if (idx < cpb * a.h) Ya[idx] = val[k];
-        }
+        if (idx < nG) Xa[idx] = vg[k];
+        if (idx < nX) Ya[idx] = vx[k];
       }
     }
     __syncthreads();
