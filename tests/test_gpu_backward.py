@@ -75,6 +75,36 @@ def test_backward_x_only_and_weights_only():
     _close(gb.cpu().numpy(), rb, 2e-4, "grad_bias only")
 
 
+@pytest.mark.parametrize("need", [(True, False, False), (False, True, True)])
+def test_backward_partial_scale1(need):
+    """Scale 1, the column pass's register path: grad_x alone (no input column transforms, no dPhi)
+    and the weight gradients alone."""
+    from conversenet_amd import functional as Fh
+    x, w, b, g = _inputs(2, 3, 30, 26, 5, 1, 1, 5)
+    rx, rw, rb = O.converse2d_module_backward(x, w, b, g, 1, 2, "circular", 1e-5)
+    gx, gw, gb = Fh.converse2d_backward(_t(g), _t(x), _t(w), _t(b), 1, 2, "circular", 1e-5, *need)
+    if need[0]:
+        assert gw is None and gb is None
+        _close(gx.cpu().numpy(), rx, 1e-4, "grad_x only")
+    else:
+        assert gx is None
+        _close(gw.cpu().numpy(), rw, 2e-4, "grad_weight only")
+        _close(gb.cpu().numpy(), rb, 2e-4, "grad_bias only")
+
+
+def test_backward_scale1_plane_past_register_path():
+    """A 2100-sample padded side at scale 1: one column class per block holds 2100 elements, more than
+    the 4 x 512 register slots, so the column pass reads conj(Phi') per element instead.  grad_x only:
+    the weight gradient's own transfer-function pass does not take planes this large."""
+    from conversenet_amd import functional as Fh
+    x, w, b, g = _inputs(1, 1, 2096, 2096, 3, 1, 1, 11)
+    rx, _, _ = O.converse2d_module_backward(x, w, b, g, 1, 2, "circular", 1e-5)
+    gx, gw, gb = Fh.converse2d_backward(_t(g), _t(x), _t(w), _t(b), 1, 2, "circular", 1e-5, True, False, False)
+    torch.cuda.synchronize()
+    assert gw is None and gb is None
+    _close(gx.cpu().numpy(), rx, 1e-4, "grad_x")
+
+
 def test_autograd_through_module():
     """Converse2D on HIP tensors that require grad runs the library's forward and backward; loss.backward()
     fills x.grad, weight.grad and bias.grad as the oracle says."""
