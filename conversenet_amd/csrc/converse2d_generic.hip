@@ -1440,7 +1440,8 @@ void bwd_layout(const Geo& g, const PlanTabs& t, BwdWs* w) {
   size_t o = 0;
   w->tabs = o; o += align_up(t.bytes);
   w->phi = o; o += align_up((size_t)g.Cp * g.NCs * g.Hs * sizeof(float2));
-  w->Sg = o; o += align_up((size_t)g.P * g.NCs * g.Hs * sizeof(float2));  // then the padding adjoint's border rows (P 2 pad W floats)
+  // Sg: row spectra of the output gradient, then the padding adjoint's border rows (P 2 pad W floats)
+  w->Sg = o; o += align_up((size_t)g.P * g.NCs * g.Hs * sizeof(float2));
   w->Sx = o; o += align_up((size_t)g.P * g.NC * g.h * sizeof(float2));
   // weight-gradient chunks over all w column classes, as in launch_phi
   w->nchunk = (int)std::min<int64_t>(g.w, std::max<int64_t>(1, (2048 + g.Cp - 1) / g.Cp));
