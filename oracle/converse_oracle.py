@@ -22,11 +22,13 @@ How each function is pinned (checked by tests/test_oracle.py and tests/test_orac
                       autograd (fp64) of the reference op sequence restated in torch
   layernorm_cf        zero mean / unit biased variance closed form; torch F.layer_norm
   conv1x1, gelu       einsum definition; erf special values; torch F.conv2d / F.gelu
-  converse_block, converse_dncnn, conv_reverse_datanet, converse_usrnet, msrresnet,
+  converse_block, converse_dncnn, conv_reverse_datanet, kernelnet, converse_usrnet, converse_net,
   converse_msrresnet, converse_up_msrresnet
-                      compositions of the pinned pieces (structure follows the reference classes)
-  conv3x3, pixel_shuffle, bilinear_upsample
-                      torch F.conv2d / nn.PixelShuffle / F.interpolate(bilinear) on the CPU
+                      outputs of the reference's own model classes (imported in the build
+                      container by tests/golden/make_model_golden.py) on seeded state dicts:
+                      tests/test_oracle_models.py, with planted mistakes that must fail
+  conv3x3, bilinear_upsample
+                      torch F.conv2d / F.interpolate(bilinear) on the CPU
 """
 from __future__ import annotations
 
@@ -365,10 +367,10 @@ def converse_dncnn(x, sd, kernel_size=7, padding=6, padding_mode="circular", num
     return conv1x1(x, sd["m_tail.0.weight"], sd["m_tail.0.bias"], dtype)
 
 
-def conv_reverse_datanet(x, k, sf, alpha, eps=1e-3, dtype=np.float64):
-    """ConvReverseDataNet.forward with padding 0 (models/converse_usrnet.py:41-68): the op with a
-    per-sample psf k (B,C,kh,kw), lambda from alpha, x0 = nearest(x)."""
-    return converse2d_op(x, nearest(x, sf), k, alpha, sf, eps, dtype)
+def conv_reverse_datanet(x, k, sf, alpha, eps=1e-3, padding=0, padding_mode="circular", dtype=np.float64):
+    """ConvReverseDataNet.forward (models/converse_usrnet.py:41-68): pad, the op with a per-sample psf
+    k (B,C,kh,kw), lambda from alpha, x0 = nearest(padded x), crop."""
+    return converse2d_module(x, k, alpha, sf, padding, padding_mode, eps, dtype)
 
 
 def kernelnet(k, sd, prefix, kernel_size, dtype=np.float64):
@@ -380,6 +382,16 @@ def kernelnet(k, sd, prefix, kernel_size, dtype=np.float64):
     t = gelu(lin(t, "fc2"))
     t = lin(t, "fc3")
     return t.reshape(b, 16, kernel_size, kernel_size)
+
+
+def converse_net(x, sd, num_iterations=5, num_blocks=7, dtype=np.float64):
+    """ConverseNet.forward (models/converse_usrnet.py:150-169): 1x1 3->64, the same
+    MultiConverseBlock (k3, padding 2, circular) applied num_iterations times, 1x1 64->3."""
+    x = conv1x1(x, sd["conv1.weight"], sd["conv1.bias"], dtype)
+    for _ in range(num_iterations):
+        for j in range(num_blocks):
+            x = converse_block(x, sd, f"p.m_body.{j}.", 3, 1, 2, "circular", 1e-5, False, dtype)
+    return conv1x1(x, sd["conv2.weight"], sd["conv2.bias"], dtype)
 
 
 def converse_usrnet(x, k, sf, sd, kernel_size, num_iterations=5, num_blocks=7, dtype=np.float64):
@@ -396,7 +408,7 @@ def converse_usrnet(x, k, sf, sd, kernel_size, num_iterations=5, num_blocks=7, d
     for i in range(num_iterations):
         k_ = conv1x1(kk, sd[f"convs.{i}.weight"], sd[f"convs.{i}.bias"], dtype)
         k_ = k_.reshape(b, 64, kernel_size, kernel_size)
-        x = conv_reverse_datanet(x, k_, sf if i == 0 else 1, sd["d.alpha"], 1e-3, dtype)
+        x = conv_reverse_datanet(x, k_, sf if i == 0 else 1, sd["d.alpha"], 1e-3, dtype=dtype)
         x = body(x)
     return conv1x1(x, sd["conv2.weight"], sd["conv2.bias"], dtype)
 
@@ -417,17 +429,6 @@ def conv3x3(x, weight, bias, dtype=np.float64):
     if bias is not None:
         y += bias.astype(dtype)[None, :, None, None]
     return y
-
-
-def pixel_shuffle(x, r):
-    """nn.PixelShuffle(r): out[b, c, h r + i, w r + j] = in[b, c r^2 + i r + j, h, w]."""
-    B, Cr, H, W = x.shape
-    C = Cr // (r * r)
-    return x.reshape(B, C, r, r, H, W).transpose(0, 1, 4, 2, 5, 3).reshape(B, C, H * r, W * r)
-
-
-def leaky_relu(x, slope=0.1):
-    return np.where(x >= 0, x, slope * x)
 
 
 def bilinear_upsample(x, s):
@@ -452,22 +453,6 @@ def residual_block(x, sd, prefix, dtype=np.float64):
     """ResidualBlock (util_converse.py:328-342): x + conv2(relu(conv1(x)))."""
     t = np.maximum(conv3x3(x, sd[prefix + "conv1.weight"], sd[prefix + "conv1.bias"], dtype), 0.0)
     return x + conv3x3(t, sd[prefix + "conv2.weight"], sd[prefix + "conv2.bias"], dtype)
-
-
-def msrresnet(x, sd, num_blocks=16, upscale=4, dtype=np.float64):
-    """MSRResNet.forward (models/converse_srresnet.py:33-47)."""
-    x = x.astype(dtype)
-    x1 = leaky_relu(conv3x3(x, sd["conv_first.weight"], sd["conv_first.bias"], dtype))
-    for i in range(num_blocks):
-        x1 = residual_block(x1, sd, f"conv_body.{i}.", dtype)
-    if upscale == 4:
-        x1 = leaky_relu(pixel_shuffle(conv3x3(x1, sd["upconv1.weight"], sd["upconv1.bias"], dtype), 2))
-        x1 = leaky_relu(pixel_shuffle(conv3x3(x1, sd["upconv2.weight"], sd["upconv2.bias"], dtype), 2))
-    elif upscale in (2, 3):
-        x1 = leaky_relu(pixel_shuffle(conv3x3(x1, sd["upconv1.weight"], sd["upconv1.bias"], dtype), upscale))
-    x1 = conv3x3(leaky_relu(conv3x3(x1, sd["conv_hres.weight"], sd["conv_hres.bias"], dtype)),
-                 sd["conv_last.weight"], sd["conv_last.bias"], dtype)
-    return x1 + bilinear_upsample(x, upscale)
 
 
 def converse_msrresnet(x, sd, num_blocks=16, upscale=4, dtype=np.float64):
