@@ -169,9 +169,10 @@ def synthetic_image(torch, g, H=256, W=256):
     return img.float()
 
 
-def make_dncnn(torch, dev):
+def make_dncnn(torch, dev, batch=8):
     """Converse-DnCNN (cfg4): default constructor (k7, p6, circular, 20 blocks, 796,353 params),
-    random init (seed 0), B=8 synthetic 1x256x256 images plus N(0, (25/255)^2) noise, not clipped."""
+    random init (seed 0), B=8 synthetic 1x256x256 images plus N(0, (25/255)^2) noise, not clipped.
+    batch < 8 gives the first images of the same batch."""
     sys.path.insert(0, ROOT)
     from conversenet_amd.converse_dncnn import ConverseDnCNN
 
@@ -179,16 +180,16 @@ def make_dncnn(torch, dev):
     m = ConverseDnCNN().to(dev).eval()
     g = torch.Generator().manual_seed(0)
     clean = torch.stack([synthetic_image(torch, g)[None] for _ in range(8)])
-    x = (clean + torch.randn(clean.shape, generator=g) * (25 / 255)).to(dev)
+    x = (clean + torch.randn(clean.shape, generator=g) * (25 / 255))[:batch].to(dev)
     return m, x
 
 
-def make_usrnet(torch, dev):
+def make_usrnet(torch, dev, batch=4):
     """Converse-USRNet (cfg5) with KernelNet(kernel_size=25), random init (seed 0), alpha1 / alpha2 /
     d.alpha drawn from N(0, 0.1) so the body blocks contribute.  Input: B=4 RGB 256x256 synthetic images
     blurred circularly by a seeded 25x25 anisotropic Gaussian (sigma1, sigma2 ~ U[0.7, 3], angle ~ U[0, pi),
     centred at (12, 12), sum 1), decimated [0::4, 0::4], plus N(0, (2.55/255)^2); the kernel is the
-    model's second input, scale factor 4."""
+    model's second input, scale factor 4.  batch < 4 gives the first images of the same batch."""
     sys.path.insert(0, ROOT)
     from conversenet_amd.converse_usrnet import ConverseUSRNet
 
@@ -200,7 +201,7 @@ def make_usrnet(torch, dev):
     m = m.to(dev).eval()
     g = torch.Generator().manual_seed(0)
     xs, ks = [], []
-    for _ in range(4):
+    for _ in range(batch):
         hr = torch.stack([synthetic_image(torch, g) for _ in range(3)]).double()
         s1, s2 = (0.7 + 2.3 * torch.rand(2, generator=g, dtype=torch.float64)).tolist()
         th = float(math.pi * torch.rand(1, generator=g, dtype=torch.float64))

@@ -20,6 +20,7 @@ CVN_ERR_WORKSPACE = -3
 CVN_ERR_HIP = -4
 
 PAD_MODES = {"constant": 0, "zeros": 0, "reflect": 1, "replicate": 2, "circular": 3}
+ROUTE_AUTO, ROUTE_FUSED, ROUTE_PFA268, ROUTE_GENERIC = 0, 1, 2, 3
 ACT_NONE = 0
 ACT_GELU = 1
 
@@ -36,15 +37,22 @@ SIGNATURES = {
     "cvn_converse2d_fwd_workspace": (_size, [_i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int]),
     "cvn_converse2d_fwd_f32": (_int, [_ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _int, _int, _ptr, _f32, _int,
                                       _int, _int, _int, _ptr, _ptr, _size, _ptr]),
-    "cvn_converse2d_table_bytes": (_size, [_i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int]),
-    "cvn_converse2d_scratch_bytes": (_size, [_i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int]),
+    "cvn_converse2d_route": (_int, [_i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int]),
+    "cvn_converse2d_supported": (_int, [_i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _int, _int]),
+    "cvn_converse2d_table_bytes": (_size, [_i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _int]),
+    "cvn_converse2d_scratch_bytes": (_size, [_i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _int]),
     "cvn_converse2d_table_f32": (_int, [_ptr, _i64, _int, _int, _ptr, _f32, _i64, _i64, _i64, _i64, _int, _int,
-                                        _ptr, _size, _ptr]),
+                                        _int, _ptr, _size, _ptr]),
     "cvn_converse2d_apply_f32": (_int, [_ptr, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _int, _int,
-                                        _ptr, _ptr, _size, _ptr, _ptr]),
+                                        _int, _ptr, _size, _ptr, _size, _ptr, _ptr]),
     "cvn_converse2d_op_workspace": (_size, [_i64, _i64, _i64, _i64, _int, _int, _int]),
     "cvn_converse2d_op_f32": (_int, [_ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _int, _int, _ptr, _f32, _int, _ptr,
                                      _ptr, _size, _ptr]),
+    "cvn_converse2d_op_table_bytes": (_size, [_i64, _i64, _i64, _int, _int, _int]),
+    "cvn_converse2d_op_scratch_bytes": (_size, [_i64, _i64, _i64, _i64, _int]),
+    "cvn_converse2d_op_table_f32": (_int, [_ptr, _int, _int, _ptr, _f32, _i64, _i64, _i64, _int, _ptr, _size, _ptr]),
+    "cvn_converse2d_op_apply_f32": (_int, [_ptr, _ptr, _i64, _i64, _i64, _i64, _int, _ptr, _size, _ptr, _size, _ptr,
+                                           _ptr]),
     "cvn_converse2d_bwd_workspace": (_size, [_i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int]),
     "cvn_converse2d_bwd_f32": (_int, [_ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _int, _int, _ptr, _f32, _int,
                                       _int, _int, _ptr, _ptr, _ptr, _ptr, _size, _ptr]),

@@ -10,8 +10,8 @@ import torch
 import torch.nn as nn
 
 from . import composite, functional
-from .util_converse import (_hip_grad_eligible, ConverseBlock, ConverseBlockAlphaVariant, _hip_eligible, run_blocks,
-                            sequential)
+from .util_converse import (_converse_hip, _hip_grad_eligible, ConverseBlock, ConverseBlockAlphaVariant,
+                            _hip_eligible, run_blocks, sequential)
 
 
 class MultiConverseBlock(nn.Module):
@@ -55,9 +55,11 @@ class ConvReverseDataNet(nn.Module):
         self.__dict__["_biaseps"] = v
 
     def forward(self, x, k, sf, padding=0, padding_mode="circular"):
-        if _hip_eligible(x, k, self.alpha):
+        if _converse_hip(x, k, self.alpha, sf, padding):
             self.biaseps = None  # read lazily from the current alpha
-            return functional.converse2d_fused(x, k, self.alpha.reshape(-1), sf, padding, padding_mode, self.eps)
+            # k is an activation computed anew on every forward: its table is never reused, so not cached
+            return functional.converse2d_fused(x, k, self.alpha.reshape(-1), sf, padding, padding_mode, self.eps,
+                                               cache=False)
         if k.dim() == 4 and _hip_grad_eligible(x, k, self.alpha, sf, padding, padding_mode):
             self.biaseps = None
             return functional.converse2d_train(x, k, self.alpha, sf, padding, padding_mode, self.eps)

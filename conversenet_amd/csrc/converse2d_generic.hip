@@ -1388,34 +1388,39 @@ bool cvn::fused_disabled() {
 
 namespace {
 
-// Which kernels serve a module-level call, and the table / scratch sizes they need.  The table
-// holds the transfer function in the layout of the chosen kernels; it depends only on the psf,
-// bias, eps and geometry, so callers may cache it across calls with unchanged weights.
+// Which kernels serve a module-level call (CVN_ROUTE_*), and the table / scratch sizes they need.
+// The table holds the transfer function in the layout of the route's kernels; it depends only on the
+// psf, bias, eps and geometry, so callers may cache it across calls with unchanged weights, keeping
+// the route next to it.
 struct Route {
-  bool fused;
-  bool pfa;  // 268 x 268 planes at scale 1: the 268 path (its table holds Phi in the quad layout)
+  int id;
   size_t table_bytes, scratch_bytes;
 };
 
 int module_route(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, int kh, int kw, int scale,
-                 int pad, Geo* g, Route* r) {
+                 int pad, int want, Geo* g, Route* r) {
   int rc = module_geo(B, C, H, W, psf_batch, kh, kw, scale, pad, g);
   if (rc != CVN_OK) return rc;
+  if (want < CVN_ROUTE_AUTO || want > CVN_ROUTE_GENERIC) return fail(CVN_ERR_ARG, "bad route %d", want);
   size_t fws = 0;
-  if (!fused_disabled() && kh <= 64 && fused_query(g->H, g->W, g->pad, g->s, g->Cp, &fws)) {
-    r->fused = true;
-    r->pfa = false;
+  const bool fused_ok = kh <= 64 && fused_query(g->H, g->W, g->pad, g->s, g->Cp, &fws);
+  const bool pfa_ok = pfa268_applies(g->h, g->w, g->s);
+  if (want == CVN_ROUTE_AUTO)
+    want = fused_disabled() ? CVN_ROUTE_GENERIC
+                            : fused_ok ? CVN_ROUTE_FUSED : pfa_ok ? CVN_ROUTE_PFA268 : CVN_ROUTE_GENERIC;
+  if ((want == CVN_ROUTE_FUSED && !fused_ok) || (want == CVN_ROUTE_PFA268 && !pfa_ok))
+    return fail(CVN_ERR_ARG, "route %d does not serve a %dx%d plane at scale %d", want, g->h, g->w, g->s);
+  r->id = want;
+  if (want == CVN_ROUTE_FUSED) {
     r->table_bytes = fws;
     r->scratch_bytes = 0;
-  } else {
-    PlanTabs t;
-    if (!plan_tabs(*g, &t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
-    const ModWs w = module_ws(*g, t);
-    r->fused = false;
-    r->pfa = !fused_disabled() && pfa268_applies(g->h, g->w, g->s);
-    r->table_bytes = w.S;
-    r->scratch_bytes = w.total - w.S;
+    return CVN_OK;
   }
+  PlanTabs t;
+  if (!plan_tabs(*g, &t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
+  const ModWs w = module_ws(*g, t);
+  r->table_bytes = w.S;
+  r->scratch_bytes = w.total - w.S;
   return CVN_OK;
 }
 
@@ -1456,21 +1461,48 @@ void bwd_layout(const Geo& g, const PlanTabs& t, BwdWs* w) {
   w->total = o;
 }
 
+// Every limit of the backward for this geometry: the workspace layout, the column pass's classes per
+// block and LDS, or CVN_ERR_UNSUPPORTED with the reason.  wg: weight or bias gradients wanted.
+int bwd_check(const Geo& g, bool wg, PlanTabs* t, BwdWs* ws, int* cpb, size_t* col_lds) {
+  if (g.P > 65535) return fail(CVN_ERR_UNSUPPORTED, "B*C = %lld planes exceeds 65535", (long long)g.P);
+  if (wg && g.s > 4) return fail(CVN_ERR_UNSUPPORTED, "weight gradients support scale <= 4");
+  if (!plan_tabs(g, t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
+  bwd_layout(g, *t, ws);
+  if (wg && ws->lds > kGradLds) return fail(CVN_ERR_UNSUPPORTED, "plane too large for the weight gradient");
+  // column pass: up to 8 classes per block, LDS within 80 KiB where possible (2 blocks per CU)
+  const size_t rad = rader_lds_bytes(t->plan[kTabH]) + rader_lds_bytes(t->plan[kTabHs]);
+  *cpb = std::max(1, std::min(8, g.NC));
+  while (*cpb > 1 && align_up(cols_bwd_lds(g.h, g.Hs, g.s, *cpb, wg), 16) + rad > 80 * 1024) --*cpb;
+  *col_lds = align_up(cols_bwd_lds(g.h, g.Hs, g.s, *cpb, wg), 16) + rad;
+  if (*col_lds > kLdsLimit) return fail(CVN_ERR_UNSUPPORTED, "plane too large for the backward column pass");
+  if (wg && g.Cp * ws->nchunk > 0x7fffffff) return fail(CVN_ERR_UNSUPPORTED, "too many gradient blocks");
+  if (wg && g.Cp > 65535) return fail(CVN_ERR_UNSUPPORTED, "too many psf planes");
+  return CVN_OK;
+}
+
 }  // namespace
 
-extern "C" size_t cvn_converse2d_table_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, int kh,
-                                             int kw, int scale, int pad) {
+extern "C" int cvn_converse2d_route(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, int kh, int kw,
+                                    int scale, int pad) {
   Geo g;
   Route r;
-  if (module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, &g, &r) != CVN_OK) return 0;
+  const int rc = module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, CVN_ROUTE_AUTO, &g, &r);
+  return rc != CVN_OK ? rc : r.id;
+}
+
+extern "C" size_t cvn_converse2d_table_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, int kh,
+                                             int kw, int scale, int pad, int route) {
+  Geo g;
+  Route r;
+  if (module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, route, &g, &r) != CVN_OK) return 0;
   return r.table_bytes;
 }
 
 extern "C" size_t cvn_converse2d_scratch_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch,
-                                               int kh, int kw, int scale, int pad) {
+                                               int kh, int kw, int scale, int pad, int route) {
   Geo g;
   Route r;
-  if (module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, &g, &r) != CVN_OK) return 0;
+  if (module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, route, &g, &r) != CVN_OK) return 0;
   return r.scratch_bytes;
 }
 
@@ -1479,42 +1511,45 @@ extern "C" size_t cvn_converse2d_fwd_workspace(int64_t B, int64_t C, int64_t H, 
                                                int pad) {
   Geo g;
   Route r;
-  if (module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, &g, &r) != CVN_OK) return 0;
+  if (module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, CVN_ROUTE_AUTO, &g, &r) != CVN_OK) return 0;
   return align_up(r.table_bytes) + r.scratch_bytes;
 }
 
 extern "C" int cvn_converse2d_table_f32(const float* psf, int64_t psf_batch, int kh, int kw, const float* bias,
                                         float eps, int64_t B, int64_t C, int64_t H, int64_t W, int scale, int pad,
-                                        void* table, size_t table_bytes, cvn_stream_t stream) {
+                                        int route, void* table, size_t table_bytes, cvn_stream_t stream) {
   Geo g;
   Route r;
-  int rc = module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, &g, &r);
+  int rc = module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, route, &g, &r);
   if (rc != CVN_OK) return rc;
   if (!psf || !bias) return fail(CVN_ERR_ARG, "null pointer");
   if (!table || table_bytes < r.table_bytes)
     return fail(CVN_ERR_WORKSPACE, "table buffer too small: need %zu bytes", r.table_bytes);
   hipStream_t st = (hipStream_t)stream;
-  if (r.fused) return fused_table(psf, bias, eps, g.C, g.Cp / g.C, kh, kw, g.H, g.W, g.pad, table, st);
+  if (r.id == CVN_ROUTE_FUSED) return fused_table(psf, bias, eps, g.C, g.Cp / g.C, kh, kw, g.H, g.W, g.pad, table, st);
   PlanTabs t;
   if (!plan_tabs(g, &t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
   const ModWs ws = module_ws(g, t);
   if ((rc = launch_plan_tabs(t, (char*)table + ws.tabs, st)) != CVN_OK) return rc;
-  return launch_phi(psf, bias, eps, g, false, (float2*)table, nullptr, st, r.pfa);
+  return launch_phi(psf, bias, eps, g, false, (float2*)table, nullptr, st, r.id == CVN_ROUTE_PFA268);
 }
 
 extern "C" int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
                                         int64_t psf_batch, int kh, int kw, int scale, int pad, int pad_mode,
-                                        int act, const void* table, void* scratch, size_t scratch_bytes,
-                                        float* out, cvn_stream_t stream) {
+                                        int act, int route, const void* table, size_t table_bytes, void* scratch,
+                                        size_t scratch_bytes, float* out, cvn_stream_t stream) {
   Geo g;
   Route r;
-  int rc = module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, &g, &r);
+  int rc = module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, route, &g, &r);
   if (rc != CVN_OK) return rc;
   if ((rc = check_mode_act(H, W, pad, pad_mode, act)) != CVN_OK) return rc;
   if (!x || !table || !out) return fail(CVN_ERR_ARG, "null pointer");
+  if (table_bytes < r.table_bytes)
+    return fail(CVN_ERR_ARG, "table of %zu bytes is smaller than route %d needs (%zu)", table_bytes, r.id,
+                r.table_bytes);
   if (B == 0) return CVN_OK;
   hipStream_t st = (hipStream_t)stream;
-  if (r.fused) {
+  if (r.id == CVN_ROUTE_FUSED) {
     if (((uintptr_t)x & 15) || ((uintptr_t)out & 15))
       return fail(CVN_ERR_ARG, "the fused kernel needs 16-byte aligned input and output");
     if (B * C > 0x7fffffff) return fail(CVN_ERR_UNSUPPORTED, "too many planes");
@@ -1532,7 +1567,7 @@ extern "C" int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, in
   const char* tabs = (const char*)table + ws.tabs;
   float2* S = (float2*)(base + ws.S);
   float2* SH = (float2*)(base + ws.SH);
-  if (r.pfa)
+  if (r.id == CVN_ROUTE_PFA268)
     return pfa268_forward(x, g.P, g.C, g.Cp / g.C, g.H, g.W, g.pad, pad_mode, act, phi, S, out, st);
   if ((rc = launch_rows_fwd(x, g.P, g.H, g.W, g.pad, pad_mode, g.h, g.w, tabs + t.off[kTabW], S, st)) != CVN_OK)
     return rc;
@@ -1559,7 +1594,7 @@ extern "C" int cvn_converse2d_fwd_f32(const float* x, int64_t B, int64_t C, int6
                                       size_t workspace_bytes, cvn_stream_t stream) {
   Geo g;
   Route r;
-  int rc = module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, &g, &r);
+  int rc = module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, CVN_ROUTE_AUTO, &g, &r);
   if (rc != CVN_OK) return rc;
   if ((rc = check_mode_act(H, W, pad, pad_mode, act)) != CVN_OK) return rc;
   if (!x || !psf || !bias || !out) return fail(CVN_ERR_ARG, "null pointer");
@@ -1568,24 +1603,120 @@ extern "C" int cvn_converse2d_fwd_f32(const float* x, int64_t B, int64_t C, int6
   if (!workspace || workspace_bytes < tb + r.scratch_bytes)
     return fail(CVN_ERR_WORKSPACE, "workspace too small: need %zu bytes", tb + r.scratch_bytes);
   char* base = (char*)workspace;
-  rc = cvn_converse2d_table_f32(psf, psf_batch, kh, kw, bias, eps, B, C, H, W, scale, pad, base, tb, stream);
+  rc = cvn_converse2d_table_f32(psf, psf_batch, kh, kw, bias, eps, B, C, H, W, scale, pad, r.id, base, tb, stream);
   if (rc != CVN_OK) return rc;
-  return cvn_converse2d_apply_f32(x, B, C, H, W, psf_batch, kh, kw, scale, pad, pad_mode, act, base, base + tb,
-                                  workspace_bytes - tb, out, stream);
+  return cvn_converse2d_apply_f32(x, B, C, H, W, psf_batch, kh, kw, scale, pad, pad_mode, act, r.id, base, tb,
+                                  base + tb, workspace_bytes - tb, out, stream);
+}
+
+// Op-level path: the table (FFT plan tables, the OTF K and the alias-class table A of the psf) depends
+// on (psf, bias, eps, C, h, w, scale) only, like the reference's cached OTF (converse2d.cpp:52-102);
+// the scratch holds the row spectra of x and x0 and the HR spectra between the passes.
+namespace {
+struct OpLayout {
+  PlanTabs t;
+  size_t kf, A, table;       // table regions
+  size_t S, S0, SH, scratch;  // scratch regions
+};
+int op_layout(int64_t B, int64_t C, int64_t h, int64_t w, int kh, int kw, int scale, Geo* g, OpLayout* L) {
+  int rc = module_geo(B, C, h, w, 1, kh, kw, scale, 0, g);
+  if (rc != CVN_OK) return rc;
+  if (!plan_tabs(*g, &L->t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
+  size_t o = L->t.bytes;
+  L->kf = o; o += align_up((size_t)g->C * g->Ws * g->Hs * sizeof(float2));
+  L->A = o; o += align_up((size_t)g->C * g->Ws * g->Hs * sizeof(float2));
+  L->table = o;
+  o = 0;
+  L->S = o; o += align_up((size_t)g->P * g->NC * g->h * sizeof(float2));
+  L->S0 = o; o += align_up((size_t)g->P * g->NCs * g->Hs * sizeof(float2));
+  L->SH = o; o += align_up((size_t)g->P * g->NCs * g->Hs * sizeof(float2));
+  L->scratch = o;
+  return CVN_OK;
+}
+size_t op_col_lds(const Geo& g, const OpLayout& L) {
+  return align_up((size_t)(3 * g.h + g.Hs + 2 * g.s * g.Hs) * sizeof(float2), 16) +
+         rader_lds_bytes(L.t.plan[kTabH]) + rader_lds_bytes(L.t.plan[kTabHs]);
+}
+}  // namespace
+
+extern "C" size_t cvn_converse2d_op_table_bytes(int64_t C, int64_t h, int64_t w, int kh, int kw, int scale) {
+  Geo g;
+  OpLayout L;
+  if (op_layout(1, C, h, w, kh, kw, scale, &g, &L) != CVN_OK) return 0;
+  return L.table;
+}
+
+extern "C" size_t cvn_converse2d_op_scratch_bytes(int64_t B, int64_t C, int64_t h, int64_t w, int scale) {
+  Geo g;
+  OpLayout L;
+  if (op_layout(B, C, h, w, 1, 1, scale, &g, &L) != CVN_OK) return 0;
+  return L.scratch;
 }
 
 extern "C" size_t cvn_converse2d_op_workspace(int64_t B, int64_t C, int64_t h, int64_t w, int kh,
                                               int kw, int scale) {
   Geo g;
-  if (module_geo(B, C, h, w, 1, kh, kw, scale, 0, &g) != CVN_OK) return 0;
-  PlanTabs t;
-  if (!plan_tabs(g, &t)) return 0;
-  size_t o = t.bytes;                                               // FFT plan tables
-  o += 2 * align_up((size_t)g.C * g.Ws * g.Hs * sizeof(float2));  // kf, A
-  o += align_up((size_t)g.P * g.NC * g.h * sizeof(float2));        // S
-  o += align_up((size_t)g.P * g.NCs * g.Hs * sizeof(float2));      // S0
-  o += align_up((size_t)g.P * g.NCs * g.Hs * sizeof(float2));      // SH
-  return o;
+  OpLayout L;
+  if (op_layout(B, C, h, w, kh, kw, scale, &g, &L) != CVN_OK) return 0;
+  return L.table + L.scratch;
+}
+
+extern "C" int cvn_converse2d_op_table_f32(const float* psf, int kh, int kw, const float* bias, float eps, int64_t C,
+                                           int64_t h, int64_t w, int scale, void* table, size_t table_bytes,
+                                           cvn_stream_t stream) {
+  Geo g;
+  OpLayout L;
+  int rc = op_layout(1, C, h, w, kh, kw, scale, &g, &L);
+  if (rc != CVN_OK) return rc;
+  if (!psf || !bias) return fail(CVN_ERR_ARG, "null pointer");
+  if (!table || table_bytes < L.table)
+    return fail(CVN_ERR_WORKSPACE, "table buffer too small: need %zu bytes", L.table);
+  hipStream_t st = (hipStream_t)stream;
+  char* base = (char*)table;
+  if ((rc = launch_plan_tabs(L.t, base, st)) != CVN_OK) return rc;
+  return launch_phi(psf, bias, eps, g, true, (float2*)(base + L.A), (float2*)(base + L.kf), st);
+}
+
+extern "C" int cvn_converse2d_op_apply_f32(const float* x, const float* x0, int64_t B, int64_t C, int64_t h,
+                                           int64_t w, int scale, const void* table, size_t table_bytes,
+                                           void* scratch, size_t scratch_bytes, float* out, cvn_stream_t stream) {
+  Geo g;
+  OpLayout L;
+  int rc = op_layout(B, C, h, w, 1, 1, scale, &g, &L);
+  if (rc != CVN_OK) return rc;
+  if (!x || !x0 || !table || !out) return fail(CVN_ERR_ARG, "null pointer");
+  if (table_bytes < L.table) return fail(CVN_ERR_ARG, "op table of %zu bytes, need %zu", table_bytes, L.table);
+  if (B == 0) return CVN_OK;
+  if (!scratch || scratch_bytes < L.scratch)
+    return fail(CVN_ERR_WORKSPACE, "scratch too small: need %zu bytes", L.scratch);
+  if (g.P > 65535) return fail(CVN_ERR_UNSUPPORTED, "B*C exceeds 65535");
+  const size_t lds = op_col_lds(g, L);
+  if (lds > kLdsLimit) return fail(CVN_ERR_UNSUPPORTED, "column class does not fit in LDS");
+  set_lds_attrs();
+  hipStream_t st = (hipStream_t)stream;
+  const char* tabs = (const char*)table;
+  const float2* kf = (const float2*)(tabs + L.kf);
+  const float2* Am = (const float2*)(tabs + L.A);
+  char* sc = (char*)scratch;
+  float2* S = (float2*)(sc + L.S);
+  float2* S0 = (float2*)(sc + L.S0);
+  float2* SH = (float2*)(sc + L.SH);
+  if ((rc = launch_rows_fwd(x, g.P, g.h, g.w, 0, CVN_PAD_ZEROS, g.h, g.w, tabs + L.t.off[kTabW], S, st)) != CVN_OK)
+    return rc;
+  if ((rc = launch_rows_fwd(x0, g.P, g.Hs, g.Ws, 0, CVN_PAD_ZEROS, g.Hs, g.Ws, tabs + L.t.off[kTabWs], S0, st)) !=
+      CVN_OK)
+    return rc;
+  ColOpArgs ca;
+  ca.S = S; ca.S0 = S0; ca.kf = kf; ca.A = Am; ca.SH = SH; ca.C = g.C;
+  ca.h = g.h; ca.w = g.w; ca.s = g.s; ca.Hs = g.Hs; ca.Ws = g.Ws; ca.NC = g.NC; ca.NCs = g.NCs;
+  ca.plan_h = L.t.plan[kTabH];
+  ca.plan_H = L.t.plan[kTabHs];
+  ca.tabs_h = tabs + L.t.off[kTabH];
+  ca.tabs_H = tabs + L.t.off[kTabHs];
+  ca.rad_off = (int)align_up((size_t)(3 * g.h + g.Hs + 2 * g.s * g.Hs) * sizeof(float2), 16);
+  hipLaunchKernelGGL(k_cols_op, dim3(g.w, (unsigned)g.P), dim3(kThreads), lds, st, ca);
+  if ((rc = check_launch("op column pass")) != CVN_OK) return rc;
+  return launch_rows_inv(SH, g, 0, g.Hs, 0, g.Ws, CVN_ACT_NONE, tabs + L.t.off[kTabWs], out, st);
 }
 
 extern "C" int cvn_converse2d_op_f32(const float* x, const float* x0, int64_t B, int64_t C,
@@ -1594,46 +1725,18 @@ extern "C" int cvn_converse2d_op_f32(const float* x, const float* x0, int64_t B,
                                      void* workspace, size_t workspace_bytes,
                                      cvn_stream_t stream) {
   Geo g;
-  int rc = module_geo(B, C, h, w, 1, kh, kw, scale, 0, &g);
+  OpLayout L;
+  int rc = op_layout(B, C, h, w, kh, kw, scale, &g, &L);
   if (rc != CVN_OK) return rc;
   if (!x || !x0 || !psf || !bias || !out) return fail(CVN_ERR_ARG, "null pointer");
   if (B == 0) return CVN_OK;
-  const size_t need = cvn_converse2d_op_workspace(B, C, h, w, kh, kw, scale);
-  if (!workspace || workspace_bytes < need)
-    return fail(CVN_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
-  if (g.P > 65535) return fail(CVN_ERR_UNSUPPORTED, "B*C exceeds 65535");
-  set_lds_attrs();
-  hipStream_t st = (hipStream_t)stream;
+  if (!workspace || workspace_bytes < L.table + L.scratch)
+    return fail(CVN_ERR_WORKSPACE, "workspace too small: need %zu bytes", L.table + L.scratch);
   char* base = (char*)workspace;
-  PlanTabs t;
-  if (!plan_tabs(g, &t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
-  const char* tabs = base;
-  if ((rc = launch_plan_tabs(t, base, st)) != CVN_OK) return rc;
-  size_t o = t.bytes;
-  float2* kf = (float2*)(base + o); o += align_up((size_t)g.C * g.Ws * g.Hs * sizeof(float2));
-  float2* Am = (float2*)(base + o); o += align_up((size_t)g.C * g.Ws * g.Hs * sizeof(float2));
-  float2* S = (float2*)(base + o); o += align_up((size_t)g.P * g.NC * g.h * sizeof(float2));
-  float2* S0 = (float2*)(base + o); o += align_up((size_t)g.P * g.NCs * g.Hs * sizeof(float2));
-  float2* SH = (float2*)(base + o);
-  if ((rc = launch_phi(psf, bias, eps, g, true, Am, kf, st)) != CVN_OK) return rc;
-  if ((rc = launch_rows_fwd(x, g.P, g.h, g.w, 0, CVN_PAD_ZEROS, g.h, g.w, tabs + t.off[kTabW], S, st)) != CVN_OK)
+  if ((rc = cvn_converse2d_op_table_f32(psf, kh, kw, bias, eps, C, h, w, scale, base, L.table, stream)) != CVN_OK)
     return rc;
-  if ((rc = launch_rows_fwd(x0, g.P, g.Hs, g.Ws, 0, CVN_PAD_ZEROS, g.Hs, g.Ws, tabs + t.off[kTabWs], S0, st)) !=
-      CVN_OK)
-    return rc;
-  ColOpArgs ca;
-  ca.S = S; ca.S0 = S0; ca.kf = kf; ca.A = Am; ca.SH = SH; ca.C = g.C;
-  ca.h = g.h; ca.w = g.w; ca.s = g.s; ca.Hs = g.Hs; ca.Ws = g.Ws; ca.NC = g.NC; ca.NCs = g.NCs;
-  if (!make_plan(g.h, &ca.plan_h) || !make_plan(g.Hs, &ca.plan_H))
-    return fail(CVN_ERR_UNSUPPORTED, "no plan for column length");
-  ca.tabs_h = tabs + t.off[kTabH];
-  ca.tabs_H = tabs + t.off[kTabHs];
-  ca.rad_off = (int)align_up((size_t)(3 * g.h + g.Hs + 2 * g.s * g.Hs) * sizeof(float2), 16);
-  const size_t lds = ca.rad_off + rader_lds_bytes(ca.plan_h) + rader_lds_bytes(ca.plan_H);
-  if (lds > kLdsLimit) return fail(CVN_ERR_UNSUPPORTED, "column class does not fit in LDS");
-  hipLaunchKernelGGL(k_cols_op, dim3(g.w, (unsigned)g.P), dim3(kThreads), lds, st, ca);
-  if ((rc = check_launch("op column pass")) != CVN_OK) return rc;
-  return launch_rows_inv(SH, g, 0, g.Hs, 0, g.Ws, CVN_ACT_NONE, tabs + t.off[kTabWs], out, st);
+  return cvn_converse2d_op_apply_f32(x, x0, B, C, h, w, scale, base, L.table, base + L.table,
+                                     workspace_bytes - L.table, out, stream);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1664,15 +1767,13 @@ extern "C" int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int
   if (!grad_out || !psf || !bias || (wg && !x)) return fail(CVN_ERR_ARG, "null pointer");
   if (!grad_x && !wg) return CVN_OK;
   if (B == 0) return CVN_OK;
-  if (g.P > 65535) return fail(CVN_ERR_UNSUPPORTED, "B*C = %lld planes exceeds 65535", (long long)g.P);
-  if (wg && g.s > 4) return fail(CVN_ERR_UNSUPPORTED, "weight gradients support scale <= 4");
   PlanTabs t;
-  if (!plan_tabs(g, &t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
   BwdWs ws;
-  bwd_layout(g, t, &ws);
+  int cpb;
+  size_t col_lds;
+  if ((rc = bwd_check(g, wg, &t, &ws, &cpb, &col_lds)) != CVN_OK) return rc;
   if (!workspace || workspace_bytes < ws.total)
     return fail(CVN_ERR_WORKSPACE, "workspace too small: need %zu bytes", ws.total);
-  if (wg && ws.lds > kGradLds) return fail(CVN_ERR_UNSUPPORTED, "plane too large for the weight gradient");
   hipStream_t st = (hipStream_t)stream;
   set_lds_attrs();
   char* base = (char*)workspace;
@@ -1697,13 +1798,9 @@ extern "C" int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int
     a.h = g.h; a.w = g.w; a.s = g.s; a.Hs = g.Hs; a.Ws = g.Ws; a.NC = g.NC; a.NCs = g.NCs;
     a.plan_h = t.plan[kTabH]; a.plan_H = t.plan[kTabHs];
     a.tabs_h = tabs + t.off[kTabH]; a.tabs_H = tabs + t.off[kTabHs];
-    // classes per block: up to 8, LDS within 80 KiB where possible (2 blocks per CU)
-    const size_t rad = rader_lds_bytes(a.plan_h) + rader_lds_bytes(a.plan_H);
-    a.cpb = std::max(1, std::min(8, g.NC));
-    while (a.cpb > 1 && align_up(cols_bwd_lds(g.h, g.Hs, g.s, a.cpb, wg), 16) + rad > 80 * 1024) --a.cpb;
+    a.cpb = cpb;
     a.rad_off = (int)align_up(cols_bwd_lds(g.h, g.Hs, g.s, a.cpb, wg), 16);
-    const size_t lds = a.rad_off + rad;
-    if (lds > kLdsLimit) return fail(CVN_ERR_UNSUPPORTED, "plane too large for the backward column pass");
+    const size_t lds = col_lds;
     const dim3 grid((unsigned)((g.NC + a.cpb - 1) / a.cpb), (unsigned)(a.psf_batch == 1 ? g.C : g.P));
     hipLaunchKernelGGL(k_cols_bwd, grid, dim3(kColsBwdThreads), lds, st, a);
     if ((rc = check_launch("backward column pass")) != CVN_OK) return rc;
@@ -1718,7 +1815,6 @@ extern "C" int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int
                               side)) != CVN_OK)
       return rc;
     if (pad_mode != CVN_PAD_ZEROS && g.pad > 0) {
-      if (g.P > 65535) return fail(CVN_ERR_UNSUPPORTED, "too many planes for the padding adjoint");
       hipLaunchKernelGGL(k_pad_rows_fold, dim3((unsigned)((g.W + 255) / 256), (unsigned)g.P), dim3(256), 0, st, side,
                          g.H, g.W, g.pad, pad_mode, grad_x);
       if ((rc = check_launch("padding adjoint")) != CVN_OK) return rc;
@@ -1735,7 +1831,6 @@ extern "C" int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int
     gr.dphi = (const float2*)(base + ws.dphi);
     gr.dK = (float2*)(base + ws.dK);
     gr.part = (double*)(base + ws.part);
-    if (g.Cp * ws.nchunk > 0x7fffffff) return fail(CVN_ERR_UNSUPPORTED, "too many gradient blocks");
     const dim3 grid((unsigned)(g.Cp * ws.nchunk));
     switch (g.s) {
       case 1: hipLaunchKernelGGL(k_phi_grad<1>, grid, dim3(kThreads), (size_t)ws.lds, st, a, gr, ws.vc, ws.nchunk); break;
@@ -1748,7 +1843,6 @@ extern "C" int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int
   double2* T = (double2*)(base + ws.T);
   if (grad_psf) {
     const dim3 grid((unsigned)((g.Hs + kGaU - 1) / kGaU), (unsigned)g.Cp);
-    if (g.Cp > 65535) return fail(CVN_ERR_UNSUPPORTED, "too many psf planes");
     hipLaunchKernelGGL(k_psf_grad_a, grid, dim3(kGaU * kGaV), ((size_t)g.Ws + kGaU * kGaV * kJ) * sizeof(double2), st,
                        (const float2*)(base + ws.dK), g.Hs, g.Ws, g.kw, T);
     if ((rc = check_launch("psf gradient (columns)")) != CVN_OK) return rc;
@@ -1757,4 +1851,20 @@ extern "C" int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int
                      (const double*)(base + ws.part), ws.nchunk, g.C, g.Cp / g.C, g.Hs, g.kh, g.kw, bias, grad_psf,
                      grad_bias);
   return check_launch("psf / bias gradient");
+}
+
+extern "C" int cvn_converse2d_supported(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, int kh, int kw,
+                                        int scale, int pad, int grad_x, int grad_weight) {
+  Geo g;
+  Route r;
+  int rc = module_route(B, C, H, W, psf_batch, kh, kw, scale, pad, CVN_ROUTE_AUTO, &g, &r);
+  if (rc != CVN_OK) return rc;
+  if (r.id == CVN_ROUTE_FUSED ? B * C > 0x7fffffff : g.P > 65535)
+    return fail(CVN_ERR_UNSUPPORTED, "B*C = %lld planes exceeds the forward's grid", (long long)g.P);
+  if (!grad_x && !grad_weight) return CVN_OK;
+  PlanTabs t;
+  BwdWs ws;
+  int cpb;
+  size_t col_lds;
+  return bwd_check(g, grad_weight != 0, &t, &ws, &cpb, &col_lds);
 }

@@ -43,21 +43,33 @@ def release_workspace():
 
 
 class TableCache:
-    """LRU cache of transfer tables keyed on (psf, bias) identity and version counters plus the
-    geometry, mirroring the reference's OTF cache (converse2d.cpp:52-102).  Entries hold strong
-    references to psf and bias, so a cached address cannot be reused by another tensor while the
-    entry lives, and an in-place update (optimizer step, load_state_dict) bumps the version and
-    misses.  Bounded by entry count and bytes."""
+    """LRU cache of transfer tables, the counterpart of the reference's OTF cache (converse2d.cpp:52-102).
 
-    def __init__(self, max_entries=128, max_bytes=8 << 30):
+    Key: the psf and bias tensors (data pointer and version counter), eps, the geometry, the route
+    (which fixes the table's layout) and the device.  Entries hold strong references to psf and bias,
+    so a cached address cannot be reused by another tensor while the entry lives.  An in-place update
+    (optimizer step, load_state_dict) bumps the version and misses; the entry of the older version is
+    dropped then, so updates leave no dead tables behind.  Writes through `.data` (p.data.copy_(...),
+    p.data.mul_(...)) do not bump the version counter: call torch.ops.converse2d.clear_cache() after such
+    a write, as with the reference's cache, which keys on the data pointer alone.
+
+    Callers cache only tables that can be hit again (see `cacheable`).  Bounded by the reference's
+    64 entries and by bytes."""
+
+    def __init__(self, max_entries=64, max_bytes=4 << 30):
         from collections import OrderedDict
 
         self.entries = OrderedDict()
+        self.latest = {}  # key without version counters -> full key
         self.max_entries = max_entries
         self.max_bytes = max_bytes
         self.bytes = 0
         self.hits = 0
         self.misses = 0
+
+    @staticmethod
+    def _stem(key):
+        return key[:2] + key[3:4] + key[5:]
 
     def get(self, key):
         e = self.entries.get(key)
@@ -68,19 +80,46 @@ class TableCache:
         self.hits += 1
         return e[0]
 
+    def _drop(self, key):
+        t, _ = self.entries.pop(key)
+        self.bytes -= t.numel()
+        stem = self._stem(key)
+        if self.latest.get(stem) == key:
+            del self.latest[stem]
+
     def put(self, key, table, refs):
+        old = self.latest.get(self._stem(key))
+        if old is not None and old in self.entries:
+            self._drop(old)  # the same tensors at an older version: never hit again
         self.entries[key] = (table, refs)
+        self.latest[self._stem(key)] = key
         self.bytes += table.numel()
         while self.entries and (len(self.entries) > self.max_entries or self.bytes > self.max_bytes):
-            _, (t, _) = self.entries.popitem(last=False)
-            self.bytes -= t.numel()
+            self._drop(next(iter(self.entries)))
 
     def clear(self):
         self.entries.clear()
+        self.latest.clear()
         self.bytes = 0
 
 
 table_cache = TableCache()
+
+
+def cacheable(weight, bias) -> bool:
+    """Whether a table for (weight, bias) can be hit by a later call: not for inference tensors (no
+    version counter; in inference mode they are fresh activations), and not while autograd tracks the
+    parameters (an optimizer step changes them before the next call; the reference bypasses its cache
+    then, converse2d.cpp:60,68,88)."""
+    for t in (weight, bias):
+        if t.is_inference() or (torch.is_grad_enabled() and t.requires_grad):
+            return False
+    return True
+
+
+def _cache_key(kind, weight, bias, eps, geo, route, dev):
+    return (kind, weight.data_ptr(), weight._version, bias.data_ptr(), bias._version, float(eps), geo, route,
+            dev.index)
 
 
 def converse2d_fused(x, weight, bias, scale=1, padding=2, padding_mode="circular", eps=1e-5, act=None,
@@ -89,7 +128,8 @@ def converse2d_fused(x, weight, bias, scale=1, padding=2, padding_mode="circular
 
     x (B,C,H,W); weight (1,C,kh,kw) or (B,C,kh,kw) (per-sample psf, as ConvReverseDataNet);
     bias (1,C,1,1) or (C,).  act='gelu' applies exact GELU to the output on store.  cache=True keeps
-    the transfer table for reuse while weight and bias are unchanged (version-checked)."""
+    the transfer table of a shared psf (psf batch 1) for reuse while weight and bias are unchanged
+    (version-checked); per-sample psfs are activations that change every call and are not cached."""
     lib = _lib.load()
     _need_hip(x, weight, bias)
     if x.dim() != 4:
@@ -114,32 +154,45 @@ def converse2d_fused(x, weight, bias, scale=1, padding=2, padding_mode="circular
     if B == 0:
         return out
     p = int(padding)
-    geo = (B if pb > 1 else 0, C, H, W, pb, kh, kw, s, p)
-    tb = lib.cvn_converse2d_table_bytes(B, C, H, W, pb, kh, kw, s, p)
-    sb = lib.cvn_converse2d_scratch_bytes(B, C, H, W, pb, kh, kw, s, p)
-    if tb == 0:
-        _lib.check(_lib.CVN_ERR_ARG, "converse2d_fused")
+    route = lib.cvn_converse2d_route(B, C, H, W, pb, kh, kw, s, p)
+    if route < 0:
+        _lib.check(route, "converse2d_fused")
+    tb = lib.cvn_converse2d_table_bytes(B, C, H, W, pb, kh, kw, s, p, route)
+    sb = lib.cvn_converse2d_scratch_bytes(B, C, H, W, pb, kh, kw, s, p, route)
     st = _stream(dev)
     key = None
     table = None
-    if cache:
-        key = (weight.data_ptr(), weight._version, bias.data_ptr(), bias._version, float(eps), geo, dev.index)
+    if cache and pb == 1 and cacheable(weight, bias):
+        key = _cache_key("module", weight, bias, eps, (C, H, W, kh, kw, s, p), route, dev)
         table = table_cache.get(key)
     if table is None:
         wc = weight.contiguous()
         bc = bias.contiguous()
         table = torch.empty(tb, dtype=torch.uint8, device=dev)
         _lib.check(lib.cvn_converse2d_table_f32(wc.data_ptr(), pb, kh, kw, bc.data_ptr(), float(eps), B, C, H, W,
-                                                s, p, table.data_ptr(), tb, st), "converse2d transfer table")
-        if cache:
+                                                s, p, route, table.data_ptr(), tb, st), "converse2d transfer table")
+        if key is not None:
             table_cache.put(key, table, (weight, bias))
     scratch = _workspace(dev, sb) if sb > 0 else None
     rc = lib.cvn_converse2d_apply_f32(
         x.data_ptr(), B, C, H, W, pb, kh, kw, s, p, _lib.PAD_MODES[padding_mode],
-        _lib.ACT_GELU if act == "gelu" else _lib.ACT_NONE, table.data_ptr(),
+        _lib.ACT_GELU if act == "gelu" else _lib.ACT_NONE, route, table.data_ptr(), tb,
         scratch.data_ptr() if scratch is not None else None, sb, out.data_ptr(), st)
     _lib.check(rc, "converse2d_fused")
     return out
+
+
+def supported(x, weight, scale, padding, grad_x=False, grad_weight=False, shape=None) -> bool:
+    """Whether the library's forward (and the requested backward) serves this geometry
+    (cvn_converse2d_supported); shapes it does not serve go to the PyTorch composition.  shape
+    (B, C, H, W) stands in for x's shape when given."""
+    lib = _lib.load()
+    if weight.dim() != 4 or (shape is None and x.dim() != 4):
+        return False
+    B, C, H, W = shape if shape is not None else x.shape
+    return lib.cvn_converse2d_supported(B, C, H, W, int(weight.shape[0]), int(weight.shape[2]),
+                                        int(weight.shape[3]), int(scale), int(padding), int(bool(grad_x)),
+                                        int(bool(grad_weight))) == _lib.CVN_OK
 
 
 def converse2d_backward(grad_out, x, weight, bias, scale=1, padding=2, padding_mode="circular", eps=1e-5,
@@ -192,7 +245,8 @@ class Converse2DFunction(torch.autograd.Function):
     def forward(ctx, x, weight, bias, scale, padding, padding_mode, eps):
         ctx.save_for_backward(x, weight, bias)
         ctx.cfg = (scale, padding, padding_mode, eps)
-        return converse2d_fused(x, weight, bias.reshape(-1), scale, padding, padding_mode, eps, cache=True)
+        # the parameters change between training steps, so their tables are not cached
+        return converse2d_fused(x, weight, bias.reshape(-1), scale, padding, padding_mode, eps, cache=False)
 
     @staticmethod
     def backward(ctx, grad_out):
@@ -208,9 +262,10 @@ def converse2d_train(x, weight, bias, scale=1, padding=2, padding_mode="circular
     return Converse2DFunction.apply(x, weight, bias, scale, padding, padding_mode, eps)
 
 
-def converse2d_op(x, x0, weight, bias, scale, eps=1e-5):
+def converse2d_op(x, x0, weight, bias, scale, eps=1e-5, cache=True):
     """The reference op (converse2d.cpp:165-209): x padded (B,C,h,w), x0 (B,C,h*s,w*s) arbitrary;
-    returns the uncropped (B,C,h*s,w*s) solution."""
+    returns the uncropped (B,C,h*s,w*s) solution.  The op table (OTF and alias-class terms) is cached
+    per (psf, bias, eps, geometry) like the reference's OTF (p2o_cached, converse2d.cpp:58-102)."""
     lib = _lib.load()
     composite.check_op_args(x, x0, weight, bias, scale)
     s = int(scale)
@@ -218,20 +273,53 @@ def converse2d_op(x, x0, weight, bias, scale, eps=1e-5):
     B, C, h, w = x.shape
     if tuple(x0.shape) != (B, C, h * s, w * s) or weight.shape[1] != C or bias.shape[1] != C:
         raise RuntimeError("shape mismatch between x, x0, weight and bias")
-    x, x0, weight, bias = x.contiguous(), x0.contiguous(), weight.contiguous(), bias.contiguous()
+    x, x0 = x.contiguous(), x0.contiguous()
     dev = x.device
     out = torch.empty((B, C, h * s, w * s), dtype=torch.float32, device=dev)
     if B == 0:
         return out
     kh, kw = int(weight.shape[2]), int(weight.shape[3])
-    nbytes = lib.cvn_converse2d_op_workspace(B, C, h, w, kh, kw, s)
-    if nbytes == 0:
-        _lib.check(_lib.CVN_ERR_ARG, "converse2d_op")
-    ws = _workspace(dev, nbytes)
-    rc = lib.cvn_converse2d_op_f32(x.data_ptr(), x0.data_ptr(), B, C, h, w, weight.data_ptr(), kh, kw,
-                                   bias.data_ptr(), float(eps), s, out.data_ptr(), ws.data_ptr(), ws.numel(),
-                                   _stream(dev))
+    tb = lib.cvn_converse2d_op_table_bytes(C, h, w, kh, kw, s)
+    sb = lib.cvn_converse2d_op_scratch_bytes(B, C, h, w, s)
+    if tb == 0 or sb == 0:
+        _lib.check(lib.cvn_converse2d_op_f32(None, None, B, C, h, w, None, kh, kw, None, float(eps), s, None, None,
+                                             0, None), "converse2d_op")
+    st = _stream(dev)
+    key = None
+    table = None
+    if cache and cacheable(weight, bias):
+        key = _cache_key("op", weight, bias, eps, (C, h, w, kh, kw, s), 0, dev)
+        table = table_cache.get(key)
+    if table is None:
+        wc, bc = weight.contiguous(), bias.contiguous()
+        table = torch.empty(tb, dtype=torch.uint8, device=dev)
+        _lib.check(lib.cvn_converse2d_op_table_f32(wc.data_ptr(), kh, kw, bc.data_ptr(), float(eps), C, h, w, s,
+                                                   table.data_ptr(), tb, st), "converse2d op table")
+        if key is not None:
+            table_cache.put(key, table, (weight, bias))
+    ws = _workspace(dev, sb)
+    rc = lib.cvn_converse2d_op_apply_f32(x.data_ptr(), x0.data_ptr(), B, C, h, w, s, table.data_ptr(), tb,
+                                         ws.data_ptr(), sb, out.data_ptr(), st)
     _lib.check(rc, "converse2d_op")
+    return out
+
+
+def converse2d_fwd_oneshot(x, weight, bias, scale=1, padding=2, padding_mode="circular", eps=1e-5, act=None):
+    """cvn_converse2d_fwd_f32: the whole module-level forward (table and apply) in one library call, on
+    the route the library picks, with one caller workspace."""
+    lib = _lib.load()
+    _need_hip(x, weight, bias)
+    B, C, H, W = x.shape
+    s, p = int(scale), int(padding)
+    kh, kw, pb = int(weight.shape[2]), int(weight.shape[3]), int(weight.shape[0])
+    x, wc, bc = x.contiguous(), weight.contiguous(), bias.contiguous()
+    out = torch.empty((B, C, H * s, W * s), dtype=torch.float32, device=x.device)
+    nb = lib.cvn_converse2d_fwd_workspace(B, C, H, W, pb, kh, kw, s, p)
+    ws = _workspace(x.device, max(nb, 1))
+    rc = lib.cvn_converse2d_fwd_f32(x.data_ptr(), B, C, H, W, wc.data_ptr(), pb, kh, kw, bc.data_ptr(), float(eps), s,
+                                    p, _lib.PAD_MODES[padding_mode], _lib.ACT_GELU if act == "gelu" else _lib.ACT_NONE,
+                                    out.data_ptr(), ws.data_ptr(), nb, _stream(x.device))
+    _lib.check(rc, "converse2d_fwd")
     return out
 
 

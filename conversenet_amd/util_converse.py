@@ -54,20 +54,24 @@ def _hip_eligible(*ts) -> bool:
     return True
 
 
+def _converse_hip(x, weight, bias, scale, padding) -> bool:
+    """True when the library's forward serves this Converse2D call: fp32 HIP tensors, no pending
+    gradient, and a geometry inside the library's limits (cvn_converse2d_supported; e.g. padded planes
+    up to 4096 samples a side).  Other geometries run the PyTorch composition, which has no limits."""
+    return _hip_eligible(x, weight, bias) and functional.supported(x, weight, scale, padding)
+
+
 def _hip_grad_eligible(x, weight, bias, scale, padding, padding_mode) -> bool:
     """True when a forward that autograd must differentiate can run on the library's forward and
-    backward kernels (fp32 HIP tensors, a configuration the backward supports)."""
+    backward kernels (fp32 HIP tensors, and a geometry the forward and the requested backward support,
+    per cvn_converse2d_supported); otherwise the composition runs under autograd."""
     ts = (x, weight, bias)
     if not all(t.is_cuda and t.dtype == torch.float32 for t in ts):
         return False
     if not (torch.is_grad_enabled() and any(t.requires_grad for t in ts)):
         return False
-    if (weight.requires_grad or bias.requires_grad) and int(scale) > 4:
-        return False
-    if x.dim() != 4 or x.shape[0] * x.shape[1] > 65535:
-        return False
     _lib.load()
-    return True
+    return functional.supported(x, weight, scale, padding, x.requires_grad, weight.requires_grad or bias.requires_grad)
 
 
 """
@@ -159,10 +163,9 @@ class Converse2D(nn.Module):
         if backend == "cuda":
             if not (_HAS_CONVERSE2D_EXT and x.is_cuda):
                 raise RuntimeError("Converse2D backend='cuda' but CUDA extension is unavailable.")
-            return _hip_eligible(x, self.weight, self.bias)
-        if backend == "pytorch":
+        elif backend == "pytorch":
             return False
-        return _hip_eligible(x, self.weight, self.bias)
+        return _converse_hip(x, self.weight, self.bias, self.scale, self.padding)
 
     @property
     def biaseps(self):
@@ -264,11 +267,18 @@ def _block_tail(parts, t, x, next_parts=None):
     return y, None
 
 
+def _parts_supported(parts, x):
+    """The block's Converse2D input is (B, 2C, H, W): inside the library's limits?"""
+    cv = parts[2]
+    return functional.supported(None, cv.weight, cv.scale, cv.padding,
+                                shape=(x.shape[0], cv.in_channels, x.shape[2], x.shape[3]))
+
+
 def _fused_block_forward(blk, x, alpha1=None, alpha2=None):
     """LN+1x1+GELU -> Converse2D+GELU -> 1x1+residual and the LN-MLP branch + residual.
-    Returns None when a shape is outside the instantiated HIP tiles."""
+    Returns None when a shape is outside the instantiated HIP tiles or the library's limits."""
     parts = _block_parts(blk)
-    if parts is None or (x.shape[2] * x.shape[3]) % 4 != 0:
+    if parts is None or (x.shape[2] * x.shape[3]) % 4 != 0 or not _parts_supported(parts, x):
         return None
     return _block_tail(parts, _block_converse(parts, _block_head(parts, x)), x)[0]
 
@@ -282,7 +292,8 @@ def run_blocks(blocks, x):
     if not blocks:
         return x
     parts = [_block_parts(b) if _hip_eligible(x, *_block_params(b)) else None for b in blocks]
-    if any(p is None for p in parts) or (x.shape[2] * x.shape[3]) % 4 != 0:
+    if (any(p is None for p in parts) or (x.shape[2] * x.shape[3]) % 4 != 0
+            or not all(_parts_supported(p, x) for p in parts)):
         for b in blocks:
             x = b(x)
         return x

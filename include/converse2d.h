@@ -11,7 +11,8 @@
  *
  * Reference interfaces replaced (paths relative to the ConverseNet repository root):
  *   cvn_converse2d_op_f32   <- converse2d_forward (Converse2D/torch_converse2d/converse2d.cpp:165-209),
- *                              registered as converse2d::forward (converse2d.cpp:218-227)
+ *                              registered as converse2d::forward (converse2d.cpp:218-227); its table /
+ *                              apply split mirrors the op's OTF cache (p2o_cached, converse2d.cpp:52-102)
  *   cvn_converse2d_fwd_f32  <- Converse2D.forward (models/util_converse.py:142-192): padding
  *                              (:144-145), x0 = nearest (:172-173), the solve (:175-187) and the crop
  *                              (:189-190) in one call; also ConvReverseDataNet.forward
@@ -63,26 +64,47 @@ int cvn_converse2d_fwd_f32(const float* x, int64_t B, int64_t C, int64_t H, int6
                            float eps, int scale, int pad, int pad_mode, int act, float* out,
                            void* workspace, size_t workspace_bytes, cvn_stream_t stream);
 
+/* Which kernels serve a module-level call, and so which layout its transfer table has:
+ * CVN_ROUTE_FUSED    one kernel per call, a plane per workgroup (132 x 132, 260 x 260 padded planes, s = 1)
+ * CVN_ROUTE_PFA268   the three-pass 268 x 268 path (Converse-DnCNN's k7 p6 layers on 256 x 256 inputs)
+ * CVN_ROUTE_GENERIC  the three-pass path for any plane up to 4096 x 4096, any scale, any psf size
+ * CVN_ROUTE_AUTO     (argument only) the route cvn_converse2d_route() picks. */
+enum { CVN_ROUTE_AUTO = 0, CVN_ROUTE_FUSED = 1, CVN_ROUTE_PFA268 = 2, CVN_ROUTE_GENERIC = 3 };
+
+/* The route the library picks for a geometry (> 0), or a negative CVN_ERR_* code.  CVN_DISABLE_FUSED=1
+ * in the environment makes it CVN_ROUTE_GENERIC; nothing else reads the environment when an explicit
+ * route is passed below. */
+int cvn_converse2d_route(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, int kh, int kw, int scale,
+                         int pad);
+
+/* CVN_OK when the module-level forward (and, if asked, the backward for grad_x and / or the weight and
+ * bias gradients) supports this geometry; otherwise CVN_ERR_UNSUPPORTED or CVN_ERR_ARG with the reason in
+ * cvn_last_error().  Launches nothing.  The reference's PyTorch path has no such limits, so callers route
+ * unsupported shapes to it (as util_converse.py:150-169 chooses between its backends). */
+int cvn_converse2d_supported(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, int kh, int kw,
+                             int scale, int pad, int grad_x, int grad_weight);
+
 /* The same forward in two steps, so that the transfer table (the psf's optical transfer function
- * combined with lambda into the closed-form solve, in the kernels' layout) can be cached across calls
+ * combined with lambda into the closed-form solve, in the route's layout) can be cached across calls
  * while weight and bias are unchanged, as the reference caches its OTF (converse2d.cpp:52-102).
- * cvn_converse2d_table_f32 writes the table; cvn_converse2d_apply_f32 runs the solve with it.  The
- * table depends on (psf, psf_batch, bias, eps, C, H, W, scale, pad) and, for psf_batch = B, on B.
- * Its layout follows the kernels chosen for the geometry (fused single-kernel path, 268 path or
- * generic passes; CVN_DISABLE_FUSED=1 in the environment selects the generic passes), so a table is
- * applied under the same environment it was written in.
- * cvn_converse2d_fwd_f32 == table into workspace[0, align256(table_bytes)) + apply with the rest. */
+ * cvn_converse2d_table_f32 writes the table for a route; cvn_converse2d_apply_f32 runs that route with
+ * it.  The caller keeps the route and the table's size with the table: the apply runs the route it is
+ * given (CVN_ERR_ARG if that route does not serve the geometry, or if table_bytes is smaller than the
+ * route's table), so a table is never read in a layout it was not written in.  The table depends on
+ * (psf, psf_batch, bias, eps, C, H, W, scale, pad, route) and, for psf_batch = B, on B.
+ * cvn_converse2d_fwd_f32 == table into workspace[0, align256(table_bytes)) + apply with the rest, on
+ * the route cvn_converse2d_route() picks. */
 size_t cvn_converse2d_table_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch,
-                                  int kh, int kw, int scale, int pad);
+                                  int kh, int kw, int scale, int pad, int route);
 size_t cvn_converse2d_scratch_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch,
-                                    int kh, int kw, int scale, int pad);
+                                    int kh, int kw, int scale, int pad, int route);
 int cvn_converse2d_table_f32(const float* psf, int64_t psf_batch, int kh, int kw, const float* bias,
                              float eps, int64_t B, int64_t C, int64_t H, int64_t W, int scale, int pad,
-                             void* table, size_t table_bytes, cvn_stream_t stream);
+                             int route, void* table, size_t table_bytes, cvn_stream_t stream);
 int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
                              int64_t psf_batch, int kh, int kw, int scale, int pad, int pad_mode,
-                             int act, const void* table, void* scratch, size_t scratch_bytes,
-                             float* out, cvn_stream_t stream);
+                             int act, int route, const void* table, size_t table_bytes, void* scratch,
+                             size_t scratch_bytes, float* out, cvn_stream_t stream);
 
 /* Backward of the module-level forward (act = none), the gradients the reference obtains by autograd
  * through Converse2D.forward (util_converse.py:142-192; its op is registered
@@ -100,16 +122,29 @@ int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int64_t B, int
 
 /* Op-level forward with the reference op's semantics: x (B,C,h,w) is the already padded input,
  * x0 (B,C,h*scale,w*scale) is arbitrary, psf (1,C,kh,kw), bias (C).  out: (B,C,h*scale,w*scale),
- * uncropped. */
+ * uncropped.  cvn_converse2d_op_f32 == cvn_converse2d_op_table_f32 into workspace[0, op_table_bytes)
+ * + cvn_converse2d_op_apply_f32 with the rest.  The op table (FFT plan tables, the OTF and the alias-class
+ * terms of the solve) depends on (psf, bias, eps, C, h, w, scale) only, not on B, x or x0: it is what the
+ * reference's OTF cache keeps (p2o_cached, converse2d.cpp:58-102), and callers may cache it the same way. */
 size_t cvn_converse2d_op_workspace(int64_t B, int64_t C, int64_t h, int64_t w, int kh, int kw,
                                    int scale);
 int cvn_converse2d_op_f32(const float* x, const float* x0, int64_t B, int64_t C, int64_t h,
                           int64_t w, const float* psf, int kh, int kw, const float* bias,
                           float eps, int scale, float* out, void* workspace,
                           size_t workspace_bytes, cvn_stream_t stream);
+size_t cvn_converse2d_op_table_bytes(int64_t C, int64_t h, int64_t w, int kh, int kw, int scale);
+size_t cvn_converse2d_op_scratch_bytes(int64_t B, int64_t C, int64_t h, int64_t w, int scale);
+int cvn_converse2d_op_table_f32(const float* psf, int kh, int kw, const float* bias, float eps, int64_t C,
+                                int64_t h, int64_t w, int scale, void* table, size_t table_bytes,
+                                cvn_stream_t stream);
+int cvn_converse2d_op_apply_f32(const float* x, const float* x0, int64_t B, int64_t C, int64_t h, int64_t w,
+                                int scale, const void* table, size_t table_bytes, void* scratch,
+                                size_t scratch_bytes, float* out, cvn_stream_t stream);
 
-/* The reference keeps an OTF cache (converse2d.cpp:52-102); this library evaluates the transfer
- * function on every call and keeps none, so clearing is a no-op kept for API parity. */
+/* The reference keeps an OTF cache inside its op (converse2d.cpp:52-102).  This library keeps no cache:
+ * transfer tables live in buffers the caller owns and may keep (the Python host caches them and
+ * converse2d::clear_cache drops that cache).  This entry point has nothing to clear and returns CVN_OK;
+ * it is kept so that a binding of the reference's clear_cache has a symbol to call. */
 int cvn_clear_cache(void);
 
 /* y = weight[c] * (x - mean_c) / sqrt(var_c + eps) + bias[c], statistics over C per pixel.

@@ -33,12 +33,48 @@ How each function is pinned (checked by tests/test_oracle.py and tests/test_orac
 from __future__ import annotations
 
 import math
+import os
+import threading
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 from scipy import fft as sfft
 from scipy import special as sspecial
 
-_WORKERS = 8
+# Host threads for the large cases (the model-size checks): independent planes, or independent rows
+# of pixels, are evaluated on a thread pool with the same per-element arithmetic as a serial call.
+_WORKERS = max(1, min(16, os.cpu_count() or 1))
+_POOL = None
+_TLS = threading.local()
+
+
+def _pool():
+    global _POOL
+    if _POOL is None:
+        _POOL = ThreadPoolExecutor(_WORKERS)
+    return _POOL
+
+
+def _parallel_ok(size):
+    return _WORKERS > 1 and size >= (1 << 20) and not getattr(_TLS, "inside", False)
+
+
+def _in_worker(fn):
+    def run(*a):
+        _TLS.inside = True
+        try:
+            return fn(*a)
+        finally:
+            _TLS.inside = False
+    return run
+
+
+def _rows_map(fn, x):
+    """fn applied to row blocks of a (B,C,H,W) array and concatenated; fn must act per pixel."""
+    if x.ndim != 4 or x.shape[2] < 2 or not _parallel_ok(x.size):
+        return fn(x)
+    parts = np.array_split(x, min(x.shape[2], 2 * _WORKERS), axis=2)
+    return np.concatenate(list(_pool().map(_in_worker(fn), parts)), axis=2)
 
 PAD_MODES = ("constant", "reflect", "replicate", "circular")
 
@@ -47,12 +83,16 @@ def _cdtype(dtype):
     return np.complex128 if np.dtype(dtype) == np.float64 else np.complex64
 
 
+def _fft_workers(workers):
+    return workers or (1 if getattr(_TLS, "inside", False) else _WORKERS)
+
+
 def fft2(a, workers=None):
-    return sfft.fftn(a, axes=(-2, -1), workers=workers or _WORKERS)
+    return sfft.fftn(a, axes=(-2, -1), workers=_fft_workers(workers))
 
 
 def ifft2(a, workers=None):
-    return sfft.ifftn(a, axes=(-2, -1), workers=workers or _WORKERS)
+    return sfft.ifftn(a, axes=(-2, -1), workers=_fft_workers(workers))
 
 
 # ------------------------------------------------------------------------------------------------
@@ -201,6 +241,15 @@ def converse2d_module(x, weight, bias, scale=1, padding=2, padding_mode="circula
                       dtype=np.float64):
     """Converse2D.forward (util_converse.py:142-192): pad, x0 = nearest(padded), op, crop."""
     s = int(scale)
+    C = x.shape[1]
+    bias = np.asarray(bias)
+    if C > 1 and bias.size == C and _parallel_ok(x.size * s * s):
+        # channels are independent planes: evaluate channel slices on the thread pool
+        b4 = bias.reshape(1, C, 1, 1)
+        slices = [slice(c[0], c[-1] + 1) for c in np.array_split(np.arange(C), min(C, 2 * _WORKERS))]
+        job = _in_worker(lambda sl: converse2d_module(x[:, sl], weight[:, sl], b4[:, sl], s, padding, padding_mode,
+                                                      eps, dtype))
+        return np.concatenate(list(_pool().map(job, slices)), axis=1)
     y = pad_nchw(x, padding, padding_mode) if padding > 0 else x
     x0 = nearest(y, s)
     out = converse2d_op(y, x0, weight, bias, s, eps, dtype)
@@ -311,16 +360,18 @@ def converse2d_module_backward(x, weight, bias, gout, scale=1, padding=2, paddin
 # ------------------------------------------------------------------------------------------------
 def layernorm_cf(x, weight, bias, eps, dtype=np.float64):
     """LayerNorm channels_first (util_converse.py:63-68): biased variance over dim 1."""
-    x = x.astype(dtype)
-    u = x.mean(axis=1, keepdims=True)
-    v = ((x - u) ** 2).mean(axis=1, keepdims=True)
-    y = (x - u) / np.sqrt(v + dtype(eps))
-    return weight.astype(dtype)[None, :, None, None] * y + bias.astype(dtype)[None, :, None, None]
+    def ln(x):
+        x = x.astype(dtype)
+        u = x.mean(axis=1, keepdims=True)
+        v = ((x - u) ** 2).mean(axis=1, keepdims=True)
+        y = (x - u) / np.sqrt(v + dtype(eps))
+        return weight.astype(dtype)[None, :, None, None] * y + bias.astype(dtype)[None, :, None, None]
+    return _rows_map(ln, x)
 
 
 def gelu(x):
     """Exact GELU 0.5 x (1 + erf(x / sqrt 2)) (nn.GELU() default, util_converse.py:280)."""
-    return 0.5 * x * (1.0 + sspecial.erf(x / math.sqrt(2.0)))
+    return _rows_map(lambda x: 0.5 * x * (1.0 + sspecial.erf(x / math.sqrt(2.0))), x)
 
 
 def conv1x1(x, weight, bias, dtype=np.float64):

@@ -66,3 +66,71 @@ def test_fwd_workspace_accounts_for_scale():
     w1 = lib.cvn_converse2d_fwd_workspace(2, 4, 16, 16, 1, 3, 3, 1, 1)
     w2 = lib.cvn_converse2d_fwd_workspace(2, 4, 16, 16, 1, 3, 3, 2, 1)
     assert w2 > 3 * w1
+
+
+def test_route_query_and_environment(monkeypatch):
+    lib = _lib.load()
+    monkeypatch.delenv("CVN_DISABLE_FUSED", raising=False)
+    assert lib.cvn_converse2d_route(16, 64, 256, 256, 1, 5, 5, 1, 2) == _lib.ROUTE_FUSED  # 260^2
+    assert lib.cvn_converse2d_route(8, 128, 256, 256, 1, 7, 7, 1, 6) == _lib.ROUTE_PFA268  # 268^2
+    assert lib.cvn_converse2d_route(8, 64, 64, 64, 1, 3, 3, 2, 1) == _lib.ROUTE_GENERIC  # s = 2
+    monkeypatch.setenv("CVN_DISABLE_FUSED", "1")
+    assert lib.cvn_converse2d_route(16, 64, 256, 256, 1, 5, 5, 1, 2) == _lib.ROUTE_GENERIC
+    assert lib.cvn_converse2d_route(8, 128, 256, 256, 1, 7, 7, 1, 6) == _lib.ROUTE_GENERIC
+    # an explicit route does not read the environment: the fused table size is still available
+    assert lib.cvn_converse2d_table_bytes(16, 64, 256, 256, 1, 5, 5, 1, 2, _lib.ROUTE_FUSED) > 0
+    assert lib.cvn_converse2d_route(1, 3, 5000, 8, 1, 3, 3, 1, 1) == _lib.CVN_ERR_UNSUPPORTED
+
+
+def test_explicit_route_must_serve_geometry_and_table_size_is_checked():
+    lib = _lib.load()
+    geo = (8, 64, 64, 64, 1, 3, 3, 2, 1)  # s = 2: only the generic route serves it
+    assert lib.cvn_converse2d_table_bytes(*geo, _lib.ROUTE_FUSED) == 0
+    assert lib.cvn_converse2d_table_bytes(*geo, _lib.ROUTE_PFA268) == 0
+    assert lib.cvn_converse2d_table_bytes(*geo, 7) == 0
+    tb = lib.cvn_converse2d_table_bytes(*geo, _lib.ROUTE_GENERIC)
+    sb = lib.cvn_converse2d_scratch_bytes(*geo, _lib.ROUTE_GENERIC)
+    assert tb > 0 and sb > 0
+    assert lib.cvn_converse2d_fwd_workspace(*geo) >= tb + sb
+    B, C, H, W, pb, kh, kw, s, p = geo
+    dummy = 256  # never dereferenced: argument checks fail first
+    rc = lib.cvn_converse2d_apply_f32(dummy, B, C, H, W, pb, kh, kw, s, p, 3, 0, _lib.ROUTE_FUSED, dummy, tb, dummy,
+                                      sb, dummy, None)
+    assert rc == _lib.CVN_ERR_ARG and b"route" in lib.cvn_last_error()
+    rc = lib.cvn_converse2d_apply_f32(dummy, B, C, H, W, pb, kh, kw, s, p, 3, 0, _lib.ROUTE_GENERIC, dummy, tb - 1,
+                                      dummy, sb, dummy, None)
+    assert rc == _lib.CVN_ERR_ARG and b"table" in lib.cvn_last_error()
+    # the fused (260^2) and 268 tables differ from the generic table of the same geometry
+    g260 = (16, 64, 256, 256, 1, 5, 5, 1, 2)
+    assert lib.cvn_converse2d_table_bytes(*g260, _lib.ROUTE_FUSED) != lib.cvn_converse2d_table_bytes(
+        *g260, _lib.ROUTE_GENERIC)
+
+
+def test_support_query_matches_library_limits():
+    lib = _lib.load()
+    ok = lambda *a: lib.cvn_converse2d_supported(*a) == _lib.CVN_OK  # noqa: E731
+    assert ok(16, 64, 256, 256, 1, 5, 5, 1, 2, 0, 0)
+    assert ok(16, 64, 256, 256, 1, 5, 5, 1, 2, 1, 1)
+    assert not ok(1, 3, 5000, 8, 1, 3, 3, 1, 1, 0, 0)          # padded side above 4096
+    assert lib.cvn_converse2d_supported(1, 3, 5000, 8, 1, 3, 3, 1, 1, 0, 0) == _lib.CVN_ERR_UNSUPPORTED
+    assert not ok(300, 300, 32, 32, 1, 3, 3, 2, 1, 0, 0)       # generic path: B*C above 65535
+    assert ok(300, 300, 128, 128, 1, 5, 5, 1, 2, 0, 0)         # fused path: no such limit
+    assert not ok(300, 300, 128, 128, 1, 5, 5, 1, 2, 1, 0)     # ... but the backward has it
+    assert not ok(1, 2, 8, 8, 1, 3, 3, 5, 1, 0, 1)             # weight gradients: scale <= 4
+    assert ok(1, 2, 8, 8, 1, 3, 3, 5, 1, 1, 0)                 # grad_x alone: any scale
+    assert not ok(1, 1, 2200, 2200, 1, 3, 3, 1, 1, 0, 1)       # weight-gradient tables above 64 KiB
+    assert ok(1, 1, 2100, 2100, 1, 3, 3, 1, 1, 1, 0)           # grad_x at a 2100 side
+    assert not ok(1, 1, 3000, 3000, 1, 3, 3, 1, 1, 1, 0)       # backward column pass above 160 KiB
+    assert not ok(2, 3, 8, 8, 3, 3, 3, 1, 1, 0, 0)             # psf batch neither 1 nor B
+
+
+def test_op_split_sizes_add_up():
+    lib = _lib.load()
+    for (B, C, h, w, k, s) in [(2, 3, 20, 18, 3, 1), (8, 64, 66, 66, 3, 2), (1, 4, 30, 26, 25, 4)]:
+        tb = lib.cvn_converse2d_op_table_bytes(C, h, w, k, k, s)
+        sb = lib.cvn_converse2d_op_scratch_bytes(B, C, h, w, s)
+        assert tb > 0 and sb > 0
+        assert lib.cvn_converse2d_op_workspace(B, C, h, w, k, k, s) == tb + sb
+        # the op table does not depend on the batch
+        assert lib.cvn_converse2d_op_table_bytes(C, h, w, k, k, s) == tb
+    assert lib.cvn_converse2d_op_table_bytes(3, 5000, 8, 3, 3, 1) == 0

@@ -1,0 +1,169 @@
+"""The drop-in boundary on the GPU: the registered op torch.ops.converse2d.forward with data (its HIP
+dispatch and cached op table), the one-shot C entry point, explicit routes and cached tables across an
+environment change, inference mode, the cache staying bounded, and geometries outside the library's
+limits running the composition instead of raising."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import converse_oracle as O
+from tests.conftest import seeded, softmax_psf
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+TOL = 1e-4
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+@pytest.mark.parametrize("s", [1, 2])
+def test_registered_op_with_data(s):
+    """torch.ops.converse2d.forward (converse2d.cpp:218-227 schema) on HIP tensors runs the library
+    (op table cached on the first call, hit on the second) and matches the reference op's arithmetic."""
+    import conversenet_amd  # noqa: F401  (registers the namespace)
+    from conversenet_amd import functional as Fh
+    rng = seeded("op", s)
+    B, C, h, w, k = 2, 5, 36, 30, 5
+    x = rng.standard_normal((B, C, h, w)).astype(np.float32)
+    x0 = rng.standard_normal((B, C, h * s, w * s)).astype(np.float32)
+    wt = softmax_psf(rng, C, k)
+    b = (0.3 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    ref = O.converse2d_op(x, x0, wt, b, s, 1e-5)
+    xt, x0t, wtt, bt = (_t(a) for a in (x, x0, wt, b))
+    hits, misses = Fh.table_cache.hits, Fh.table_cache.misses
+    with torch.no_grad():
+        got1 = torch.ops.converse2d.forward(xt, x0t, wtt, bt, s, 1e-5).cpu().numpy()
+        got2 = torch.ops.converse2d.forward(xt, x0t, wtt, bt, s, 1e-5).cpu().numpy()
+    assert Fh.table_cache.misses == misses + 1 and Fh.table_cache.hits == hits + 1
+    err = max(np.abs(got1 - ref).max(), np.abs(got2 - ref).max())
+    print(f"converse2d::forward s={s}: max-abs {err:.3e}")
+    assert err <= TOL
+    # a new psf value in place: the cached table must not be reused
+    with torch.no_grad():
+        wtt.mul_(0.5).add_(0.5 / (k * k))
+        got3 = torch.ops.converse2d.forward(xt, x0t, wtt, bt, s, 1e-5).cpu().numpy()
+    ref3 = O.converse2d_op(x, x0, 0.5 * wt + 0.5 / (k * k), b, s, 1e-5)
+    assert np.abs(got3 - ref3).max() <= TOL
+    # clear_cache drops the tables (converse2d.cpp:211-216)
+    torch.ops.converse2d.clear_cache()
+    assert Fh.table_cache.bytes == 0
+
+
+@pytest.mark.parametrize("H,k,p,s", [(256, 5, 2, 1), (256, 7, 6, 1), (40, 3, 1, 2), (30, 5, 2, 3)])
+def test_one_shot_entry_point(H, k, p, s):
+    """cvn_converse2d_fwd_f32 with data on each route: fused 260^2, 268 path, generic s = 2 / 3."""
+    from conversenet_amd import functional as Fh
+    rng = seeded("oneshot", H, k, p, s)
+    B, C = 2, 3
+    x = rng.standard_normal((B, C, H, H)).astype(np.float32)
+    wt = softmax_psf(rng, C, k)
+    b = (0.3 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    got = Fh.converse2d_fwd_oneshot(_t(x), _t(wt), _t(b).reshape(-1), s, p, "circular", 1e-5).cpu().numpy()
+    ref = O.converse2d_module(x, wt, b, s, p, "circular", 1e-5)
+    err = np.abs(got - ref).max()
+    print(f"one-shot {H}^2 k{k} p{p} s{s}: max-abs {err:.3e}")
+    assert err <= TOL
+
+
+def test_cached_table_survives_environment_change(monkeypatch):
+    """A table cached on the fused route stays correct after CVN_DISABLE_FUSED=1 selects the generic
+    route for new tables: the route is part of the cache key and travels with the table."""
+    from conversenet_amd import _lib
+    from conversenet_amd import functional as Fh
+    rng = seeded("route-env")
+    B, C, H = 2, 4, 256
+    x = _t(rng.standard_normal((B, C, H, H)).astype(np.float32))
+    wt = _t(softmax_psf(rng, C, 5))
+    b = torch.zeros(C, device=DEV)
+    monkeypatch.delenv("CVN_DISABLE_FUSED", raising=False)
+    y_fused = Fh.converse2d_fused(x, wt, b, 1, 2, "circular", 1e-5)
+    assert list(Fh.table_cache.entries)[-1][7] == _lib.ROUTE_FUSED
+    monkeypatch.setenv("CVN_DISABLE_FUSED", "1")
+    y_gen = Fh.converse2d_fused(x, wt, b, 1, 2, "circular", 1e-5)
+    assert list(Fh.table_cache.entries)[-1][7] == _lib.ROUTE_GENERIC
+    monkeypatch.delenv("CVN_DISABLE_FUSED")
+    y_again = Fh.converse2d_fused(x, wt, b, 1, 2, "circular", 1e-5)  # cached fused table, fused route
+    ref = O.converse2d_module(x.cpu().numpy(), wt.cpu().numpy(), np.zeros((1, C, 1, 1), np.float32), 1, 2,
+                              "circular", 1e-5)
+    for y in (y_fused, y_gen, y_again):
+        assert np.abs(y.cpu().numpy() - ref).max() <= TOL
+
+
+def test_inference_mode_models_and_cache_bound():
+    """Converse2D and Converse-USRNet under torch.inference_mode (the per-sample psf is then an inference
+    tensor without a version counter), and the table cache staying flat over repeated forwards."""
+    from conversenet_amd import functional as Fh
+    from conversenet_amd.converse_usrnet import ConverseUSRNet
+    from conversenet_amd.util_converse import Converse2D
+    torch.manual_seed(3)
+    m = ConverseUSRNet().to(DEV).eval()
+    with torch.no_grad():
+        for prm in (m.d.alpha, *[blk.alpha1 for blk in m.p.m_body], *[blk.alpha2 for blk in m.p.m_body]):
+            prm.normal_(0, 0.1)
+    cv = Converse2D(8, 8, 3, scale=2, padding=1).to(DEV)
+    rng = seeded("infer")
+    x = _t(rng.random((1, 3, 12, 12)).astype(np.float32))
+    k = rng.random((1, 1, 7, 7)).astype(np.float32)
+    k = _t(k / k.sum())
+    xc = torch.randn(2, 8, 10, 12, device=DEV)
+    with torch.no_grad():
+        ref_m = m(x, k, 2).cpu().numpy()
+        ref_c = cv(xc).cpu().numpy()
+    sizes = []
+    with torch.inference_mode():
+        for _ in range(3):
+            got_m = m(x, k, 2).cpu().numpy()
+            got_c = cv(xc).cpu().numpy()
+            sizes.append((len(Fh.table_cache.entries), Fh.table_cache.bytes))
+    assert np.abs(got_m - ref_m).max() <= 1e-4 * max(1.0, np.abs(ref_m).max())
+    assert np.abs(got_c - ref_c).max() <= 1e-6
+    assert sizes[0] == sizes[1] == sizes[2], sizes
+    print("cache entries / bytes over inference forwards:", sizes)
+
+
+def test_training_steps_leave_no_dead_tables():
+    """Training through Converse2D (library forward and backward) with optimizer steps: the table cache
+    does not grow, and an eval forward after the steps sees the updated weights."""
+    from conversenet_amd import functional as Fh
+    from conversenet_amd.util_converse import Converse2D
+    torch.manual_seed(4)
+    m = Converse2D(4, 4, 5, padding=2).to(DEV)
+    opt = torch.optim.SGD(m.parameters(), lr=1e-3)
+    x = torch.randn(2, 4, 24, 20, device=DEV)
+    n0, b0 = len(Fh.table_cache.entries), Fh.table_cache.bytes
+    for _ in range(4):
+        opt.zero_grad()
+        m(x).square().mean().backward()
+        opt.step()
+        with torch.no_grad():
+            m(x)
+    assert len(Fh.table_cache.entries) <= n0 + 1 and Fh.table_cache.bytes <= b0 + 4 * 4096 * 1024
+    with torch.no_grad():
+        got = m(x).cpu().numpy()
+    ref = O.converse2d_module(x.cpu().numpy(), m.weight.detach().cpu().numpy(), m.bias.detach().cpu().numpy(), 1, 2,
+                              "circular", 1e-5)
+    assert np.abs(got - ref).max() <= TOL
+
+
+def test_outside_library_limits_runs_the_composition():
+    """A padded side above 4096 and weight gradients at scale 5 are outside the library's limits: the
+    module runs the PyTorch composition (torch.fft on the GPU) instead of raising."""
+    from conversenet_amd.util_converse import Converse2D
+    torch.manual_seed(5)
+    m = Converse2D(1, 1, 3, padding=1).to(DEV)
+    x = torch.randn(1, 1, 4100, 6, device=DEV)
+    with torch.no_grad():
+        got = m(x).cpu().numpy()
+    ref = O.converse2d_module(x.cpu().numpy(), m.weight.detach().cpu().numpy(), m.bias.detach().cpu().numpy(), 1, 1,
+                              "circular", 1e-5)
+    err = np.abs(got - ref).max()
+    print(f"4100x6 plane on the composition: max-abs {err:.3e}")
+    # the composition keeps the reference's fp32 op order, whose (FR - FBC invWBR) / lambda cancellation
+    # costs up to a few 1e-3 against the exact (fp64) result
+    assert err <= 1e-2
+    up = Converse2D(2, 2, 3, scale=5, padding=1).to(DEV)
+    xs = torch.randn(1, 2, 6, 7, device=DEV)
+    up(xs).sum().backward()  # weight gradients at s = 5: composition under autograd
+    assert up.weight.grad is not None and torch.isfinite(up.weight.grad).all()
