@@ -21,6 +21,7 @@ CVN_ERR_HIP = -4
 
 PAD_MODES = {"constant": 0, "zeros": 0, "reflect": 1, "replicate": 2, "circular": 3}
 ROUTE_AUTO, ROUTE_FUSED, ROUTE_PFA268, ROUTE_GENERIC = 0, 1, 2, 3
+NOALLOC_SCRATCH_BYTES = 64 << 20  # CVN_NOALLOC_SCRATCH_BYTES
 ACT_NONE = 0
 ACT_GELU = 1
 
@@ -37,6 +38,8 @@ SIGNATURES = {
     "cvn_converse2d_fwd_workspace": (_size, [_i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int]),
     "cvn_converse2d_fwd_f32": (_int, [_ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _int, _int, _ptr, _f32, _int,
                                       _int, _int, _int, _ptr, _ptr, _size, _ptr]),
+    "cvn_converse2d_fwd_noalloc_f32": (_int, [_ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _int, _int, _ptr, _f32,
+                                              _int, _int, _int, _int, _ptr, _ptr]),
     "cvn_converse2d_route": (_int, [_i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int]),
     "cvn_converse2d_supported": (_int, [_i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _int, _int]),
     "cvn_converse2d_table_bytes": (_size, [_i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _int]),

@@ -64,6 +64,19 @@ int cvn_converse2d_fwd_f32(const float* x, int64_t B, int64_t C, int64_t H, int6
                            float eps, int scale, int pad, int pad_mode, int act, float* out,
                            void* workspace, size_t workspace_bytes, cvn_stream_t stream);
 
+/* The module-level forward above without any allocation and without a caller workspace.  No counterpart
+ * in the reference: it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Its table and scratch live in a file-scope
+ * device array of CVN_NOALLOC_SCRATCH_BYTES that each device holds until the process ends; a call whose
+ * cvn_converse2d_fwd_workspace() exceeds it returns CVN_ERR_UNSUPPORTED (cfg1-cfg3-sized calls fit; a
+ * Converse-DnCNN layer at B = 8 does not).  Calls on one device share the array: calls that overlap on
+ * one device race. */
+#define CVN_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int cvn_converse2d_fwd_noalloc_f32(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,
+                                   const float* psf, int64_t psf_batch, int kh, int kw, const float* bias,
+                                   float eps, int scale, int pad, int pad_mode, int act, float* out,
+                                   cvn_stream_t stream);
+
 /* Which kernels serve a module-level call, and so which layout its transfer table has:
  * CVN_ROUTE_FUSED    one kernel per call, a plane per workgroup (132 x 132, 260 x 260 padded planes, s = 1)
  * CVN_ROUTE_PFA268   the three-pass 268 x 268 path (Converse-DnCNN's k7 p6 layers on 256 x 256 inputs)

@@ -134,3 +134,16 @@ def test_op_split_sizes_add_up():
         # the op table does not depend on the batch
         assert lib.cvn_converse2d_op_table_bytes(C, h, w, k, k, s) == tb
     assert lib.cvn_converse2d_op_table_bytes(3, 5000, 8, 3, 3, 1) == 0
+
+
+def test_noalloc_limit_and_rejection_without_device():
+    lib = _lib.load()
+    text = open(HEADER).read()
+    m = re.search(r"#define CVN_NOALLOC_SCRATCH_BYTES \(\(size_t\)(\d+) << (\d+)\)", text)
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.NOALLOC_SCRATCH_BYTES
+    # above the array's size: rejected before any device call
+    rc = lib.cvn_converse2d_fwd_noalloc_f32(256, 8, 128, 256, 256, 256, 1, 7, 7, 256, 1e-5, 1, 6, 3, 0, 256, None)
+    assert rc == _lib.CVN_ERR_UNSUPPORTED and b"scratch" in lib.cvn_last_error()
+    # invalid geometry: the forward's own argument error
+    rc = lib.cvn_converse2d_fwd_noalloc_f32(None, 1, 2, 8, 8, None, 3, 3, 3, None, 1e-5, 1, 1, 3, 0, None, None)
+    assert rc == _lib.CVN_ERR_ARG
