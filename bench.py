@@ -42,30 +42,80 @@ def cfg3_bytes(c=CFG3):
     return 4 * B * C * H * W + 4 * B * C * H * s * W * s + 4 * C * (k * k + 1)
 
 
-def make_cfg3_inputs(torch, c=CFG3):
+def make_cfg3_inputs(torch):
     """Seeded on the CPU (generator seeds 0 and 1) so the GPU run and the CPU baseline see the same
     tensors."""
-    g0 = torch.Generator().manual_seed(0)
-    x = torch.randn(c["B"], c["C"], c["H"], c["W"], generator=g0)
-    g1 = torch.Generator().manual_seed(1)
-    w = torch.softmax(torch.randn(1, c["C"], c["k"] * c["k"], generator=g1), dim=-1)
-    w = w.reshape(1, c["C"], c["k"], c["k"])
-    b = torch.zeros(1, c["C"], 1, 1)
-    return x, w, b
+    return make_layer_inputs(torch, "cfg3")
 
 
 # ------------------------------------------------------------------------------------------------
 # CPU baseline worker (separate process: loads the reference op library, never this package)
 # ------------------------------------------------------------------------------------------------
+LAYER_CFGS = {
+    # name: (B, C, H, W, k, scale, padding, input distribution)
+    "cfg1": (1, 64, 128, 128, 5, 1, 2, "uniform"),
+    "cfg2": (8, 64, 64, 64, 3, 2, 1, "normal"),
+    "cfg3": (16, 64, 256, 256, 5, 1, 2, "normal"),
+}
+
+
+def make_layer_inputs(torch, name):
+    """Seeded on the CPU (generator seeds 0 and 1: input, then softmax psf), zero bias."""
+    B, C, H, W, k, s, p, dist = LAYER_CFGS[name]
+    g0 = torch.Generator().manual_seed(0)
+    x = torch.rand(B, C, H, W, generator=g0) if dist == "uniform" else torch.randn(B, C, H, W, generator=g0)
+    g1 = torch.Generator().manual_seed(1)
+    w = torch.softmax(torch.randn(1, C, k * k, generator=g1), dim=-1).reshape(1, C, k, k)
+    return x, w, torch.zeros(1, C, 1, 1)
+
+
+def _cpu_model_name():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def cpu_model_worker(args):
+    """cfg4 / cfg5 on the host: this package's model classes with the PyTorch backend (the reference's
+    own pure-PyTorch op sequence, restated) on CPU tensors, one image of each benchmark batch."""
+    import torch
+
+    os.environ["CONVERSE2D_BACKEND"] = "pytorch"
+    cores = min(os.cpu_count() or 1, args.cpu_threads)
+    torch.set_num_threads(cores)
+    cpu = torch.device("cpu")
+    out = {}
+    m, x = make_dncnn(torch, cpu, batch=1)
+    m2, x2, k2 = make_usrnet(torch, cpu, batch=1)
+    for name, fn, per in (("cfg4", lambda: m(x), "Converse-DnCNN 1x256x256 (one image of the cfg4 batch)"),
+                          ("cfg5", lambda: m2(x2, k2, 4), "Converse-USRNet 3x64x64 -> 256x256 x4, KernelNet(25) "
+                                                          "(one image of the cfg5 batch)")):
+        with torch.no_grad():
+            t0 = time.perf_counter()
+            fn()
+            t = time.perf_counter() - t0
+        out[name] = {"value": 1.0 / t, "unit": "images/s", "cores": torch.get_num_threads(), "kind": "port",
+                     "sample": per + ", fp32, CONVERSE2D_BACKEND=pytorch on CPU tensors, 1 timed call",
+                     "ms_per_image": t * 1e3}
+    out["cpu_model"] = _cpu_model_name()
+    print(json.dumps(out))
+
+
 def cpu_worker(args):
     import torch
     import torch.nn.functional as F
 
     cores = min(os.cpu_count() or 1, args.cpu_threads)
     torch.set_num_threads(cores)
+    name = args.cpu_case
+    B, C, H, W, k, s, p, _ = LAYER_CFGS[name]
     c = dict(CFG3)
-    x, w, b = make_cfg3_inputs(torch, c)
-    p, s = c["padding"], c["scale"]
+    x, w, b = make_layer_inputs(torch, name)
     ref_so = os.path.join(ROOT, "oracle", "_ref", "converse2d_ref.so")
     if os.path.exists(ref_so):
         torch.ops.load_library(ref_so)
@@ -87,34 +137,27 @@ def cpu_worker(args):
         def step():
             return O.converse2d_module(xn, wn, bn, s, p, c["mode"], c["eps"], np.float32)
 
+    iters = args.cpu_iters if name == "cfg3" else 4 * args.cpu_iters
     times = []
     with torch.no_grad():
         step()  # warmup
-        for _ in range(args.cpu_iters):
+        for _ in range(iters):
             t0 = time.perf_counter()
             step()
             times.append(time.perf_counter() - t0)
     mean = statistics.mean(times)
-    npix = c["B"] * c["C"] * c["H"] * s * c["W"] * s
-    cpu_model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    npix = B * C * H * s * W * s
     print(json.dumps({
         "value": npix / mean / 1e9, "unit": "Gpix*ch/s", "cores": torch.get_num_threads(), "kind": kind,
-        "sample": f"cfg3 full batch (B16 C64 256x256 k5 s1 p2 circular, fp32), F.pad + reference "
-                  f"converse2d::forward + crop, 1 warmup + {args.cpu_iters} timed calls, mean",
-        "ms_per_call": mean * 1e3, "p50_ms": statistics.median(times) * 1e3, "cpu_model": cpu_model,
+        "sample": f"{name} full batch (B{B} C{C} {H}x{W} k{k} s{s} p{p} circular, fp32), F.pad + reference "
+                  f"converse2d::forward + crop, 1 warmup + {iters} timed calls, mean",
+        "ms_per_call": mean * 1e3, "p50_ms": statistics.median(times) * 1e3, "cpu_model": _cpu_model_name(),
         "os_cpu_count": os.cpu_count()}))
 
 
-def run_cpu_baseline(args):
-    cmd = [sys.executable, os.path.abspath(__file__), "--cpu-worker", "--cpu-iters", str(args.cpu_iters),
+def run_cpu_baseline(args, case="cfg3"):
+    flag = ["--cpu-model-worker"] if case == "models" else ["--cpu-worker", "--cpu-case", case]
+    cmd = [sys.executable, os.path.abspath(__file__), *flag, "--cpu-iters", str(args.cpu_iters),
            "--cpu-threads", str(args.cpu_threads)]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
     if r.returncode != 0:
@@ -243,18 +286,77 @@ def bench_usrnet(torch, dev, iters=3):
             "images_per_s": 4 / t, "params": sum(p.numel() for p in m.parameters()), "iters": iters}
 
 
-def bench_layer(torch, Fh, dev, B, C, H, W, k, s, p, dist, iters):
-    """One Converse2D layer (module level, cached table) at a survey configuration: time and Gpix*ch/s."""
-    g0 = torch.Generator().manual_seed(0)
-    x = (torch.rand(B, C, H, W, generator=g0) if dist == "uniform" else torch.randn(B, C, H, W, generator=g0)).to(dev)
-    g1 = torch.Generator().manual_seed(1)
-    w = torch.softmax(torch.randn(1, C, k * k, generator=g1), dim=-1).reshape(1, C, k, k).to(dev)
-    b = torch.zeros(C, device=dev)
+def time_events_flushed(torch, fn, iters, flush):
+    """Median duration of single calls, each preceded by a pass over a buffer larger than the 256 MB
+    MALL (Infinity Cache), so every call starts with its inputs and tables out of the caches."""
+    st = torch.cuda.current_stream()
+    fn()
+    st.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    for e0, e1 in ev:
+        flush()
+        e0.record(st)
+        fn()
+        e1.record(st)
+    st.synchronize()
+    return statistics.median(e0.elapsed_time(e1) for e0, e1 in ev) * 1e-3
+
+
+def bench_layer(torch, Fh, dev, name, iters, flush):
+    """One Converse2D layer (module level, cached table) at a survey configuration: time and Gpix*ch/s,
+    back to back (MALL-warm: cfg1's 8.4 MB and cfg2's 42 MB stay in the 256 MB MALL between calls) and
+    with the MALL flushed before each call."""
+    B, C, H, W, k, s, p, _ = LAYER_CFGS[name]
+    x, w, b = (t.to(dev) for t in make_layer_inputs(torch, name))
+    b = b.reshape(-1)
     fn = lambda: Fh.converse2d_fused(x, w, b, s, p, "circular", 1e-5)
     t = time_events(torch, fn, iters)
+    tf = time_events_flushed(torch, fn, max(10, iters // 2), flush)
     nbytes = 4 * B * C * H * W + 4 * B * C * H * s * W * s + 4 * C * (k * k + 1)
-    return {"workload": f"Converse2D B{B} C{C} {H}x{W} k{k} s{s} p{p} circular", "ms": t * 1e3,
-            "Gpix*ch/s": B * C * H * s * W * s / t / 1e9, "GB/s": nbytes / t / 1e9, "frac_hbm": nbytes / t / HBM_PEAK}
+    npix = B * C * H * s * W * s
+    return {"workload": f"Converse2D B{B} C{C} {H}x{W} k{k} s{s} p{p} circular", "route": _route(Fh, x, w, s, p),
+            "ms_mall_warm": t * 1e3, "Gpix*ch/s_mall_warm": npix / t / 1e9, "frac_hbm_mall_warm": nbytes / t / HBM_PEAK,
+            "ms": tf * 1e3, "Gpix*ch/s": npix / tf / 1e9, "GB/s": nbytes / tf / 1e9, "frac_hbm": nbytes / tf / HBM_PEAK,
+            "timing": "ms / Gpix*ch/s / frac_hbm: median single call after a 1 GiB read-modify-write pass "
+                      "(MALL flushed); *_mall_warm: back-to-back calls"}
+
+
+def _route(Fh, x, w, s, p):
+    from conversenet_amd import _lib
+    B, C, H, W = x.shape
+    r = _lib.load().cvn_converse2d_route(B, C, H, W, w.shape[0], w.shape[2], w.shape[3], s, p)
+    return {1: "fused", 2: "pfa268", 3: "generic"}.get(r, str(r))
+
+
+def bench_copy(torch, Fh, dev, iters):
+    """Attainable HBM bandwidth on this box: the library's copy kernel over 256 MiB (read) + 256 MiB
+    (written), far beyond the MALL."""
+    src = torch.randn(COPY_FLOATS, device=dev)
+    dst = torch.empty_like(src)
+    t = time_events(torch, lambda: Fh.copy_(dst, src), iters)
+    return {"bytes": 8 * COPY_FLOATS, "ms": t * 1e3, "GB/s": 8 * COPY_FLOATS / t / 1e9,
+            "frac_hbm": 8 * COPY_FLOATS / t / HBM_PEAK}
+
+
+def bench_speed_grid(torch, dev, iters):
+    """The reference's own timing grid (test/test_speed.py:137-146, 253-271): the op
+    torch.ops.converse2d.forward(x, x0 = nearest(x), psf, 0, s) on B8 C8 256x256 for s in {1, 2, 3} and
+    k in {3, 5, 7}, fp32, psf softmax-normalised (torch.manual_seed(0) as there), throughput
+    B * (H s) * (W s) / t in Gpix/s (channels not counted, as there).  Forward only."""
+    import torch.nn.functional as F
+    out = {}
+    B, C, H, W = 8, 8, 256, 256
+    for s in (1, 2, 3):
+        for k in (3, 5, 7):
+            torch.manual_seed(0)
+            x = torch.randn(B, C, H, W, device=dev)
+            x0 = x if s == 1 else F.interpolate(x, scale_factor=s, mode="nearest")
+            w = torch.softmax(torch.randn(1, C, k * k, device=dev), dim=-1).view(1, C, k, k).contiguous()
+            b = torch.zeros(1, C, 1, 1, device=dev)
+            with torch.no_grad():
+                t = time_events(torch, lambda: torch.ops.converse2d.forward(x, x0, w, b, s, 1e-5), iters)
+            out[f"s{s}_k{k}"] = {"fwd_ms": t * 1e3, "fwd_gpix_per_s": B * H * s * W * s / t / 1e9}
+    return out
 
 
 def bench_backward(torch, Fh, dev, x, w, bias, c, iters):
@@ -355,6 +457,28 @@ def only_kernel(torch, Fh, args, dev, x, step):
         m, xin, kin = make_usrnet(torch, dev)
         torch.set_grad_enabled(False)
         fn = lambda: m(xin, kin, 4)
+    elif args.only in ("cfg1", "cfg2"):
+        B, C, H, W, k, s, p, _ = LAYER_CFGS[args.only]
+        xl, wl, bl = (t.to(dev) for t in make_layer_inputs(torch, args.only))
+        fn = lambda: Fh.converse2d_fused(xl, wl, bl.reshape(-1), s, p, "circular", 1e-5)
+    elif args.only == "pfa268":
+        # one Converse-DnCNN layer: B8 C128 256x256 k7 p6 circular (268 x 268 planes)
+        g = torch.Generator().manual_seed(0)
+        xl = torch.randn(8, 128, 256, 256, generator=g).to(dev)
+        wl = torch.softmax(torch.randn(1, 128, 49, generator=g), -1).reshape(1, 128, 7, 7).to(dev)
+        bl = torch.zeros(128, device=dev)
+        fn = lambda: Fh.converse2d_fused(xl, wl, bl, 1, 6, "circular", 1e-5)
+    elif args.only == "tail":
+        # the block tail with the next block's head at Converse-DnCNN's shape (B8, 64 / 128 channels, 256x256)
+        g = torch.Generator(device=dev).manual_seed(3)
+        t = torch.randn(8, 128, 256, 256, device=dev, generator=g)
+        xr = torch.randn(8, 64, 256, 256, device=dev, generator=g)
+        w0 = torch.randn(64, 128, 1, 1, device=dev, generator=g) / 11
+        w1 = torch.randn(128, 64, 1, 1, device=dev, generator=g) / 8
+        b0, b1 = torch.randn(64, device=dev, generator=g), torch.randn(128, device=dev, generator=g)
+        lw, lb = torch.ones(64, device=dev), torch.zeros(64, device=dev)
+        fn = lambda: Fh.conv_ln_mlp_residual(t, xr, w0, b0, lw, lb, 1e-5, w1, b1, w0, b0,
+                                             head=(lw, lb, 1e-5, w1, b1))
     else:
         raise SystemExit(f"unknown --only {args.only}")
     for _ in range(args.warmup):
@@ -376,14 +500,20 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-model", action="store_true")
     ap.add_argument("--cpu-worker", action="store_true")
+    ap.add_argument("--cpu-case", default="cfg3", choices=sorted(LAYER_CFGS))
+    ap.add_argument("--cpu-model-worker", action="store_true")
     ap.add_argument("--cpu-iters", type=int, default=3)
     ap.add_argument("--cpu-threads", type=int, default=16)
-    ap.add_argument("--only", choices=["converse2d", "layernorm", "conv1x1", "copy", "dncnn", "usrnet", "backward"],
+    ap.add_argument("--only", choices=["converse2d", "layernorm", "conv1x1", "copy", "dncnn", "usrnet", "backward",
+                                       "cfg1", "cfg2", "pfa268", "tail"],
                     help="run one kernel family alone (for rocprofv3)")
     args = ap.parse_args()
 
     if args.cpu_worker:
         cpu_worker(args)
+        return 0
+    if args.cpu_model_worker:
+        cpu_model_worker(args)
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the Converse2D path shards over the batch with no exchange, "
@@ -446,12 +576,38 @@ def main():
     if not args.no_model:
         extra["converse_dncnn"] = bench_model(torch, dev)
         extra["converse_usrnet"] = bench_usrnet(torch, dev)
-    extra["cfg1"] = bench_layer(torch, Fh, dev, 1, 64, 128, 128, 5, 1, 2, "uniform", max(20, args.steps))
-    extra["cfg2"] = bench_layer(torch, Fh, dev, 8, 64, 64, 64, 3, 2, 1, "normal", max(20, args.steps))
+    flush_buf = torch.empty(256 * 1024 * 1024, device=dev)  # 1 GiB
+
+    def flush():
+        flush_buf.add_(1.0)
+
+    extra["cfg1"] = bench_layer(torch, Fh, dev, "cfg1", max(20, args.steps), flush)
+    extra["cfg2"] = bench_layer(torch, Fh, dev, "cfg2", max(20, args.steps), flush)
+    del flush_buf
+    extra["copy"] = bench_copy(torch, Fh, dev, max(10, args.steps // 2))
+    # the operator path (what the reference's own Converse2D calls through torch.ops.converse2d.forward):
+    # padding and x0 = nearest in torch, the library's op kernels with the cached op table
+    import torch.nn.functional as F
+    y = F.pad(x, [c["padding"]] * 4, mode=c["mode"])
+    b4 = bias.reshape(1, -1, 1, 1)
+    with torch.no_grad():
+        t_op = time_events(torch, lambda: torch.ops.converse2d.forward(y, y, w, b4, 1, c["eps"]),
+                           max(5, args.steps // 5))
+    extra["cfg3_operator_path"] = {"ms": t_op * 1e3, "Gpix*ch/s": npix * (260 * 260) / (256 * 256) / t_op / 1e9,
+                                   "note": "converse2d::forward on the padded 260x260 input (x0 = padded input), "
+                                           "uncropped output, op table cached; padding not timed"}
+    extra["reference_speed_grid"] = bench_speed_grid(torch, dev, max(10, args.steps // 5))
 
     cpu = None
     if not args.no_cpu:
         cpu = run_cpu_baseline(args)
+        for name in ("cfg1", "cfg2"):
+            extra[name]["cpu_baseline"] = run_cpu_baseline(args, name)
+        if not args.no_model:
+            models = run_cpu_baseline(args, "models")
+            for name, key in (("cfg4", "converse_dncnn"), ("cfg5", "converse_usrnet")):
+                if name in models and key in extra:
+                    extra[key]["cpu_baseline"] = models[name]
 
     line = {
         "metric": "Converse2D fwd Gpix*ch/s", "value": npix / per_call / 1e9, "unit": "Gpix*ch/s", "n_gpus": 1,

@@ -593,10 +593,295 @@ __global__ void __launch_bounds__(256) k_phi_fused(PhiFusedArgs a) {
 }
 
 // ----------------------------------------------------------------------------------------------
+// Scale s > 1 (zero-insert upsample, converse2d.cpp:104-119; nearest x0, util_converse.py:172-173):
+// the high-resolution (HR) plane N x M = (h s) x (w s) has a fused plan, the low-resolution (LR)
+// padded plane h x w is transformed in LDS.  By the tiling identities, the HR spectra of the
+// zero-inserted y and of nearest(y) are Y(u mod h, v mod w) and Y(u mod h, v mod w) Hn(u, v), so the
+// solved HR spectrum is X(u, v) = Phi(u, v) Y(u mod h, v mod w) with the module-form transfer
+// function (alias-class means M over the s x s aliases (u + a h, v + b w) of a bin)
+//   Phi = Hn + conj(K) (1 - M(K Hn)) / (M(|K|^2) + lambda),  Hn(u, v) = H_s(u; N) H_s(v; M),
+//   H_s(u; N) = sum_{a < s} exp(-2 pi i u a / N),
+// normalised by 1 / (N M).  The kernel writes X straight into the two HR groups in the fused slot
+// order (E' = X(k) + X(k + N/2) for the even HR rows, O' = conj(W^k) (X(k) - X(k + N/2)) for the
+// odd rows) and runs the fused inverse passes; nothing but the LR input and the HR output touches HBM.
+// ----------------------------------------------------------------------------------------------
+struct PhiUpArgs {
+  const float* psf;
+  const float* bias;
+  int64_t C;
+  int kh, kw, s;
+  double eps;
+  float4* tab4;
+};
+
+__device__ __forceinline__ double2 d_hold(int64_t u, int s, int L) {  // H_s(u; L)
+  double2 acc = make_double2(0.0, 0.0);
+  for (int a = 0; a < s; ++a) {
+    const double2 r = d_root(u * a, L);
+    acc.x += r.x;
+    acc.y += r.y;
+  }
+  return acc;
+}
+
+// One block per (psf plane, half-spectrum column q); threads over the column sub-frequency k < N/2,
+// writing (Phi(k, q), Phi(k + N/2, q)) at the slot of (k, q), in fp64.
+template <class P>
+__global__ void __launch_bounds__(256) k_phi_fused_up(PhiUpArgs a) {
+  __shared__ double2 Pq[4][64];  // row sums of the psf at the s column aliases of q
+  __shared__ double2 Hq[4];      // H_s at those columns
+  const int64_t cp = blockIdx.x / P::NQ;
+  const int q = (int)(blockIdx.x - cp * P::NQ);
+  const int c = (int)(cp % a.C);
+  const int s = a.s, h = P::N / s, w = P::M / s;
+  const float* psf = a.psf + cp * a.kh * a.kw;
+  for (int idx = threadIdx.x; idx < s * a.kh; idx += blockDim.x) {
+    const int b = idx / a.kh, i = idx - b * a.kh;
+    const int64_t qb = (q + (int64_t)b * w) % P::M;
+    const double2 r = d_root(qb, P::M);
+    double2 e = d_root(-qb * (a.kw / 2), P::M);
+    double2 acc = make_double2(0.0, 0.0);
+    for (int j = 0; j < a.kw; ++j) {
+      const double t = (double)psf[i * a.kw + j];
+      acc.x += t * e.x;
+      acc.y += t * e.y;
+      e = d_cmul(e, r);
+    }
+    Pq[b][i] = acc;
+  }
+  if (threadIdx.x < s) Hq[threadIdx.x] = d_hold((q + (int64_t)threadIdx.x * w) % P::M, s, P::M);
+  __syncthreads();
+  const double lmb = 1.0 / (1.0 + exp(-((double)a.bias[c] - 9.0))) + a.eps;
+  const double norm = 1.0 / ((double)P::N * (double)P::M);
+  const double inv_s2 = 1.0 / (double)(s * s);
+  for (int k = threadIdx.x; k < P::NH; k += blockDim.x) {
+    double2 ph[2];
+    for (int hh = 0; hh < 2; ++hh) {
+      const int u = k + hh * P::NH;
+      double sk2 = 0.0;
+      double2 skh = make_double2(0.0, 0.0), k00 = skh, h00 = skh;
+      for (int al = 0; al < s; ++al) {
+        const int64_t ua = (u + (int64_t)al * h) % P::N;
+        const double2 hu = d_hold(ua, s, P::N);
+        const double2 r = d_root(ua, P::N);
+        double2 e = d_root(-ua * (a.kh / 2), P::N);
+        double2 K[4];
+        for (int b = 0; b < s; ++b) K[b] = make_double2(0.0, 0.0);
+        for (int i = 0; i < a.kh; ++i) {
+          for (int b = 0; b < s; ++b) {
+            const double2 t = d_cmul(e, Pq[b][i]);
+            K[b].x += t.x;
+            K[b].y += t.y;
+          }
+          e = d_cmul(e, r);
+        }
+        for (int b = 0; b < s; ++b) {
+          const double2 hn = d_cmul(hu, Hq[b]);
+          const double2 kh_ = d_cmul(K[b], hn);
+          sk2 += K[b].x * K[b].x + K[b].y * K[b].y;
+          skh.x += kh_.x;
+          skh.y += kh_.y;
+          if (al == 0 && b == 0) {
+            k00 = K[b];
+            h00 = hn;
+          }
+        }
+      }
+      const double den = sk2 * inv_s2 + lmb;
+      const double2 g = make_double2((1.0 - skh.x * inv_s2) / den, -skh.y * inv_s2 / den);
+      const double2 cg = d_cmul(make_double2(k00.x, -k00.y), g);  // conj(K) g
+      ph[hh] = make_double2((h00.x + cg.x) * norm, (h00.y + cg.y) * norm);
+    }
+    const int rp = P::rfpos(k);
+    const int slot = (rp >> 1) * P::RS + ((rp & 1) ? P::pb(q) : P::pa(q));
+    a.tab4[cp * P::SLOTS + slot] = make_float4((float)ph[0].x, (float)ph[0].y, (float)ph[1].x, (float)ph[1].y);
+  }
+}
+
+struct FusedUpArgs {
+  FusedArgs hr;        // x = LR input (P, H, W); out = HR output (P, H s, W s); H, W, pad: the HR crop
+  int Hl, Wl, padl;    // LR input size and padding
+  int y_off, tw_off, idx_off;  // LDS offsets (bytes) of the LR spectrum, LR twiddles, kof / qof tables
+};
+
+// Stockham radices of the LR transform length L = 132 / s (fixed butterflies, first to last).
+template <int L> struct LrRadices;
+template <> struct LrRadices<66> { static constexpr int n = 3, r0 = 2, r1 = 3, r2 = 11; };
+template <> struct LrRadices<44> { static constexpr int n = 2, r0 = 4, r1 = 11, r2 = 1; };
+template <> struct LrRadices<33> { static constexpr int n = 2, r0 = 3, r1 = 11, r2 = 1; };
+
+// The LR transform of `ntr` rows of length L (a -> b -> ...), compile-time radices; returns the buffer
+// holding the result.
+template <int L>
+__device__ __forceinline__ float2* lr_fft(float2* a, float2* b, int ntr, const float2* tw, int tid) {
+  using Rd = LrRadices<L>;
+  stockham_pass<Rd::r0, false>(a, b, L, 1, ntr, tw, tid, kFT);
+  __syncthreads();
+  stockham_pass<Rd::r1, false>(b, a, L, Rd::r0, ntr, tw, tid, kFT);
+  __syncthreads();
+  if constexpr (Rd::n == 3) {
+    stockham_pass<Rd::r2, false>(a, b, L, Rd::r0 * Rd::r1, ntr, tw, tid, kFT);
+    __syncthreads();
+    return b;
+  }
+  return a;
+}
+
+// LR padded-plane index maps use the padding map of the LR input (as the reference pads before the
+// upsample, util_converse.py:144-145).
+// Two workgroups per CU (8 waves per SIMD): the even-row group is parked in registers and the LDS
+// holds one group, the slot tables and the LR spectrum.
+template <class P, int S>
+__global__ void __launch_bounds__(kFT, 8) k_converse2d_fused_up(FusedUpArgs ua) {
+  static_assert(P::N == P::M && P::N % S == 0, "square HR plane, LR side N / S");
+  constexpr int h = P::N / S, w = P::M / S, ncl = w / 2 + 1, npl = (h + 1) / 2;
+  extern __shared__ float2 smem[];
+  const FusedArgs& a = ua.hr;
+  float2* buf = smem;
+  float2* wtab = smem + P::SLOTS_PAD;
+  short* pa = (short*)(wtab + P::NH + 2);
+  short* pb = pa + P::NQ;
+  short* pos = pb + P::NQ;
+  unsigned char* isb = (unsigned char*)(pos + 2 * P::M);
+  char* base = (char*)smem;
+  float2* Y = (float2*)(base + ua.y_off);      // LR half spectrum, column-major: Y[v h + u]
+  float2* twl = (float2*)(base + ua.tw_off);   // exp(-2 pi i m / w), m < w
+  float2* twh = twl + w;                       // exp(-2 pi i m / h), m < h
+  short* kof = (short*)(base + ua.idx_off);    // column frequency k of row position rp
+  short* qof = kof + P::NH;                    // half-spectrum column q of a row-pair position
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t plane = fused_plane(blockIdx.x, a);
+  const int64_t cp = (a.psf_batch == 1) ? (plane % a.C) : plane;
+  const uint32_t in_bytes = (uint32_t)(ua.Hl * ua.Wl) * 4u, out_bytes = (uint32_t)(a.H * a.W) * 4u;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + plane * (int64_t)ua.Hl * ua.Wl, in_bytes);
+  const __amdgpu_buffer_rsrc_t orsrc = make_rsrc(a.out + plane * (int64_t)a.H * a.W, out_bytes);
+  const __amdgpu_buffer_rsrc_t t4r = make_rsrc(a.tab4 + cp * P::SLOTS, P::SLOTS * 16u);
+  // tables: radix-2 twiddles, slot positions, LR twiddles
+  for (int p = tid; p < P::RS; p += kFT) isb[p] = 0;
+  for (int k = tid; k < P::NH + 2; k += kFT) {
+    double sn = 0.0, cs = 0.0;
+    if (k < P::NH) sincospi(-2.0 * (double)k / (double)P::N, &sn, &cs);
+    wtab[k < P::NH ? P::rfpos(k) : k] = make_float2((float)cs, (float)sn);
+    if (k < P::NH) kof[P::rfpos(k)] = (short)k;
+  }
+  for (int m = tid; m < w + h; m += kFT) {
+    const int L = m < w ? w : h, mm = m < w ? m : m - w;
+    double sn, cs;
+    sincospi(-2.0 * (double)mm / (double)L, &sn, &cs);
+    twl[m] = make_float2((float)cs, (float)sn);
+  }
+  lds_barrier();
+  for (int q = tid; q < P::NQ; q += kFT) {
+    pa[q] = P::pa(q);
+    pb[q] = P::pb(q);
+    isb[P::pb(q)] = 1;
+    qof[P::pa(q)] = (short)q;
+    qof[P::pb(q)] = (short)q;
+  }
+  for (int j = tid; j < P::M; j += kFT) pos[j] = P::pos_in(j);
+  // LR padded plane as complex row pairs (row 2t in .x, 2t + 1 in .y) in buf
+  float2* A = buf;
+  float2* Bw = buf + npl * w;
+  for (int e = tid; e < npl * w; e += kFT) {
+    const int t = e / w, j = e - t * w;
+    const int sc = fpad_src(j, ua.Wl, ua.padl, a.mode);
+    const int r0 = fpad_src(2 * t, ua.Hl, ua.padl, a.mode);
+    const int r1 = 2 * t + 1 < h ? fpad_src(2 * t + 1, ua.Hl, ua.padl, a.mode) : -1;
+    float2 v = make_float2(0.f, 0.f);
+    if (sc >= 0) {
+      if (r0 >= 0) v.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, 4u * (uint32_t)(r0 * ua.Wl + sc), 0u, 0));
+      if (r1 >= 0) v.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, 4u * (uint32_t)(r1 * ua.Wl + sc), 0u, 0));
+    }
+    A[e] = v;
+  }
+  __syncthreads();
+  const float2* R = lr_fft<w>(A, Bw, npl, twl, tid);
+  // Hermitian unpack of each row pair into the two rows' half spectra, column-major into Y
+  for (int e = tid; e < npl * ncl; e += kFT) {
+    const int t = e / ncl, v = e - t * ncl;
+    const float2 zl = R[t * w + v], zh = R[t * w + (v ? w - v : 0)];
+    Y[v * h + 2 * t] = make_float2(0.5f * (zl.x + zh.x), 0.5f * (zl.y - zh.y));
+    if (2 * t + 1 < h) Y[v * h + 2 * t + 1] = make_float2(0.5f * (zl.y + zh.y), 0.5f * (zh.x - zl.x));
+  }
+  __syncthreads();
+  const float2* Yr = lr_fft<h>(Y, buf, ncl, twh, tid);
+  if (Yr != Y) {
+    for (int e = tid; e < ncl * h; e += kFT) Y[e] = Yr[e];
+    __syncthreads();
+  }
+  // solved HR spectrum straight into the two groups: G1 (odd HR rows) in buf, G0 (even) parked
+  float2 park[P::PARK];
+#pragma unroll
+  for (int i0 = 0; i0 < P::PARK; ++i0) {
+    const int sl = tid + i0 * kFT;
+    float2 e0 = make_float2(0.f, 0.f), o1 = e0;
+    if (sl < P::SLOTS) {
+      const int t = sl / P::RS, p = sl - t * P::RS;
+      const int rp = 2 * t + isb[p];
+      const int k = kof[rp], q = qof[p];
+      const float4 f = bload4(t4r, 16u * (uint32_t)sl, 0u);
+      float2 yk[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int uu = (k + hh * P::NH) % h, vv = q % w;
+        yk[hh] = vv < ncl ? Y[vv * h + uu] : cconj(Y[(w - vv) * h + (uu ? h - uu : 0)]);
+      }
+      const float2 x0 = cmul(make_float2(f.x, f.y), yk[0]), x1 = cmul(make_float2(f.z, f.w), yk[1]);
+      e0 = cadd(x0, x1);
+      o1 = cmul(cconj(wtab[rp]), csub(x0, x1));
+    }
+    park[i0] = e0;
+    buf[sl] = o1;
+  }
+  lds_barrier();
+  int lp[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) lp[c] = P::pos_in(min(a.pad + 4 * lane + c, P::M - 1));
+  group_inverse_store<P>(buf, pa, pb, lp, orsrc, a, 1, wave, lane, tid);
+  lds_barrier();
+#pragma unroll
+  for (int i = 0; i < P::PARK; ++i) buf[tid + i * kFT] = park[i];
+  lds_barrier();
+  group_inverse_store<P>(buf, pa, pb, lp, orsrc, a, 0, wave, lane, tid);
+}
+
+// ----------------------------------------------------------------------------------------------
 // host dispatch
 // ----------------------------------------------------------------------------------------------
 using Plan260 = FusedPlan<260, 4, 5, 13, 5, 13, 5>;   // rows 260 = 4 5 13, columns 130 = 5 13 2
 using Plan132 = FusedPlan<132, 4, 3, 11, 3, 11>;   // rows 132 = 4 3 11, columns 66 = 3 11 2
+
+// LDS layout of the up kernel after the fused kernel's own regions.
+struct UpLayout {
+  int y_off, tw_off, idx_off;
+  size_t bytes;
+};
+template <class P>
+UpLayout up_layout(int h, int w) {
+  UpLayout L;
+  size_t o = align_up((size_t)P::SLOTS_PAD * 8 + P::TAB_BYTES, 16);
+  L.y_off = (int)o;
+  o += (size_t)(w / 2 + 1) * h * 8;
+  L.tw_off = (int)o;
+  o += (size_t)(w + h) * 8;
+  L.idx_off = (int)o;
+  o += (size_t)(P::NH + P::RS) * 2;
+  L.bytes = align_up(o, 16);
+  return L;
+}
+
+// The up path serves HR planes of the 132 x 132 plan from LR planes h = w = 132 / s, s in 2..4,
+// whose transforms use fixed radices only; the LR pair buffers (2 (h + 1) / 2 w) and the column
+// transform's scratch fit in the group buffer and the parked rounds.
+bool fused_up_geometry(int H, int W, int pad, int s) {
+  using P = Plan132;
+  const int h = H + 2 * pad, w = W + 2 * pad;
+  if (s < 2 || s > 4 || h * s != P::N || w * s != P::M || (W * s) % 4 != 0) return false;
+  const int npl = (h + 1) / 2;
+  if ((size_t)2 * npl * w > (size_t)P::SLOTS_PAD || (size_t)(w / 2 + 1) * h > (size_t)P::SLOTS_PAD) return false;
+  return up_layout<P>(h, w).bytes <= 80 * 1024;  // two workgroups per CU
+}
 
 template <class P>
 size_t fused_ws(int64_t Cp) {
@@ -629,9 +914,15 @@ int fused_apply_run(const float* x, int64_t B, int64_t C, int H, int W, int64_t 
   return check_launch("fused converse2d");
 }
 
-// The fused kernel loads rows as float4 per lane: W must be a multiple of 4 and at most 256.
+// The fused kernel loads rows as float4 per lane: W must be a multiple of 4 and at most 256.  At
+// scale > 1 the HR plane must have a fused plan (fused_up_geometry).
 int fused_query(int H, int W, int pad, int scale, int64_t Cp, size_t* ws_bytes) {
-  if (scale != 1 || W % 4 != 0 || W > 256) return 0;
+  if (scale != 1) {
+    if (!fused_up_geometry(H, W, pad, scale)) return 0;
+    *ws_bytes = fused_ws<Plan132>(Cp);
+    return 1;
+  }
+  if (W % 4 != 0 || W > 256) return 0;
   const int h = H + 2 * pad, w = W + 2 * pad;
   if (h == 260 && w == 260) { *ws_bytes = fused_ws<Plan260>(Cp); return 1; }
   if (h == 132 && w == 132) { *ws_bytes = fused_ws<Plan132>(Cp); return 1; }
@@ -639,14 +930,48 @@ int fused_query(int H, int W, int pad, int scale, int64_t Cp, size_t* ws_bytes) 
 }
 
 int fused_table(const float* psf, const float* bias, float eps, int64_t C, int64_t psf_batch, int kh, int kw,
-                int H, int W, int pad, void* table, hipStream_t st) {
+                int H, int W, int pad, int scale, void* table, hipStream_t st) {
+  if (scale != 1) {
+    const int64_t Cp = psf_batch * C;
+    PhiUpArgs pa{psf, bias, C, kh, kw, scale, (double)eps, (float4*)table};
+    hipLaunchKernelGGL(k_phi_fused_up<Plan132>, dim3((unsigned)(Cp * Plan132::NQ)), dim3(256), 0, st, pa);
+    return check_launch("fused transfer table (scale > 1)");
+  }
   const int h = H + 2 * pad;
   if (h == 260) return fused_table_run<Plan260>(psf, bias, eps, C, psf_batch, kh, kw, table, st);
   return fused_table_run<Plan132>(psf, bias, eps, C, psf_batch, kh, kw, table, st);
 }
 
 int fused_apply(const float* x, int64_t B, int64_t C, int H, int W, int64_t psf_batch, int pad, int mode, int act,
-                const void* table, float* out, hipStream_t st) {
+                int scale, const void* table, float* out, hipStream_t st) {
+  if (scale != 1) {
+    using P = Plan132;
+    static std::atomic<uint64_t> attr{0};
+    once_per_device(attr, [] {
+      for (const void* k : {(const void*)k_converse2d_fused_up<P, 2>, (const void*)k_converse2d_fused_up<P, 3>,
+                            (const void*)k_converse2d_fused_up<P, 4>})
+        (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024);
+      (void)hipGetLastError();
+    });
+    if (!fused_up_geometry(H, W, pad, scale))
+      return fail(CVN_ERR_UNSUPPORTED, "no fused plan for this upsampling geometry");
+    FusedUpArgs ua;
+    const UpLayout L = up_layout<P>(H + 2 * pad, W + 2 * pad);
+    ua.hr = FusedArgs{x, (const float4*)table, out, B, C, psf_batch, H * scale, W * scale, pad * scale, mode, act};
+    ua.Hl = H;
+    ua.Wl = W;
+    ua.padl = pad;
+    ua.y_off = L.y_off;
+    ua.tw_off = L.tw_off;
+    ua.idx_off = L.idx_off;
+    const dim3 grid((unsigned)(B * C));
+    switch (scale) {
+      case 2: hipLaunchKernelGGL((k_converse2d_fused_up<P, 2>), grid, dim3(kFT), L.bytes, st, ua); break;
+      case 3: hipLaunchKernelGGL((k_converse2d_fused_up<P, 3>), grid, dim3(kFT), L.bytes, st, ua); break;
+      default: hipLaunchKernelGGL((k_converse2d_fused_up<P, 4>), grid, dim3(kFT), L.bytes, st, ua); break;
+    }
+    return check_launch("fused converse2d (scale > 1)");
+  }
   const int h = H + 2 * pad;
   if (h == 260) return fused_apply_run<Plan260>(x, B, C, H, W, psf_batch, pad, mode, act, table, out, st);
   return fused_apply_run<Plan132>(x, B, C, H, W, psf_batch, pad, mode, act, table, out, st);

@@ -1526,7 +1526,8 @@ extern "C" int cvn_converse2d_table_f32(const float* psf, int64_t psf_batch, int
   if (!table || table_bytes < r.table_bytes)
     return fail(CVN_ERR_WORKSPACE, "table buffer too small: need %zu bytes", r.table_bytes);
   hipStream_t st = (hipStream_t)stream;
-  if (r.id == CVN_ROUTE_FUSED) return fused_table(psf, bias, eps, g.C, g.Cp / g.C, kh, kw, g.H, g.W, g.pad, table, st);
+  if (r.id == CVN_ROUTE_FUSED)
+    return fused_table(psf, bias, eps, g.C, g.Cp / g.C, kh, kw, g.H, g.W, g.pad, g.s, table, st);
   PlanTabs t;
   if (!plan_tabs(g, &t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
   const ModWs ws = module_ws(g, t);
@@ -1553,7 +1554,7 @@ extern "C" int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, in
     if (((uintptr_t)x & 15) || ((uintptr_t)out & 15))
       return fail(CVN_ERR_ARG, "the fused kernel needs 16-byte aligned input and output");
     if (B * C > 0x7fffffff) return fail(CVN_ERR_UNSUPPORTED, "too many planes");
-    return fused_apply(x, B, C, g.H, g.W, g.Cp / g.C, pad, pad_mode, act, table, out, st);
+    return fused_apply(x, B, C, g.H, g.W, g.Cp / g.C, pad, pad_mode, act, g.s, table, out, st);
   }
   if (!scratch || scratch_bytes < r.scratch_bytes)
     return fail(CVN_ERR_WORKSPACE, "scratch too small: need %zu bytes", r.scratch_bytes);

@@ -132,12 +132,13 @@ inline bool make_plan(int L, FftPlan* plan) {
 }
 
 // Fused single-kernel path (converse2d_fused.hip): returns 1 and the workspace it needs when the
-// padded plane (H + 2 pad, W + 2 pad) at this scale has an instantiated plan.
+// padded plane (H + 2 pad, W + 2 pad) at this scale has an instantiated plan (at scale > 1: when the
+// upsampled plane has one).
 int fused_query(int H, int W, int pad, int scale, int64_t Cp, size_t* ws_bytes);
 int fused_table(const float* psf, const float* bias, float eps, int64_t C, int64_t psf_batch, int kh, int kw,
-                int H, int W, int pad, void* table, hipStream_t st);
+                int H, int W, int pad, int scale, void* table, hipStream_t st);
 int fused_apply(const float* x, int64_t B, int64_t C, int H, int W, int64_t psf_batch, int pad, int mode, int act,
-                const void* table, float* out, hipStream_t st);
+                int scale, const void* table, float* out, hipStream_t st);
 // 268 x 268 planes at scale 1 (converse2d_pfa.hip): in-place prime-factor FFTs 268 = 4 * 67 with an
 // in-register Rader 67-point DFT.
 bool pfa268_applies(int h, int w, int s);

@@ -273,6 +273,12 @@ def converse2d_op(x, x0, weight, bias, scale, eps=1e-5, cache=True):
     B, C, h, w = x.shape
     if tuple(x0.shape) != (B, C, h * s, w * s) or weight.shape[1] != C or bias.shape[1] != C:
         raise RuntimeError("shape mismatch between x, x0, weight and bias")
+    if (s == 1 and x0.data_ptr() == x.data_ptr() and x0.stride() == x.stride() and B > 0
+            and supported(x, weight, 1, 0)):
+        # x0 is x, as the reference module passes it at scale 1 (util_converse.py:166): then
+        # X0 = Y and the solve is the module's X = Y (conj K + lambda) / (|K|^2 + lambda) on the
+        # given (already padded) plane, one forward and one inverse transform instead of two and one
+        return converse2d_fused(x, weight, bias.reshape(-1), 1, 0, "constant", eps, cache=cache)
     x, x0 = x.contiguous(), x0.contiguous()
     dev = x.device
     out = torch.empty((B, C, h * s, w * s), dtype=torch.float32, device=dev)

@@ -73,7 +73,8 @@ def test_route_query_and_environment(monkeypatch):
     monkeypatch.delenv("CVN_DISABLE_FUSED", raising=False)
     assert lib.cvn_converse2d_route(16, 64, 256, 256, 1, 5, 5, 1, 2) == _lib.ROUTE_FUSED  # 260^2
     assert lib.cvn_converse2d_route(8, 128, 256, 256, 1, 7, 7, 1, 6) == _lib.ROUTE_PFA268  # 268^2
-    assert lib.cvn_converse2d_route(8, 64, 64, 64, 1, 3, 3, 2, 1) == _lib.ROUTE_GENERIC  # s = 2
+    assert lib.cvn_converse2d_route(8, 64, 64, 64, 1, 3, 3, 2, 1) == _lib.ROUTE_FUSED  # cfg2: 66 -> 132
+    assert lib.cvn_converse2d_route(8, 64, 60, 60, 1, 3, 3, 2, 1) == _lib.ROUTE_GENERIC  # 62 -> 124
     monkeypatch.setenv("CVN_DISABLE_FUSED", "1")
     assert lib.cvn_converse2d_route(16, 64, 256, 256, 1, 5, 5, 1, 2) == _lib.ROUTE_GENERIC
     assert lib.cvn_converse2d_route(8, 128, 256, 256, 1, 7, 7, 1, 6) == _lib.ROUTE_GENERIC
@@ -84,7 +85,7 @@ def test_route_query_and_environment(monkeypatch):
 
 def test_explicit_route_must_serve_geometry_and_table_size_is_checked():
     lib = _lib.load()
-    geo = (8, 64, 64, 64, 1, 3, 3, 2, 1)  # s = 2: only the generic route serves it
+    geo = (8, 64, 60, 60, 1, 3, 3, 2, 1)  # s = 2 onto a 124 x 124 plane: only the generic route serves it
     assert lib.cvn_converse2d_table_bytes(*geo, _lib.ROUTE_FUSED) == 0
     assert lib.cvn_converse2d_table_bytes(*geo, _lib.ROUTE_PFA268) == 0
     assert lib.cvn_converse2d_table_bytes(*geo, 7) == 0

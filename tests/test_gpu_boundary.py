@@ -51,6 +51,24 @@ def test_registered_op_with_data(s):
     assert Fh.table_cache.bytes == 0
 
 
+@pytest.mark.parametrize("h,w", [(36, 30), (260, 260)])
+def test_registered_op_x0_is_x(h, w):
+    """The reference module's scale-1 call passes x0 = x (util_converse.py:166): the op then takes the
+    module route on the padded plane; the result is the op's, for an x whose border is arbitrary."""
+    rng = seeded("op-alias", h, w)
+    B, C, k = 2, 3, 5
+    x = rng.standard_normal((B, C, h, w)).astype(np.float32)
+    wt = softmax_psf(rng, C, k)
+    b = (0.3 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    xt = _t(x)
+    with torch.no_grad():
+        got = torch.ops.converse2d.forward(xt, xt, _t(wt), _t(b), 1, 1e-5).cpu().numpy()
+    ref = O.converse2d_op(x, x, wt, b, 1, 1e-5)
+    err = np.abs(got - ref).max()
+    print(f"converse2d::forward x0 is x {h}x{w}: max-abs {err:.3e}")
+    assert err <= TOL
+
+
 @pytest.mark.parametrize("H,k,p,s", [(256, 5, 2, 1), (256, 7, 6, 1), (40, 3, 1, 2), (30, 5, 2, 3)])
 def test_one_shot_entry_point(H, k, p, s):
     """cvn_converse2d_fwd_f32 with data on each route: fused 260^2, 268 path, generic s = 2 / 3."""

@@ -330,3 +330,40 @@ def test_module_biaseps_after_hip_forward():
         d(torch.randn(1, 64, 8, 8, device=dev), torch.rand(1, 64, 3, 3, device=dev), 2)
     assert torch.allclose(m.biaseps, torch.sigmoid(m.bias - 9.0) + 1e-5)
     assert torch.allclose(d.biaseps, torch.sigmoid(d.alpha - 9.0) + 1e-3)
+
+
+# ---------------------------------------------------------------------------------------------
+# Fused upsampling path: HR plane 132 x 132 from LR planes of 66 (s = 2), 44 (s = 3), 33 (s = 4)
+# ---------------------------------------------------------------------------------------------
+UP_CASES = [
+    # (B, C, H, W, k, s, p, mode, psf batch)
+    (2, 3, 64, 64, 3, 2, 1, "circular", 1),   # cfg2's geometry
+    (1, 2, 62, 62, 5, 2, 2, "reflect", 1),
+    (2, 2, 40, 40, 5, 3, 2, "replicate", 1),
+    (1, 3, 31, 31, 4, 4, 1, "constant", 1),
+    (2, 2, 33, 33, 7, 4, 0, "circular", 2),   # per-sample psf, no padding
+]
+
+
+@pytest.mark.parametrize("B,C,H,W,k,s,p,mode,pb", UP_CASES)
+def test_fused_upsampling_path(B, C, H, W, k, s, p, mode, pb, monkeypatch):
+    from conversenet_amd import _lib
+    from conversenet_amd import functional as Fh
+    rng = seeded("up", B, C, H, W, k, s, p, mode, pb)
+    x = rng.standard_normal((B, C, H, W)).astype(np.float32)
+    w = softmax_psf(rng, C, k, pb)
+    b = (0.3 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    lib = _lib.load()
+    assert lib.cvn_converse2d_route(B, C, H, W, pb, k, k, s, p) == _lib.ROUTE_FUSED
+    dev = torch.device("cuda")
+    xt, wt, bt = (torch.from_numpy(a).to(dev) for a in (x, w, b))
+    got = Fh.converse2d_fused(xt, wt, bt.reshape(-1), s, p, mode, 1e-5).cpu().numpy()
+    gelu = Fh.converse2d_fused(xt, wt, bt.reshape(-1), s, p, mode, 1e-5, act="gelu").cpu().numpy()
+    ref = O.converse2d_module(x, w, b, s, p, mode, 1e-5)
+    err = np.abs(got - ref).max()
+    print(f"fused up B{B} C{C} {H}x{W} k{k} s{s} p{p} {mode} pb{pb}: max-abs {err:.3e}")
+    assert err <= TOL
+    assert np.abs(gelu - O.gelu(ref)).max() <= TOL
+    monkeypatch.setenv("CVN_DISABLE_FUSED", "1")
+    generic = Fh.converse2d_fused(xt, wt, bt.reshape(-1), s, p, mode, 1e-5).cpu().numpy()
+    assert np.abs(generic - got).max() <= TOL
