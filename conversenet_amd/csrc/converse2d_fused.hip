@@ -382,18 +382,10 @@ __device__ __forceinline__ void group_forward_passes_loading(float2* buf, const 
   group_prefetch<P, C3, N>(pre, xr, a, 1, wave, lane);
 }
 
+// Cropped rows of group G (inverse transformed, in LDS) to the output, GELU applied on store.
 template <class P>
-__device__ __forceinline__ void group_inverse_store(float2* buf, const short* pa, const short* pb, const int (&lp)[4],
-                                                    __amdgpu_buffer_rsrc_t orsrc, const FusedArgs& a, int G,
-                                                    int wave, int lane, int tid) {
-  col_pass_b<P, true>(buf, pa, pb, tid);
-  lds_barrier();
-  col_pass_a_inv<P>(buf, pa, pb, tid);
-  lds_barrier();
-  row_pass_b<P, true>(buf, tid);
-  lds_barrier();
-  row_pass_a<P, true>(buf, tid);
-  lds_barrier();
+__device__ __forceinline__ void group_store(const float2* buf, const int (&lp)[4], __amdgpu_buffer_rsrc_t orsrc,
+                                            const FusedArgs& a, int G, int wave, int lane) {
   const float* fb = (const float*)buf;
 #pragma unroll 1
   for (int i = 0; i < RowIO<P>::RPW; ++i) {
@@ -410,6 +402,21 @@ __device__ __forceinline__ void group_inverse_store(float2* buf, const short* pa
       }
     }
   }
+}
+
+template <class P>
+__device__ __forceinline__ void group_inverse_store(float2* buf, const short* pa, const short* pb, const int (&lp)[4],
+                                                    __amdgpu_buffer_rsrc_t orsrc, const FusedArgs& a, int G,
+                                                    int wave, int lane, int tid) {
+  col_pass_b<P, true>(buf, pa, pb, tid);
+  lds_barrier();
+  col_pass_a_inv<P>(buf, pa, pb, tid);
+  lds_barrier();
+  row_pass_b<P, true>(buf, tid);
+  lds_barrier();
+  row_pass_a<P, true>(buf, tid);
+  lds_barrier();
+  group_store<P>(buf, lp, orsrc, a, G, wave, lane);
 }
 
 // Table entries of the combine step are loaded kTabBatch slots at a time.
@@ -907,7 +914,6 @@ int fused_apply_run(const float* x, int64_t B, int64_t C, int H, int W, int64_t 
                               (int)P::LDS_BYTES);
     (void)hipGetLastError();
   });
-  const int64_t Cp = psf_batch * C;
   const float4* t4 = (const float4*)table;
   FusedArgs fa{x, t4, out, B, C, psf_batch, H, W, pad, mode, act};
   hipLaunchKernelGGL(k_converse2d_fused<P>, dim3((unsigned)(B * C)), dim3(kFT), P::LDS_BYTES, st, fa);

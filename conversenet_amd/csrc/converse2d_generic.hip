@@ -1420,7 +1420,7 @@ int module_route(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, 
   if (!plan_tabs(*g, &t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
   const ModWs w = module_ws(*g, t);
   r->table_bytes = w.S;
-  r->scratch_bytes = w.total - w.S;
+  r->scratch_bytes = want == CVN_ROUTE_PFA268 ? std::max(w.total - w.S, pfa268_scratch_bytes(g->P)) : w.total - w.S;
   return CVN_OK;
 }
 

@@ -23,6 +23,11 @@ namespace cvn {
 namespace pfa268 {
 
 constexpr int L = 268, P = 67, RM = 66, NC = L / 2 + 1;  // NC: half-spectrum bins
+// Between the passes a half-spectrum column occupies LP = 272 rows (2176 B, a whole number of 128-B
+// lines; rows 268..271 are padding), and the row passes index LQ = 136 quads per plane (134 row
+// pairs and 2 idle quads on the padding rows), so that each wave's 16 quads cover whole 128-B lines
+// of every column they read or write: no line is shared between waves, each is fetched once.
+constexpr int LP = 272, LQ = 136;
 
 // Index tables, evaluated at compile time: gp[q] = 2^q mod 67, gq[q] = 2^-q mod 67 (34 = 2^-1), and
 // kap[s] = the k with k = s (mod 6), k = 2 s (mod 11).
@@ -295,9 +300,11 @@ __global__ void __launch_bounds__(256) k_pfa_rows_fwd(RowsArgs a) {
   const int k = threadIdx.x & 3;
   const int64_t gq = (int64_t)blockIdx.x * (blockDim.x >> 2) + (threadIdx.x >> 2);
   if (gq >= a.nquad) return;  // whole quads leave together
-  const int64_t plane = gq / (L / 2);
-  const int t = (int)(gq - plane * (L / 2));
-  const int ra = pad_map(2 * t, a.H, a.pad, a.mode), rb = pad_map(2 * t + 1, a.H, a.pad, a.mode);
+  const int64_t plane = gq / LQ;
+  const int t = (int)(gq - plane * LQ);
+  // quads t = 134, 135 transform zero rows and write the padding rows 268..271
+  const int ra = t < L / 2 ? pad_map(2 * t, a.H, a.pad, a.mode) : -1;
+  const int rb = t < L / 2 ? pad_map(2 * t + 1, a.H, a.pad, a.mode) : -1;
   const float* xa = a.x + (plane * a.H + (ra < 0 ? 0 : ra)) * (int64_t)a.W;
   const float* xb = a.x + (plane * a.H + (rb < 0 ? 0 : rb)) * (int64_t)a.W;
   const int sig = quad_sig(k);
@@ -329,13 +336,13 @@ __global__ void __launch_bounds__(256) k_pfa_rows_fwd(RowsArgs a) {
   sched_fence();
   // two real rows: Ya = (Z[v] + conj Z[-v]) / 2, Yb = (Z[v] - conj Z[-v]) / (2i)
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.S, a.s_bytes);
-  const uint32_t base = (uint32_t)((plane * NC * L + 2 * t) * 8);
+  const uint32_t base = (uint32_t)((plane * NC * LP + 2 * t) * 8);
   int v = (201 * quad_bin(k)) % L;
 #pragma unroll
   for (int j = 0; j < P; ++j) {
     const float2 z = x[j], zm = dpp2<kHerm>(x[(P - j) % P]);
     bstore4(make_float4(0.5f * (z.x + zm.x), 0.5f * (z.y - zm.y), 0.5f * (z.y + zm.y), 0.5f * (zm.x - z.x)), sr,
-            v <= L / 2 ? base + (uint32_t)(v * L * 8) : kDrop);
+            v <= L / 2 ? base + (uint32_t)(v * LP * 8) : kDrop);
     v += 68;
     if (v >= L) v -= L;
     if (j % kLoadChunk == kLoadChunk - 1) sched_fence();
@@ -345,21 +352,36 @@ __global__ void __launch_bounds__(256) k_pfa_rows_fwd(RowsArgs a) {
 // ---- columns: forward transform, x Phi, inverse transform, in place on S ----
 // quad index g = plane * NC + column.
 struct ColsArgs {
-  float2* S;          // (P, NC, L)
+  float2* S;          // (P, NC, LP)
   const float2* phi;  // (Cp, P, NC, 4) quad layout (pfa268_phi_index), 1/(L L) folded in
-  int64_t C, psf_batch, nquad;
+  int64_t B, C, psf_batch, nquad;
 };
+
+// Column quad handled by a thread.  With one table per channel, the quads are walked channel-major
+// (the B planes of a channel one after another), and the dispatcher's round-robin over the 8 XCDs
+// (workgroup i runs on XCD i % 8) is undone, so the workgroups of one XCD take consecutive runs of
+// that order: a channel's 289 KB table is then fetched into an XCD's L2 once for its B planes instead
+// of once per plane.
+__device__ __forceinline__ int64_t cols_quad(const ColsArgs& a) {
+  int64_t blk = blockIdx.x;
+  const int64_t nblk = gridDim.x;
+  if (a.psf_batch == 1 && nblk % 8 == 0) blk = (blk & 7) * (nblk >> 3) + (blk >> 3);
+  const int64_t g = blk * (blockDim.x >> 2) + (threadIdx.x >> 2);
+  if (a.psf_batch != 1 || g >= a.nquad) return g;
+  const int64_t pl = g / NC;  // plane in channel-major order
+  return ((pl % a.B) * a.C + pl / a.B) * NC + (g - pl * NC);
+}
 
 __global__ void __launch_bounds__(256) k_pfa_cols(ColsArgs a) {
   __shared__ QuadTabs T;
   load_quad_tabs(T, 0, 0, 0);
   const int k = threadIdx.x & 3;
-  const int64_t gq = (int64_t)blockIdx.x * (blockDim.x >> 2) + (threadIdx.x >> 2);
+  const int64_t gq = cols_quad(a);
   if (gq >= a.nquad) return;
   const int64_t plane = gq / NC;
   const int c = (int)(gq - plane * NC);
   const int64_t cp = a.psf_batch == 1 ? plane % a.C : plane;
-  float2* col = a.S + (plane * NC + c) * (int64_t)L + quad_sig(k);
+  float2* col = a.S + gq * (int64_t)LP + quad_sig(k);
   float2 x[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) {
@@ -417,10 +439,12 @@ __global__ void __launch_bounds__(256) k_pfa_rows_inv(RowsInvArgs a) {
   const int k = threadIdx.x & 3;
   const int64_t gq = (int64_t)blockIdx.x * (blockDim.x >> 2) + (threadIdx.x >> 2);
   if (gq >= a.nquad) return;
-  const int64_t plane = gq / (L / 2);
-  const int t = (int)(gq - plane * (L / 2));
-  const float2* Sp = a.S + plane * (int64_t)NC * L + 2 * t;
-  // Z[v] = Ha[v] + i Hb[v] with H[-v] = conj H[v]
+  const int64_t plane = gq / LQ;
+  const int t = (int)(gq - plane * LQ);  // t = 134, 135: padding rows, nothing stored
+  const float2* Sp = a.S + plane * (int64_t)NC * LP + 2 * t;
+  // Z[v] = Ha[v] + i Hb[v] with H[-v] = conj H[v].  (Each column is read twice by a quad, for v and for
+  // -v; pairing the two reads in time cuts the reads from 1.55x to 1.0x the half spectra but made the
+  // pass slower: it is latency-bound, and the pairing held more registers live.)
   float2 x[P];
   const int kb = quad_bin(k);
   int v = (201 * kb) % L;
@@ -433,7 +457,7 @@ __global__ void __launch_bounds__(256) k_pfa_rows_inv(RowsInvArgs a) {
 #pragma unroll
     for (int jj = 0; jj < kLoadChunk && j0 + jj < P; ++jj) {
       const bool lo = v <= L / 2;
-      h[jj] = *(const float4*)(Sp + (int64_t)(lo ? v : L - v) * L);
+      h[jj] = *(const float4*)(Sp + (int64_t)(lo ? v : L - v) * LP);
       // imaginary parts: conjugated past L/2, zero at the real bins 0 and L/2
       sg[jj] = j0 + jj == 0 ? sg0 : (lo ? 1.f : -1.f);
       v += 68;
@@ -452,7 +476,7 @@ __global__ void __launch_bounds__(256) k_pfa_rows_inv(RowsInvArgs a) {
   dft67_reg<true>(x);
   sched_fence();
   const int sig = quad_sig(k);
-  const int r0 = 2 * t - a.pad, r1 = r0 + 1;
+  const int r0 = t < L / 2 ? 2 * t - a.pad : -1, r1 = t < L / 2 ? r0 + 1 : -1;
   const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.out, a.out_bytes);
   const bool wa = r0 >= 0 && r0 < a.H, wb = r1 >= 0 && r1 < a.H;
   const uint32_t ba = (uint32_t)(((plane * a.H + r0) * a.W - a.pad + sig) * 4);
@@ -481,28 +505,30 @@ constexpr int kQuadsPerBlock = 64;  // 256 threads
 
 bool pfa268_applies(int h, int w, int s) { return h == pfa268::L && w == pfa268::L && s == 1; }
 
-// S: (P, NC, L) scratch; phi: (Cp, NC, L).
+size_t pfa268_scratch_bytes(int64_t P) { return align_up((size_t)P * pfa268::NC * pfa268::LP * sizeof(float2)); }
+
+// S: (P, NC, LP) scratch (pfa268_scratch_bytes); phi: (Cp, NC, L) in the quad layout.
 int pfa268_forward(const float* x, int64_t P, int64_t C, int64_t psf_batch, int H, int W, int pad, int mode, int act,
                    const float2* phi, float2* S, float* out, hipStream_t st) {
   using namespace pfa268;
-  const int64_t nrq = P * (L / 2), ncq = P * NC;
-  const int64_t nrb = (nrq + kQuadsPerBlock - 1) / kQuadsPerBlock, ncb = (ncq + kQuadsPerBlock - 1) / kQuadsPerBlock;
-  if (ncb > 0x7fffffff) return fail(CVN_ERR_UNSUPPORTED, "too many planes for the 268 path");
-  const int64_t s_bytes = P * NC * L * 8, o_bytes = P * (int64_t)H * W * 4;
+  const int64_t nfq = P * LQ, ncq = P * NC;
+  const int64_t ncb = (ncq + kQuadsPerBlock - 1) / kQuadsPerBlock, nfb = (nfq + kQuadsPerBlock - 1) / kQuadsPerBlock;
+  if (ncb > 0x7fffffff || nfb > 0x7fffffff) return fail(CVN_ERR_UNSUPPORTED, "too many planes for the 268 path");
+  const int64_t s_bytes = P * NC * LP * 8, o_bytes = P * (int64_t)H * W * 4;
   if (s_bytes >= ((int64_t)1 << 31) || o_bytes >= ((int64_t)1 << 31))
     return fail(CVN_ERR_UNSUPPORTED, "the 268 path addresses its buffers with 31-bit byte offsets");
-  RowsArgs ra{x, S, nrq, H, W, pad, mode, (uint32_t)s_bytes};
-  hipLaunchKernelGGL(k_pfa_rows_fwd, dim3((unsigned)nrb), dim3(4 * kQuadsPerBlock), 0, st, ra);
+  RowsArgs ra{x, S, nfq, H, W, pad, mode, (uint32_t)s_bytes};
+  hipLaunchKernelGGL(k_pfa_rows_fwd, dim3((unsigned)nfb), dim3(4 * kQuadsPerBlock), 0, st, ra);
   int rc = check_launch("268 row pass");
   if (rc != CVN_OK) return rc;
-  ColsArgs ca{S, phi, C, psf_batch, ncq};
+  ColsArgs ca{S, phi, P / C, C, psf_batch, ncq};
   hipLaunchKernelGGL(k_pfa_cols, dim3((unsigned)ncb), dim3(4 * kQuadsPerBlock), 0, st, ca);
   if ((rc = check_launch("268 column pass")) != CVN_OK) return rc;
-  RowsInvArgs ia{S, out, nrq, H, W, pad, (uint32_t)o_bytes};
+  RowsInvArgs ia{S, out, nfq, H, W, pad, (uint32_t)o_bytes};
   if (act == CVN_ACT_GELU)
-    hipLaunchKernelGGL(k_pfa_rows_inv<true>, dim3((unsigned)nrb), dim3(4 * kQuadsPerBlock), 0, st, ia);
+    hipLaunchKernelGGL(k_pfa_rows_inv<true>, dim3((unsigned)nfb), dim3(4 * kQuadsPerBlock), 0, st, ia);
   else
-    hipLaunchKernelGGL(k_pfa_rows_inv<false>, dim3((unsigned)nrb), dim3(4 * kQuadsPerBlock), 0, st, ia);
+    hipLaunchKernelGGL(k_pfa_rows_inv<false>, dim3((unsigned)nfb), dim3(4 * kQuadsPerBlock), 0, st, ia);
   return check_launch("268 inverse row pass");
 }
 

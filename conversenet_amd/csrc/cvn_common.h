@@ -152,6 +152,8 @@ __host__ __device__ inline int64_t pfa268_phi_index(int64_t cp, int v, int u) {
 }
 int pfa268_forward(const float* x, int64_t P, int64_t C, int64_t psf_batch, int H, int W, int pad, int mode, int act,
                    const float2* phi, float2* S, float* out, hipStream_t st);
+// Scratch the 268 path needs between its passes (at least the generic path's S region).
+size_t pfa268_scratch_bytes(int64_t P);
 // CVN_DISABLE_FUSED=1 in the environment routes every call through the generic multi-pass path.
 bool fused_disabled();
 
