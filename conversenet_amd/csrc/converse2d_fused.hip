@@ -46,8 +46,12 @@ __device__ __forceinline__ float4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t voff
 __device__ __forceinline__ float2 bload2(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
 }
+// Output rows are written once and never read back by the kernel: stored non-temporal (cache policy
+// bit NT), so they stream through L2 instead of evicting the transfer tables and the input rows that
+// the other planes on the XCD are still reading (measured at cfg3: 0.238 -> 0.218 ms per call).
+constexpr int kCpolNT = 2;
 __device__ __forceinline__ void bstore4(float4 v, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, v), r, voff, soff, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, v), r, voff, soff, kCpolNT);
 }
 
 __device__ __forceinline__ void lds_barrier() {
