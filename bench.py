@@ -468,6 +468,24 @@ def only_kernel(torch, Fh, args, dev, x, step):
         wl = torch.softmax(torch.randn(1, 128, 49, generator=g), -1).reshape(1, 128, 7, 7).to(dev)
         bl = torch.zeros(128, device=dev)
         fn = lambda: Fh.converse2d_fused(xl, wl, bl, 1, 6, "circular", 1e-5)
+    elif args.only == "oppath":
+        # torch.ops.converse2d.forward at cfg3 on the padded input (x0 = padded input), op table cached
+        import torch.nn.functional as F
+        c = CFG3
+        y = F.pad(x, [c["padding"]] * 4, mode=c["mode"])
+        b4 = step.b.reshape(1, -1, 1, 1)
+        torch.set_grad_enabled(False)
+        fn = lambda: torch.ops.converse2d.forward(y, y, step.w, b4, 1, c["eps"])
+    elif args.only == "grid":
+        # one point of the reference's speed grid: B8 C8 256x256, s = 2, k = 5, x0 = nearest(x)
+        import torch.nn.functional as F
+        torch.manual_seed(0)
+        xg = torch.randn(8, 8, 256, 256, device=dev)
+        x0 = F.interpolate(xg, scale_factor=2, mode="nearest")
+        wg = torch.softmax(torch.randn(1, 8, 25, device=dev), dim=-1).view(1, 8, 5, 5).contiguous()
+        bg = torch.zeros(1, 8, 1, 1, device=dev)
+        torch.set_grad_enabled(False)
+        fn = lambda: torch.ops.converse2d.forward(xg, x0, wg, bg, 2, 1e-5)
     elif args.only == "tail":
         # the block tail with the next block's head at Converse-DnCNN's shape (B8, 64 / 128 channels, 256x256)
         g = torch.Generator(device=dev).manual_seed(3)
@@ -505,7 +523,7 @@ def main():
     ap.add_argument("--cpu-iters", type=int, default=3)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--only", choices=["converse2d", "layernorm", "conv1x1", "copy", "dncnn", "usrnet", "backward",
-                                       "cfg1", "cfg2", "pfa268", "tail"],
+                                       "cfg1", "cfg2", "pfa268", "tail", "oppath", "grid"],
                     help="run one kernel family alone (for rocprofv3)")
     args = ap.parse_args()
 
