@@ -107,13 +107,34 @@ struct FusedPlan {
   static __host__ __device__ constexpr int rfpos(int k) { return (k % Q1) * CS1 + (k % Q2) * CS2 + (k % 2); }
 };
 
+// Work item w of a row pass -> (row pair t, index i < PER within the row pair).  Row pairs run fastest
+// across the lanes of a wave: with the odd row-pair stride RS, the 64 row pairs of a wave then fall on
+// every LDS bank (32 banks of 8 bytes for 64-bit accesses) exactly twice.  Whole blocks of 64 row
+// pairs come first, each wave taking one index i of one block; the NP mod 64 remaining row pairs
+// come last, row pair fastest.  (A plain i = w / NP, t = w mod NP lets a wave straddle the wrap from
+// row pair NP - 1 to row pair 0, which puts three lanes on some banks.)
+template <class P, int PER>
+__device__ __forceinline__ void row_item(int w, int& t, int& i) {
+  constexpr int T0 = P::NP / 64 * 64, RT = P::NP - T0;
+  if (T0 > 0 && w < T0 * PER) {
+    const int blk = (w >> 6) / PER;
+    i = (w >> 6) - blk * PER;
+    t = 64 * blk + (w & 63);
+  } else {
+    const int v = w - T0 * PER;
+    i = v / RT;
+    t = T0 + (v - i * RT);
+  }
+}
+
 // Row pass A: radix R3 along the contiguous axis (positions base + m, m < R3).
 template <class P, bool INV>
 __device__ __forceinline__ void row_pass_a(float2* buf, int tid) {
   constexpr int R = P::R3, PER = P::M / R;
 #pragma unroll 1
   for (int w = tid; w < P::NP * PER; w += kFT) {
-    const int i = w / P::NP, t = w - i * P::NP;  // row pair fastest across lanes (LDS bank spread)
+    int t, i;
+    row_item<P, PER>(w, t, i);
     dft_odd_mem<R, 1, INV>(buf + t * P::RS + i * R);
   }
 }
@@ -124,7 +145,8 @@ __device__ __forceinline__ void row_pass_b(float2* buf, int tid) {
   constexpr int R1 = P::R1, R2 = P::R2, PER = P::R3;
 #pragma unroll 1
   for (int w = tid; w < P::NP * PER; w += kFT) {
-    const int n3 = w / P::NP, t = w - n3 * P::NP;  // row pair fastest across lanes (LDS bank spread)
+    int t, n3;
+    row_item<P, PER>(w, t, n3);
     float2* b = buf + t * P::RS + n3;
     float2 u[R1][R2];
 #pragma unroll
