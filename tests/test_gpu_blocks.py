@@ -282,6 +282,27 @@ def test_cfg3_full_size_planes_vs_oracle():
     assert err <= TOL
 
 
+def test_cfg3_full_size_layernorm_and_conv1x1_gelu_vs_oracle():
+    """The rest of the cfg3 workload at its full shape (B16 C64 256x256): channels-first LayerNorm
+    (eps 1e-6, non-trivial affine) and the 1x1 conv 64 -> 64 + GELU on its output, each against the
+    fp64 oracle on the same inputs."""
+    from conversenet_amd import functional as Fh
+    x, _ = _cfg3()
+    g = torch.Generator().manual_seed(5)
+    lw, lb = 1 + 0.1 * torch.randn(64, generator=g), 0.1 * torch.randn(64, generator=g)
+    cw, cb = torch.randn(64, 64, 1, 1, generator=g) / 8, 0.1 * torch.randn(64, generator=g)
+    xd = x.to(DEV)
+    ln = Fh.layernorm_cf(xd, lw.to(DEV), lb.to(DEV), 1e-6)
+    y = Fh.conv1x1(ln, cw.to(DEV), cb.to(DEV), act="gelu")
+    torch.cuda.synchronize()
+    ln_ref = O.layernorm_cf(x.numpy(), lw.numpy(), lb.numpy(), 1e-6)
+    e_ln = float(np.abs(ln.cpu().numpy() - ln_ref).max())
+    y_ref = O.gelu(O.conv1x1(ln.cpu().numpy(), cw.numpy(), cb.numpy()))  # same input as the kernel saw
+    e_y = float(np.abs(y.cpu().numpy() - y_ref).max())
+    print(f"cfg3 LayerNorm max-abs {e_ln:.3e}, 1x1+GELU max-abs {e_y:.3e}")
+    assert e_ln <= TOL and e_y <= TOL
+
+
 def test_cfg3_full_size_linearity_and_identity():
     """The solve is linear in x for fixed psf and bias; a centred delta psf makes it the identity
     (K = 1, so (conj K + lambda) / (|K|^2 + lambda) = 1)."""
