@@ -43,6 +43,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
 __device__ __forceinline__ float4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
+__device__ __forceinline__ float bload1(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
 __device__ __forceinline__ float2 bload2(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
 }
@@ -52,6 +55,14 @@ __device__ __forceinline__ float2 bload2(__amdgpu_buffer_rsrc_t r, uint32_t voff
 constexpr int kCpolNT = 2;
 __device__ __forceinline__ void bstore4(float4 v, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, v), r, voff, soff, kCpolNT);
+}
+// Rows whose byte length is not a multiple of the 128-B line (W % 32 != 0) make partial-line
+// writes, which are merged in L2 with ordinary stores and not with streaming ones; so are single words.
+__device__ __forceinline__ void bstore4c(float4 v, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, v), r, voff, soff, 0);
+}
+__device__ __forceinline__ void bstore1(float v, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v), r, voff, soff, 0);
 }
 
 __device__ __forceinline__ void lds_barrier() {
@@ -331,6 +342,37 @@ __device__ __forceinline__ int plane_row(int rp, int G) {
   return 2 * g + G;
 }
 
+// Rows wider than the 256 columns the 64 lanes' float4 loads cover (the 260-point plan with no
+// padding to apply: the operator path on an already padded plane).  The tail elements of a group --
+// row position tr = tid / 4, column 256 + tid % 4 -- take one word per thread, loaded with the group's
+// rows and deposited and stored beside them.
+template <class P>
+struct RowTail {
+  static constexpr int TW = P::M > 256 ? P::M - 256 : 0;  // at most 4 for the 260 plan
+  static constexpr bool kAny = TW > 0;
+};
+template <class P, bool WIDE>
+__device__ __forceinline__ bool tail_item(const FusedArgs& a, int tid, int& tr, int& tc) {
+  if (!WIDE || !RowTail<P>::kAny || a.W <= 256) return false;
+  tr = tid >> 2;
+  tc = 256 + (tid & 3);
+  return tr < P::NH && tc < a.W;
+}
+template <class P, bool WIDE>
+__device__ __forceinline__ float tail_load(__amdgpu_buffer_rsrc_t xr, const FusedArgs& a, int G, int tid) {
+  int tr, tc;
+  float t = 0.f;
+  if (tail_item<P, WIDE>(a, tid, tr, tc)) {
+    const int sr = fpad_src(plane_row<P>(tr, G), a.H, a.pad, a.mode);
+    if (sr >= 0) t = bload1(xr, 4u * (uint32_t)tc, (uint32_t)(sr * a.W) * 4u);
+  }
+  return t;
+}
+template <class P>
+__device__ __forceinline__ float* tail_slot(float* fb, const FusedArgs& a, int tr, int tc) {
+  return fb + 2 * ((tr >> 1) * P::RS + P::pos_in(a.pad + tc)) + (tr & 1);
+}
+
 template <class P, int I0 = 0, int I1 = RowIO<P>::RPW>
 __device__ __forceinline__ void group_prefetch(float4 (&v)[RowIO<P>::RPW], __amdgpu_buffer_rsrc_t xr, const FusedArgs& a,
                                                int G, int wave, int lane) {
@@ -345,14 +387,14 @@ __device__ __forceinline__ void group_prefetch(float4 (&v)[RowIO<P>::RPW], __amd
   }
 }
 
-template <class P>
+template <class P, bool WIDE = false>
 __device__ __forceinline__ void group_deposit(float2* buf, const float4 (&v)[RowIO<P>::RPW], const int (&lp)[4],
-                                              int W, int wave, int lane) {
+                                              const FusedArgs& a, float tail, int wave, int lane) {
   float* fb = (float*)buf;
 #pragma unroll
   for (int i = 0; i < RowIO<P>::RPW; ++i) {
     const int rp = wave + i * RowIO<P>::NW;
-    if (rp < P::NH && 4 * lane < W) {
+    if (rp < P::NH && 4 * lane < a.W) {
       float* r = fb + 2 * ((rp >> 1) * P::RS) + (rp & 1);
       r[2 * lp[0]] = v[i].x;
       r[2 * lp[1]] = v[i].y;
@@ -360,6 +402,8 @@ __device__ __forceinline__ void group_deposit(float2* buf, const float4 (&v)[Row
       r[2 * lp[3]] = v[i].w;
     }
   }
+  int tr, tc;
+  if (tail_item<P, WIDE>(a, 64 * wave + lane, tr, tc)) *tail_slot<P>(fb, a, tr, tc) = tail;
 }
 
 // Padding columns copied inside LDS from the interior column they replicate (or zeroed).
@@ -390,13 +434,14 @@ __device__ __forceinline__ void group_forward_passes(float2* buf, const short* p
 
 // The same passes with G1's row loads issued a few at a time between them, so the loads never
 // queue up behind each other at issue and their HBM traffic spreads over G0's compute.
-template <class P>
+template <class P, bool WIDE>
 __device__ __forceinline__ void group_forward_passes_loading(float2* buf, const short* pa, const short* pb, int tid,
-                                                             float4 (&pre)[RowIO<P>::RPW],
+                                                             float4 (&pre)[RowIO<P>::RPW], float& tail,
                                                              __amdgpu_buffer_rsrc_t xr, const FusedArgs& a,
                                                              int wave, int lane) {
   constexpr int N = RowIO<P>::RPW, C1 = (N + 3) / 4, C2 = (2 * N + 3) / 4, C3 = (3 * N + 3) / 4;
   group_prefetch<P, 0, C1>(pre, xr, a, 1, wave, lane);
+  tail = tail_load<P, WIDE>(xr, a, 1, 64 * wave + lane);
   row_pass_a<P, false>(buf, tid);
   lds_barrier();
   group_prefetch<P, C1, C2>(pre, xr, a, 1, wave, lane);
@@ -409,7 +454,7 @@ __device__ __forceinline__ void group_forward_passes_loading(float2* buf, const 
 }
 
 // Cropped rows of group G (inverse transformed, in LDS) to the output, GELU applied on store.
-template <class P>
+template <class P, bool WIDE = false>
 __device__ __forceinline__ void group_store(const float2* buf, const int (&lp)[4], __amdgpu_buffer_rsrc_t orsrc,
                                             const FusedArgs& a, int G, int wave, int lane) {
   const float* fb = (const float*)buf;
@@ -424,13 +469,23 @@ __device__ __forceinline__ void group_store(const float2* buf, const int (&lp)[4
         if (a.act == CVN_ACT_GELU) {
           v.x = fgelu(v.x); v.y = fgelu(v.y); v.z = fgelu(v.z); v.w = fgelu(v.w);
         }
-        bstore4(v, orsrc, 16u * lane, (uint32_t)(orr * a.W) * 4u);
+        if (!WIDE || (a.W & 31) == 0) bstore4(v, orsrc, 16u * lane, (uint32_t)(orr * a.W) * 4u);
+        else bstore4c(v, orsrc, 16u * lane, (uint32_t)(orr * a.W) * 4u);
       }
+    }
+  }
+  int tr, tc;
+  if (tail_item<P, WIDE>(a, 64 * wave + lane, tr, tc)) {
+    const int orr = plane_row<P>(tr, G) - a.pad;
+    if (orr >= 0 && orr < a.H) {
+      float t = *tail_slot<P>(const_cast<float*>(fb), a, tr, tc);
+      if (a.act == CVN_ACT_GELU) t = fgelu(t);
+      bstore1(t, orsrc, 4u * (uint32_t)tc, (uint32_t)(orr * a.W) * 4u);
     }
   }
 }
 
-template <class P>
+template <class P, bool WIDE = false>
 __device__ __forceinline__ void group_inverse_store(float2* buf, const short* pa, const short* pb, const int (&lp)[4],
                                                     __amdgpu_buffer_rsrc_t orsrc, const FusedArgs& a, int G,
                                                     int wave, int lane, int tid) {
@@ -442,13 +497,15 @@ __device__ __forceinline__ void group_inverse_store(float2* buf, const short* pa
   lds_barrier();
   row_pass_a<P, true>(buf, tid);
   lds_barrier();
-  group_store<P>(buf, lp, orsrc, a, G, wave, lane);
+  group_store<P, WIDE>(buf, lp, orsrc, a, G, wave, lane);
 }
 
 // Table entries of the combine step are loaded kTabBatch slots at a time.
 constexpr int kTabBatch = 4;
 
-template <class P>
+// WIDE: rows past 256 columns (the 260 plan with no padding); a separate instantiation, so the
+// padded-input kernel carries none of the row-tail code.
+template <class P, bool WIDE>
 __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
   extern __shared__ float2 smem[];
   float2* buf = smem;
@@ -488,12 +545,13 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
   for (int c = 0; c < 4; ++c) lp[c] = P::pos_in(min(a.pad + 4 * lane + c, P::M - 1));
   float4 pre[RowIO<P>::RPW];
   group_prefetch<P>(pre, xr, a, 0, wave, lane);
+  float tail = tail_load<P, WIDE>(xr, a, 0, tid);
   lds_barrier();
-  group_deposit<P>(buf, pre, lp, a.W, wave, lane);
+  group_deposit<P, WIDE>(buf, pre, lp, a, tail, wave, lane);
   lds_barrier();
   group_pad_cols<P>(buf, pos, colsrc, a.pad, tid);
   lds_barrier();
-  group_forward_passes_loading<P>(buf, pa, pb, tid, pre, xr, a, wave, lane);  // G1 rows arrive meanwhile
+  group_forward_passes_loading<P, WIDE>(buf, pa, pb, tid, pre, tail, xr, a, wave, lane);  // G1 rows arrive meanwhile
   col_pass_b<P, false>(buf, pa, pb, tid);
   lds_barrier();
   constexpr int PL = P::PARK_LDS, PR = P::PARK - P::PARK_LDS;
@@ -505,7 +563,7 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
     else park[i - PL] = v;
   }
   lds_barrier();
-  group_deposit<P>(buf, pre, lp, a.W, wave, lane);
+  group_deposit<P, WIDE>(buf, pre, lp, a, tail, wave, lane);
   lds_barrier();
   group_pad_cols<P>(buf, pos, colsrc, a.pad, tid);
   lds_barrier();
@@ -546,12 +604,12 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
     asm volatile("" ::: "memory");  // the next batch's loads may not be hoisted above this one
   }
   lds_barrier();
-  group_inverse_store<P>(buf, pa, pb, lp, orsrc, a, 1, wave, lane, tid);
+  group_inverse_store<P, WIDE>(buf, pa, pb, lp, orsrc, a, 1, wave, lane, tid);
   lds_barrier();
 #pragma unroll
   for (int i = 0; i < P::PARK; ++i) buf[tid + i * kFT] = i < PL ? parkl[i * kFT + tid] : park[i < PL ? 0 : i - PL];
   lds_barrier();
-  group_inverse_store<P>(buf, pa, pb, lp, orsrc, a, 0, wave, lane, tid);
+  group_inverse_store<P, WIDE>(buf, pa, pb, lp, orsrc, a, 0, wave, lane, tid);
 }
 
 // ----------------------------------------------------------------------------------------------
@@ -936,25 +994,36 @@ int fused_apply_run(const float* x, int64_t B, int64_t C, int H, int W, int64_t 
                     int act, const void* table, float* out, hipStream_t st) {
   static std::atomic<uint64_t> attr{0};
   once_per_device(attr, [] {
-    (void)hipFuncSetAttribute((const void*)k_converse2d_fused<P>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    (void)hipFuncSetAttribute((const void*)k_converse2d_fused<P, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)P::LDS_BYTES);
+    if constexpr (RowTail<P>::kAny)
+      (void)hipFuncSetAttribute((const void*)k_converse2d_fused<P, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)P::LDS_BYTES);
     (void)hipGetLastError();
   });
   const float4* t4 = (const float4*)table;
   FusedArgs fa{x, t4, out, B, C, psf_batch, H, W, pad, mode, act};
-  hipLaunchKernelGGL(k_converse2d_fused<P>, dim3((unsigned)(B * C)), dim3(kFT), P::LDS_BYTES, st, fa);
+  bool wide = false;
+  if constexpr (RowTail<P>::kAny) wide = W > 256;
+  if constexpr (RowTail<P>::kAny) {
+    if (wide)
+      hipLaunchKernelGGL((k_converse2d_fused<P, true>), dim3((unsigned)(B * C)), dim3(kFT), P::LDS_BYTES, st, fa);
+  }
+  if (!wide)
+    hipLaunchKernelGGL((k_converse2d_fused<P, false>), dim3((unsigned)(B * C)), dim3(kFT), P::LDS_BYTES, st, fa);
   return check_launch("fused converse2d");
 }
 
-// The fused kernel loads rows as float4 per lane: W must be a multiple of 4 and at most 256.  At
-// scale > 1 the HR plane must have a fused plan (fused_up_geometry).
+// The fused kernel loads rows as float4 per lane: W must be a multiple of 4 and at most 256, or 260
+// on the 260-point plan with no padding (the last 4 columns go through single-word loads and stores).
+// At scale > 1 the HR plane must have a fused plan (fused_up_geometry).
 int fused_query(int H, int W, int pad, int scale, int64_t Cp, size_t* ws_bytes) {
   if (scale != 1) {
     if (!fused_up_geometry(H, W, pad, scale)) return 0;
     *ws_bytes = fused_ws<Plan132>(Cp);
     return 1;
   }
-  if (W % 4 != 0 || W > 256) return 0;
+  if (W % 4 != 0 || W > 260) return 0;  // past 256 columns only the 260 plan with no padding applies
   const int h = H + 2 * pad, w = W + 2 * pad;
   if (h == 260 && w == 260) { *ws_bytes = fused_ws<Plan260>(Cp); return 1; }
   if (h == 132 && w == 132) { *ws_bytes = fused_ws<Plan132>(Cp); return 1; }

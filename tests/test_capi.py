@@ -75,6 +75,8 @@ def test_route_query_and_environment(monkeypatch):
     assert lib.cvn_converse2d_route(8, 128, 256, 256, 1, 7, 7, 1, 6) == _lib.ROUTE_PFA268  # 268^2
     assert lib.cvn_converse2d_route(8, 64, 64, 64, 1, 3, 3, 2, 1) == _lib.ROUTE_FUSED  # cfg2: 66 -> 132
     assert lib.cvn_converse2d_route(8, 64, 60, 60, 1, 3, 3, 2, 1) == _lib.ROUTE_GENERIC  # 62 -> 124
+    assert lib.cvn_converse2d_route(16, 64, 260, 260, 1, 5, 5, 1, 0) == _lib.ROUTE_FUSED  # padded input, op path
+    assert lib.cvn_converse2d_route(16, 64, 258, 258, 1, 5, 5, 1, 1) == _lib.ROUTE_GENERIC  # 258 % 4 != 0
     monkeypatch.setenv("CVN_DISABLE_FUSED", "1")
     assert lib.cvn_converse2d_route(16, 64, 256, 256, 1, 5, 5, 1, 2) == _lib.ROUTE_GENERIC
     assert lib.cvn_converse2d_route(8, 128, 256, 256, 1, 7, 7, 1, 6) == _lib.ROUTE_GENERIC

@@ -123,6 +123,29 @@ def test_fused_path_vs_oracle(B, C, H, W, k, p, mode):
     assert err <= TOL, err
 
 
+@pytest.mark.parametrize("act", [None, "gelu"])
+def test_fused_260_wide_rows_no_padding(act):
+    """An already padded 260 x 260 plane with no padding to apply (the operator path's module route):
+    the fused kernel takes the row tail past 256 columns through single-word loads and stores."""
+    from conversenet_amd import _lib
+    from conversenet_amd import functional as Fh
+    rng = seeded("fused260", act)
+    B, C, k = 2, 3, 5
+    x = rng.standard_normal((B, C, 260, 260)).astype(np.float32)
+    w = softmax_psf(rng, C, k)
+    b = (0.4 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    assert _lib.load().cvn_converse2d_route(B, C, 260, 260, 1, k, k, 1, 0) == _lib.ROUTE_FUSED
+    ref = O.converse2d_module(x, w, b, 1, 0, "constant", 1e-5)
+    if act:
+        ref = O.gelu(ref)
+    dev = torch.device("cuda")
+    got = Fh.converse2d_fused(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev),
+                              torch.from_numpy(b).reshape(-1).to(dev), 1, 0, "constant", 1e-5, act=act)
+    err = np.abs(got.cpu().numpy() - ref).max()
+    print(f"fused 260 wide, no padding, act {act}: max-abs {err:.3e}")
+    assert err <= TOL, err
+
+
 def test_fused_per_sample_psf_and_gelu():
     from conversenet_amd import functional as Fh
     rng = seeded("fused-ps")
