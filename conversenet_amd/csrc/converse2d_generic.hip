@@ -216,10 +216,16 @@ __global__ void k_phi_op(PhiArgs a) {
 // formulas as k_phi_module / k_phi_op.
 // ------------------------------------------------------------------------------------------------
 struct PhiTileLds {
-  int zH, phH, hH, zW, phW, hW, P, psf, total;  // byte offsets
+  int zH, phH, hH, zW, phW, hW, P, psf, part, total;  // byte offsets
 };
 __host__ __device__ inline int round4(int n) { return (n + 3) & ~3; }
-__host__ __device__ inline PhiTileLds phi_tile_lds(int s, int Hs, int kh, int kw, int vc) {
+// The split-DFT evaluation of the tables (phi_tile_rows16) applies: scale 1, 2 or 4, HR height a
+// multiple of 16, all S (Hs / 16) row threads of an alias-class column in one block, and not the 268
+// path's layout.
+__host__ __device__ inline bool phi_rows16(int s, int Hs, bool q268) {
+  return !q268 && (s == 1 || s == 2 || s == 4) && Hs % 16 == 0 && s * (Hs / 16) <= 256;
+}
+__host__ __device__ inline PhiTileLds phi_tile_lds(int s, int Hs, int kh, int kw, int vc, bool fast = false) {
   PhiTileLds L;
   int o = 0;
   L.zH = o; o += Hs * 16;
@@ -230,6 +236,8 @@ __host__ __device__ inline PhiTileLds phi_tile_lds(int s, int Hs, int kh, int kw
   L.hW = o; o += vc * s * 16;
   L.P = o; o += vc * s * round4(kh) * 16;
   L.psf = o; o += kh * round4(kw) * 4;
+  o = (o + 15) & ~15;
+  L.part = o; o += (fast && s > 1 ? vc * Hs * 24 : 0);  // class partial sums (|K|^2, K h) per column member
   L.total = (o + 15) & ~15;
   return L;
 }
@@ -259,11 +267,12 @@ struct PhiTileView {
   double2 *zH, *phH, *hH, *zW, *phW, *hW, *P;
 };
 template <int S>
-__device__ PhiTileView phi_tile_prep(const PhiArgs& a, unsigned char* phl, int64_t cp, int vbeg, int nv, int vc) {
+__device__ PhiTileView phi_tile_prep(const PhiArgs& a, unsigned char* phl, int64_t cp, int vbeg, int nv, int vc,
+                                     bool fast = false) {
   const int tid = threadIdx.x, nth = blockDim.x;
   const int Hs = a.Hs, Ws = a.Ws, kh = a.kh, kw = a.kw;
   const int kh4 = round4(kh), kw4 = round4(kw);
-  const PhiTileLds L = phi_tile_lds(S, Hs, kh, kw, vc);
+  const PhiTileLds L = phi_tile_lds(S, Hs, kh, kw, vc, fast);
   PhiTileView t;
   t.zH = (double2*)(phl + L.zH);
   t.phH = (double2*)(phl + L.phH);
@@ -279,10 +288,23 @@ __device__ PhiTileView phi_tile_prep(const PhiArgs& a, unsigned char* phl, int64
     const int i = e / kw4, j = e - i * kw4;
     ps[e] = j < kw ? psf[i * kw + j] : 0.f;
   }
-  for (int u = tid; u < Hs; u += nth) {
-    t.zH[u] = dexpi((double)u, (double)Hs);
-    t.phH[u] = dexpi(-(double)(((int64_t)u * (kh / 2)) % Hs), (double)Hs);
-    if (S > 1) t.hH[u] = hold(S, u, Hs);
+  if (fast) {
+    // split-DFT form: z^u only (Hs a multiple of 4: a quarter by sincospi, the rest by the exact
+    // rotations z^(Q) = -i, z^(2Q) = -1, z^(3Q) = i); the hold sums follow from it below
+    const int Q = Hs >> 2;
+    for (int u = tid; u < Q; u += nth) {
+      const double2 z = dexpi((double)u, (double)Hs);
+      t.zH[u] = z;
+      t.zH[u + Q] = make_double2(z.y, -z.x);
+      t.zH[u + 2 * Q] = make_double2(-z.x, -z.y);
+      t.zH[u + 3 * Q] = make_double2(-z.y, z.x);
+    }
+  } else {
+    for (int u = tid; u < Hs; u += nth) {
+      t.zH[u] = dexpi((double)u, (double)Hs);
+      t.phH[u] = dexpi(-(double)(((int64_t)u * (kh / 2)) % Hs), (double)Hs);
+      if (S > 1) t.hH[u] = hold(S, u, Hs);
+    }
   }
   for (int e = tid; e < nv * S; e += nth) {
     const int v = e / S, b = e - v * S;
@@ -292,6 +314,18 @@ __device__ PhiTileView phi_tile_prep(const PhiArgs& a, unsigned char* phl, int64
     t.hW[e] = hold(S, vb, Ws);
   }
   __syncthreads();
+  if (S > 1 && fast)
+    for (int u = tid; u < Hs; u += nth) {  // hold sum sum_{t<S} z^(u t)
+      double2 acc = make_double2(1.0, 0.0);
+      int m = 0;
+      for (int q = 1; q < S; ++q) {
+        m += u;
+        m -= m >= Hs ? Hs : 0;
+        acc.x += t.zH[m].x;
+        acc.y += t.zH[m].y;
+      }
+      t.hH[u] = acc;
+    }
   // row sums (real coefficients, same four-chain Horner); rows zero-padded to kh4
   for (int e = tid; e < nv * S * kh4; e += nth) {
     const int vbq = e / kh4, i = e - vbq * kh4;
@@ -313,6 +347,187 @@ __device__ PhiTileView phi_tile_prep(const PhiArgs& a, unsigned char* phl, int64
   return t;
 }
 
+// 16-point DFT in place, X[k] = sum_i x[i] exp(-2 pi i i k / 16), fp64: radix 4 x 4 (decimation in
+// time: i = i0 + 4 i1, k = k0 + 4 k1; four 4-point DFTs over i1, twiddles w16^(i0 k0), four 4-point
+// DFTs over i0).  Twiddle constants cos / sin (2 pi m / 16), m = i0 k0 <= 9.
+__device__ __forceinline__ void ddft4(double2& x0, double2& x1, double2& x2, double2& x3) {
+  const double2 a0 = make_double2(x0.x + x2.x, x0.y + x2.y), a1 = make_double2(x0.x - x2.x, x0.y - x2.y);
+  const double2 b0 = make_double2(x1.x + x3.x, x1.y + x3.y), b1 = make_double2(x1.x - x3.x, x1.y - x3.y);
+  x0 = make_double2(a0.x + b0.x, a0.y + b0.y);
+  x2 = make_double2(a0.x - b0.x, a0.y - b0.y);
+  x1 = make_double2(a1.x + b1.y, a1.y - b1.x);  // a1 - i b1
+  x3 = make_double2(a1.x - b1.y, a1.y + b1.x);  // a1 + i b1
+}
+__device__ __forceinline__ void ddft16(double2 (&x)[16]) {
+  constexpr double kC[10] = {1.0, 0.92387953251128674, 0.70710678118654752, 0.38268343236508977, 0.0,
+                             -0.38268343236508977, -0.70710678118654752, -0.92387953251128674, -1.0,
+                             -0.92387953251128674};
+  constexpr double kS[10] = {0.0, 0.38268343236508977, 0.70710678118654752, 0.92387953251128674, 1.0,
+                             0.92387953251128674, 0.70710678118654752, 0.38268343236508977, 0.0,
+                             -0.38268343236508977};
+#pragma unroll
+  for (int i0 = 0; i0 < 4; ++i0) ddft4(x[i0], x[i0 + 4], x[i0 + 8], x[i0 + 12]);  // y[i0][k0] in x[i0 + 4 k0]
+#pragma unroll
+  for (int i0 = 1; i0 < 4; ++i0)
+#pragma unroll
+    for (int k0 = 1; k0 < 4; ++k0) {
+      const int m = i0 * k0;
+      const double2 v = x[i0 + 4 * k0];  // times exp(-2 pi i m / 16) = (cos, -sin)
+      x[i0 + 4 * k0] = make_double2(v.x * kC[m] + v.y * kS[m], v.y * kC[m] - v.x * kS[m]);
+    }
+#pragma unroll
+  for (int k0 = 0; k0 < 4; ++k0) ddft4(x[4 * k0], x[4 * k0 + 1], x[4 * k0 + 2], x[4 * k0 + 3]);  // X[k0 + 4 k1] in x[4 k0 + k1]
+  double2 t[16];
+#pragma unroll
+  for (int k0 = 0; k0 < 4; ++k0)
+#pragma unroll
+    for (int k1 = 0; k1 < 4; ++k1) t[k0 + 4 * k1] = x[4 * k0 + k1];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) x[k] = t[k];
+}
+
+// 1 / d in fp64 from the hardware reciprocal estimate and two Newton steps (relative error at the
+// level of fp64 rounding; the table entries are rounded to fp32 afterwards).
+__device__ __forceinline__ double drcp(double d) {
+  double r = __builtin_amdgcn_rcp(d);
+  r = fma(r, fma(-d, r, 1.0), r);
+  r = fma(r, fma(-d, r, 1.0), r);
+  return r;
+}
+
+// Split-DFT evaluation of the transfer function over rows (phi_rows16: Hs a multiple of 16).  One
+// thread per (HR column vb, row residue u1 < H1 = Hs / 16) evaluates K at the 16 rows u = u1 + H1 u2
+// by one split step of the DFT over rows instead of 16 Horner sums: with the centred psf rows
+// p_j = P[j + kh/2] (j in [-kh/2, kh - 1 - kh/2]), K(u) = sum_j p_j z^(u j), z = exp(-2 pi i / Hs), and
+// z^(H1 u2 j) depends on j mod 16 only, so K(u1 + H1 u2) = DFT16_u2( R[r] ), R[r] = sum_{j = r mod 16}
+// p_j z^(u1 j): about a fifth of the Horner form's fp64 operations per entry.
+__device__ __forceinline__ void phi_rows16_k(const PhiTileView& tv, int Hs, int kh, const double2* Pv, int u1,
+                                             double2 (&x)[16]) {
+  const int ch = kh / 2;
+  // R[r]: taps j = r - 16 q, r - 16 q + 16, ... from the lowest j >= -ch; z^(u1 j) as the table index
+  // m = u1 j mod Hs, stepped by A = 16 u1 < Hs (u1 r < Hs is already reduced)
+  const int A = 16 * u1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int q = (r + ch) >> 4;
+    int m = u1 * r;
+    for (int t = 0; t < q; ++t) {
+      m -= A;
+      m += m < 0 ? Hs : 0;
+    }
+    double2 acc = make_double2(0.0, 0.0);
+    for (int j = r - 16 * q; j < kh - ch; j += 16) {
+      const double2 p = Pv[j + ch], z = tv.zH[m];
+      acc = make_double2(fma(p.x, z.x, fma(-p.y, z.y, acc.x)), fma(p.x, z.y, fma(p.y, z.x, acc.y)));
+      m += A;
+      m -= m >= Hs ? Hs : 0;
+    }
+    x[r] = acc;
+  }
+  ddft16(x);
+}
+
+// Table entries from K, the same formulas as the Horner form of k_phi_tile: with the alias class's
+// sums mk2 = sum |K|^2 and mkh = sum K h_u h_v over its S x S members and rD = 1 / (mk2 / S^2 + lambda),
+// module: (h_u h_v + conj K (1 - mkh / S^2) rD) / (Hs Ws) (for S = 1: (conj K + lambda) rD / (Hs Ws));
+// op: K, and conj K rD / (Hs Ws).  At scale S > 1 a thread's 16 rows hold 16 / S whole alias classes
+// (rows u0 + a h, h = (16 / S) H1), and the S column members of a class are the block's threads
+// (v, b, u1) for b < S, which exchange their partial sums through LDS.
+template <int S>
+__device__ void phi_tile_rows16(const PhiArgs& a, int op, const PhiTileView& tv, double* part, int64_t cp, int vbeg,
+                                int nv, double lmb) {
+  const int Hs = a.Hs, kh4 = round4(a.kh), H1 = Hs >> 4;
+  const double norm = 1.0 / ((double)Hs * (double)a.Ws);
+  if constexpr (S == 1) {
+    for (int it = threadIdx.x; it < nv * H1; it += blockDim.x) {
+      const int v = it / H1, u1 = it - v * H1;
+      double2 x[16];
+      phi_rows16_k(tv, Hs, a.kh, tv.P + v * kh4, u1, x);
+      const int64_t vb = vbeg + v;
+#pragma unroll
+      for (int u2 = 0; u2 < 16; ++u2) {
+        const double2 k = x[u2];
+        const int u = u1 + H1 * u2;
+        const double rD = drcp(k.x * k.x + k.y * k.y + lmb);
+        if (op) {
+          const int64_t o = (cp * a.Ws + vb) * Hs + u;
+          a.kf[o] = make_float2((float)k.x, (float)k.y);
+          a.phi[o] = make_float2((float)(k.x * rD * norm), (float)(-k.y * rD * norm));
+        } else {
+          a.phi[(cp * a.NCs + vb) * Hs + u] = make_float2((float)((k.x + lmb) * rD * norm), (float)(-k.y * rD * norm));
+        }
+      }
+    }
+  } else {
+    constexpr int NM = 16 / S;  // alias classes per thread
+    constexpr double inv_s2 = 1.0 / (double)(S * S);
+    const int h = a.h;          // = NM H1
+    const int it = threadIdx.x;
+    const bool act = it < nv * S * H1;
+    const int v = it / (S * H1), rem = it - v * S * H1, b = rem / H1, u1 = rem - b * H1;
+    const int e = v * S + b;
+    double2 x[16];
+    if (act) {
+      phi_rows16_k(tv, Hs, a.kh, tv.P + e * kh4, u1, x);
+      const double2 hv = tv.hW[e];
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        double p2 = 0.0;
+        double2 pk = make_double2(0.0, 0.0);
+#pragma unroll
+        for (int aa = 0; aa < S; ++aa) {
+          const double2 k = x[m + NM * aa];
+          p2 += k.x * k.x + k.y * k.y;
+          if (!op) {
+            const double2 t = dcmul(k, tv.hH[u1 + H1 * (m + NM * aa)]);
+            pk.x += t.x;
+            pk.y += t.y;
+          }
+        }
+        pk = dcmul(pk, hv);
+        double* pp = part + ((int64_t)(v * h + u1 + H1 * m) * S + b) * 3;
+        pp[0] = p2;
+        pp[1] = pk.x;
+        pp[2] = pk.y;
+      }
+    }
+    __syncthreads();
+    if (act) {
+      const int64_t vb = vbeg + v + (int64_t)b * a.w;
+      const double2 hv = tv.hW[e];
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        const double* pp = part + (int64_t)(v * h + u1 + H1 * m) * S * 3;
+        double mk2 = 0.0;
+        double2 mkh = make_double2(0.0, 0.0);
+#pragma unroll
+        for (int bb = 0; bb < S; ++bb) {
+          mk2 += pp[3 * bb];
+          mkh.x += pp[3 * bb + 1];
+          mkh.y += pp[3 * bb + 2];
+        }
+        const double rD = drcp(mk2 * inv_s2 + lmb);
+        const double2 g = make_double2((1.0 - mkh.x * inv_s2) * rD, -mkh.y * inv_s2 * rD);
+        const double gop = rD * norm;
+#pragma unroll
+        for (int aa = 0; aa < S; ++aa) {
+          const double2 k = x[m + NM * aa];
+          const int u = u1 + H1 * (m + NM * aa);
+          if (op) {
+            const int64_t o = (cp * a.Ws + vb) * Hs + u;
+            a.kf[o] = make_float2((float)k.x, (float)k.y);
+            a.phi[o] = make_float2((float)(k.x * gop), (float)(-k.y * gop));
+          } else if (vb <= a.Ws / 2) {
+            const double2 hn = dcmul(tv.hH[u], hv);
+            const double2 t = dcmul(make_double2(k.x, -k.y), g);
+            a.phi[(cp * a.NCs + vb) * Hs + u] = make_float2((float)((hn.x + t.x) * norm), (float)((hn.y + t.y) * norm));
+          }
+        }
+      }
+    }
+  }
+}
+
 template <int S>
 __global__ void __launch_bounds__(256) k_phi_tile(PhiArgs a, int op, int vc, int nchunk) {
   extern __shared__ __align__(16) unsigned char phl[];
@@ -324,10 +539,17 @@ __global__ void __launch_bounds__(256) k_phi_tile(PhiArgs a, int op, int vc, int
   const int c = (int)(cp % a.C);
   const int Hs = a.Hs, Ws = a.Ws, h = a.h, kh = a.kh;
   const int kh4 = round4(kh);
-  const PhiTileView tv = phi_tile_prep<S>(a, phl, cp, vbeg, nv, vc);
+  const bool fast = phi_rows16(S, Hs, a.q268 != 0);
+  const PhiTileView tv = phi_tile_prep<S>(a, phl, cp, vbeg, nv, vc, fast);
   const double2 *zH = tv.zH, *phH = tv.phH, *hH = tv.hH, *hW = tv.hW, *P = tv.P;
 
   const double lmb = lambda_of(a, c);
+  if constexpr (S != 3) {
+    if (fast) {
+      phi_tile_rows16<S>(a, op, tv, (double*)(phl + phi_tile_lds(S, Hs, kh, a.kw, vc, true).part), cp, vbeg, nv, lmb);
+      return;
+    }
+  }
   const double norm = 1.0 / ((double)Hs * (double)Ws);
   const double inv_s2 = 1.0 / (double)(S * S);
   const int items = nv * h;
@@ -1318,8 +1540,11 @@ int launch_phi(const float* psf, const float* bias, float eps, const Geo& g, boo
     constexpr int kTileLds = 64 * 1024;
     int nchunk = (int)std::min<int64_t>(a.nv0, std::max<int64_t>(1, (2048 + g.Cp - 1) / g.Cp));
     int vc = (a.nv0 + nchunk - 1) / nchunk;
-    while (vc > 1 && phi_tile_lds(g.s, g.Hs, g.kh, g.kw, vc).total > kTileLds) --vc;
-    const int lds = phi_tile_lds(g.s, g.Hs, g.kh, g.kw, vc).total;
+    // split-DFT form (phi_tile_rows16): S Hs / 16 threads per LR column class, one round per block
+    const bool fast = phi_rows16(g.s, g.Hs, q268);
+    if (fast) vc = std::max(1, std::min(a.nv0, 256 / (g.s * (g.Hs / 16))));
+    while (vc > 1 && phi_tile_lds(g.s, g.Hs, g.kh, g.kw, vc, fast).total > kTileLds) --vc;
+    const int lds = phi_tile_lds(g.s, g.Hs, g.kh, g.kw, vc, fast).total;
     nchunk = (a.nv0 + vc - 1) / vc;
     if (lds <= kTileLds && g.Cp * nchunk <= 0x7fffffff) {
       const dim3 grid((unsigned)(g.Cp * nchunk));

@@ -298,9 +298,12 @@ def test_pfa268_per_sample_psf_gelu_and_generic_agreement(monkeypatch):
 DATA_STEP_CASES = [
     # (B, C, h, w, s)
     (2, 5, 64, 64, 1),
+    (2, 3, 256, 48, 1),
+    (1, 2, 96, 80, 1),
     (2, 3, 300, 40, 1),
     (2, 4, 16, 16, 4),
     (1, 3, 64, 64, 4),
+    (1, 2, 24, 20, 2),
     (2, 3, 30, 26, 2),
     (1, 2, 100, 34, 3),
 ]
@@ -323,11 +326,11 @@ def test_data_step_per_sample_psf(B, C, h, w, s):
     assert err <= TOL
 
 
-@pytest.mark.parametrize("s", [1, 4])
-def test_op_level_large_psf(s):
+@pytest.mark.parametrize("s,h,w", [(1, 30, 26), (4, 30, 26), (1, 32, 48), (2, 24, 20), (4, 16, 12)])
+def test_op_level_large_psf(s, h, w):
     from conversenet_amd import functional as Fh
-    rng = np.random.default_rng(77 + s)
-    B, C, h, w, k = 2, 3, 30, 26, 25
+    rng = np.random.default_rng(77 + s + h)
+    B, C, k = 2, 3, 25
     x = rng.standard_normal((B, C, h, w)).astype(np.float32)
     x0 = rng.standard_normal((B, C, h * s, w * s)).astype(np.float32)
     wt = softmax_psf(rng, C, k)
@@ -336,6 +339,22 @@ def test_op_level_large_psf(s):
     dev = torch.device("cuda")
     got = Fh.converse2d_op(*(torch.from_numpy(a).to(dev) for a in (x, x0, wt, b)), s, 1e-5).cpu().numpy()
     assert np.abs(got - ref).max() <= TOL
+
+
+@pytest.mark.parametrize("k", [2, 17, 34])
+def test_table_split_dft_rows_psf_sizes(k):
+    """Scale-1 tables on planes whose height is a multiple of 16 take the split-DFT evaluation of the
+    transfer function (one to three psf rows per residue mod 16, even and odd sizes)."""
+    rng = seeded("rows16", k)
+    B, C, H, W = 1, 3, 64, 48
+    x = rng.standard_normal((B, C, H, W)).astype(np.float32)
+    w = softmax_psf(rng, C, k)
+    b = (0.4 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    ref = O.converse2d_module(x, w, b, 1, 0, "circular", 1e-5)
+    got = _run_fused(x, w, b, 1, 0, "circular", 1e-5)
+    err = np.abs(got - ref).max()
+    print(f"rows16 k{k}: max-abs {err:.3e}")
+    assert err <= TOL, err
 
 
 def test_module_biaseps_after_hip_forward():
