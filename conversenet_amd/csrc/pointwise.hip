@@ -350,6 +350,126 @@ __device__ __forceinline__ void gemm_from_acc(const v4f (&v)[K / 16][Q], const f
   }
 }
 
+// ------------------------------------------------------------------------------------------------
+// fp32 products on the fp16 matrix cores ("split fp16").  Every operand x is split as x = x_h + x_l,
+// x_h = fp16(x) and x_l = fp16(x - x_h), both rounded toward zero (x - x_h is exact in fp32), so
+// |x - x_h - x_l| < 2^-20 |x|; a product is formed as a_l b_h + a_h b_l + a_h b_h (three
+// v_mfma_f32_16x16x32_f16, each product exact in the fp32 accumulator), dropping a_l b_l (< 2^-20
+// |a b|).  fp16 inputs below the normal range are kept by the matrix cores (gradual underflow), so
+// small values lose no relative accuracy beyond 2^-24 absolute.  A 16 x 16 x 32 block update then
+// takes three of these MFMAs (8192 multiply-adds each, half the issue time of one 16x16x4 fp32 MFMA)
+// instead of eight fp32 MFMAs.  fp16's range ends at 65504: a k-chunk whose activations exceed it in
+// any lane of the wave is multiplied on the fp32 matrix cores instead (weights rebuilt as x_h + x_l),
+// so no input range is lost.
+// Operand layout of the 16x16x32 MFMA: lane l = 16 g + j holds A[row j][k = 8 g + e] and
+// B[k = 8 g + e][col j], e < 8; D as for the fp32 MFMAs (lane 16 g + j: rows 4 g + r, col j).  The k
+// slot 8 g + e (e = 4 hf + r) of input chunk c is channel 16 (2 c + hf) + 4 g + r: the channels lane
+// group g holds in the accumulator layout (channel 16 rb + 4 g + r in register r of row block rb), so
+// a layer's accumulators feed the next layer's B operand directly.
+// ------------------------------------------------------------------------------------------------
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+constexpr float kF16Max = 65504.f;
+
+__device__ __forceinline__ void split_f16(const float (&x)[8], f16x8& h, f16x8& l) {
+  u32x4_t H, L;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const auto hp = __builtin_amdgcn_cvt_pkrtz(x[2 * i], x[2 * i + 1]);
+    const auto lp = __builtin_amdgcn_cvt_pkrtz(x[2 * i] - (float)hp[0], x[2 * i + 1] - (float)hp[1]);
+    H[i] = __builtin_bit_cast(unsigned, hp);
+    L[i] = __builtin_bit_cast(unsigned, lp);
+  }
+  h = __builtin_bit_cast(f16x8, H);
+  l = __builtin_bit_cast(f16x8, L);
+}
+
+// Weights (N outputs x K inputs, row-major fp32) in LDS for gemm_f16s: for input chunk c, output
+// block ob and lane 16 g + j, 16 bytes of high parts (W[16 ob + j][channel of k slot 8 g + e], e < 8),
+// and 1 KB further on the 16 bytes of low parts: consecutive lanes read consecutive 16-byte words.
+template <int N, int K>
+__device__ __forceinline__ void stage_f16s(const float* __restrict__ W, _Float16* Wl) {
+  for (int e = threadIdx.x; e < N * K; e += blockDim.x) {
+    const int e8 = e & 7, lj = (e >> 3) & 63, cob = e >> 9;
+    const int g = lj >> 4, j = lj & 15, hf = e8 >> 2, r = e8 & 3;
+    const int ob = cob % (N / 16), c = cob / (N / 16);
+    const float w = W[(16 * ob + j) * K + 16 * (2 * c + hf) + 4 * g + r];
+    const auto hp = __builtin_amdgcn_cvt_pkrtz(w, 0.f);
+    const auto lp = __builtin_amdgcn_cvt_pkrtz(w - (float)hp[0], 0.f);
+    Wl[cob * 1024 + lj * 8 + e8] = (_Float16)hp[0];
+    Wl[cob * 1024 + 512 + lj * 8 + e8] = (_Float16)lp[0];
+  }
+}
+
+// acc[ob][q] += W[16 ob + j][k] v[k] over all K input channels; v in the accumulator layout.
+template <int K, int N, int Q>
+__device__ __forceinline__ void gemm_f16s(const v4f (&v)[K / 16][Q], const _Float16* Wl, int lane,
+                                          v4f (&acc)[N / 16][Q]) {
+#pragma unroll
+  for (int c = 0; c < K / 32; ++c) {
+    float xb[Q][8];
+    float mx = 0.f;
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xb[q][e] = v[2 * c + (e >> 2)][q][e & 3];
+        mx = fmaxf(mx, fabsf(xb[q][e]));
+      }
+    // NaN compares false here and passes through the fp16 products as NaN
+    if (__builtin_amdgcn_ballot_w64(mx > kF16Max) == 0) {
+      f16x8 bh[Q], bl[Q];
+#pragma unroll
+      for (int q = 0; q < Q; ++q) split_f16(xb[q], bh[q], bl[q]);
+#pragma unroll
+      for (int ob = 0; ob < N / 16; ++ob) {
+        const u32x4_t* wp = (const u32x4_t*)(Wl + (c * (N / 16) + ob) * 1024) + lane;
+        const f16x8 ah = __builtin_bit_cast(f16x8, wp[0]), al = __builtin_bit_cast(f16x8, wp[64]);
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+          v4f t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[q], acc[ob][q], 0, 0, 0);
+          t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[q], t, 0, 0, 0);
+          acc[ob][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[q], t, 0, 0, 0);
+        }
+        mem_fence_sched();
+      }
+    } else {
+#pragma unroll
+      for (int ob = 0; ob < N / 16; ++ob) {
+        const u32x4_t* wp = (const u32x4_t*)(Wl + (c * (N / 16) + ob) * 1024) + lane;
+        const f16x8 ah = __builtin_bit_cast(f16x8, wp[0]), al = __builtin_bit_cast(f16x8, wp[64]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float w = (float)ah[e] + (float)al[e];
+#pragma unroll
+          for (int q = 0; q < Q; ++q) acc[ob][q] = mfma4(w, xb[q][e], acc[ob][q]);
+        }
+        mem_fence_sched();
+      }
+    }
+  }
+}
+
+// Loads a (channels x pixels) tile in the accumulator layout: channel 16 rb + 4 g + r in register r of
+// row block rb, Q consecutive pixels per lane (zeros outside the image).
+template <int N, int Q>
+__device__ __forceinline__ void load_acc(const float* w, int64_t hw, bool inb, uint32_t yoff, v4f (&v)[N / 16][Q]) {
+#pragma unroll
+  for (int rb = 0; rb < N / 16; ++rb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float rr[Q];
+      if (inb) {
+        ldq<Q>(at_off(w + (int64_t)(16 * rb + r) * hw, yoff), rr);
+      } else {
+#pragma unroll
+        for (int q = 0; q < Q; ++q) rr[q] = 0.f;
+      }
+#pragma unroll
+      for (int q = 0; q < Q; ++q) v[rb][q][r] = rr[q];
+    }
+}
+
 // ConverseBlock conv2 branch: y = x + res_scale * (W2 GELU(W1 LN(x) + b1) + b2)
 template <int C, int CM, int Q, int NW>
 __global__ void __launch_bounds__(64 * NW) k_ln_mlp_mfma(const float* x, int64_t HW, int64_t tpb, int64_t ntiles,
@@ -476,19 +596,16 @@ __device__ __forceinline__ void store_acc(const v4f (&v)[N / 16][Q], float* yw, 
 
 template <int CIN, int C, int CM, int Q, int NW, bool HEAD>
 __global__ void __launch_bounds__(64 * NW) k_conv_ln_mlp_mfma(TailArgs a) {
-  constexpr int LD0 = C + 16;   // W0t[k][i], k < CIN, i < C; read at (4 ks + g) LD0 + 16 rb + j
-  constexpr int LD1 = CM + 4;   // W1t[k][i], k < C, i < CM; read at (16 rb + 4 g + r) LD1 + 16 ob + j
-  constexpr int LD2 = C + 4;    // W2t[k][i], k < CM, i < C
-  constexpr int LDH = CIN + 4;  // Wht[k][i], k < C, i < CIN
+  static_assert(CIN % 32 == 0 && C % 32 == 0 && CM % 32 == 0, "split-fp16 GEMM chunks");
   constexpr int NP = 6 * C + CM + (HEAD ? 2 * C + CIN : 0);
-  __shared__ float W0t[CIN * LD0];
-  __shared__ float W1t[C * LD1];
-  __shared__ float W2t[CM * LD2];
-  __shared__ float Wht[HEAD ? C * LDH : 1];
+  __shared__ __align__(16) _Float16 W0l[2 * C * CIN];  // stage_f16s layouts
+  __shared__ __align__(16) _Float16 W1l[2 * CM * C];
+  __shared__ __align__(16) _Float16 W2l[2 * C * CM];
+  __shared__ __align__(16) _Float16 Whl[HEAD ? 2 * CIN * C : 8];
   __shared__ float prm[NP];  // b0, s1, LN weight, LN bias, b2, s2, b1 [, head LN weight, bias, head bias]
-  stage_wt<C, CIN, LD0>(a.W0, W0t);
-  stage_wt<CM, C, LD1>(a.W1, W1t);
-  stage_wt<C, CM, LD2>(a.W2, W2t);
+  stage_f16s<C, CIN>(a.W0, W0l);
+  stage_f16s<CM, C>(a.W1, W1l);
+  stage_f16s<C, CM>(a.W2, W2l);
   stage_vec<C>(a.b0, 0.f, prm);
   stage_vec<C>(a.s1, 1.f, prm + C);
   stage_vec<C>(a.lw, 1.f, prm + 2 * C);
@@ -497,7 +614,7 @@ __global__ void __launch_bounds__(64 * NW) k_conv_ln_mlp_mfma(TailArgs a) {
   stage_vec<C>(a.s2, 1.f, prm + 5 * C);
   stage_vec<CM>(a.b1, 0.f, prm + 6 * C);
   if (HEAD) {
-    stage_wt<CIN, C, LDH>(a.Wh, Wht);
+    stage_f16s<CIN, C>(a.Wh, Whl);
     stage_vec<C>(a.hlw, 1.f, prm + 6 * C + CM);
     stage_vec<C>(a.hlb, 0.f, prm + 7 * C + CM);
     stage_vec<CIN>(a.bh, 0.f, prm + 8 * C + CM);
@@ -505,7 +622,6 @@ __global__ void __launch_bounds__(64 * NW) k_conv_ln_mlp_mfma(TailArgs a) {
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, j = lane & 15;
-  const uint32_t xoff = (uint32_t)(((int64_t)g * a.HW + Q * j) * 4);
   const uint32_t yoff = (uint32_t)(((int64_t)4 * g * a.HW + Q * j) * 4);
   for (int64_t tt = blockIdx.x; tt < a.ntiles; tt += gridDim.x) {
     mem_fence_sched();
@@ -513,13 +629,13 @@ __global__ void __launch_bounds__(64 * NW) k_conv_ln_mlp_mfma(TailArgs a) {
     int64_t b;
     const int64_t pw = tile_px(tt, a.tpb, Q, NW, wave, &b);
     const bool inb = pw + Q * j < hw;
-    // first branch's last layer: acc = W0 t
+    // first branch's last layer: acc = W0 t (t read in the accumulator layout)
     v4f acc[C / 16][Q];
     {
-      float tv[CIN / 4][Q];
-      load_tile<CIN, Q>(a.t + b * CIN * hw + pw, hw, inb, xoff, tv);
+      v4f tv[CIN / 16][Q];
+      load_acc<CIN, Q>(a.t + b * CIN * hw + pw, hw, inb, yoff, tv);
       zero_acc<C, Q>(acc);
-      gemm_tile<CIN, C, Q>(tv, W0t, LD0, g, j, acc);
+      gemm_f16s<CIN, C, Q>(tv, W0l, lane, acc);
     }
     // y' = x + s1 (acc + b0), channel 16 rb + 4 g + r; x read in the same layout
     const float* xw = a.x + b * C * hw + pw;
@@ -547,7 +663,7 @@ __global__ void __launch_bounds__(64 * NW) k_conv_ln_mlp_mfma(TailArgs a) {
         v4f xn[C / 16][Q];
         ln_acc<C, Q>(acc, prm + 2 * C, prm + 3 * C, a.eps, g, xn);
         zero_acc<CM, Q>(h);
-        gemm_from_acc<C, CM, Q>(xn, W1t, LD1, g, j, h);
+        gemm_f16s<C, CM, Q>(xn, W1l, lane, h);
       }
 #pragma unroll
       for (int rb = 0; rb < CM / 16; ++rb)
@@ -558,7 +674,7 @@ __global__ void __launch_bounds__(64 * NW) k_conv_ln_mlp_mfma(TailArgs a) {
           for (int q = 0; q < Q; ++q) h[rb][q][r] = gelu_f(h[rb][q][r] + bo);
         }
       zero_acc<C, Q>(acc2);
-      gemm_from_acc<CM, C, Q>(h, W2t, LD2, g, j, acc2);
+      gemm_f16s<CM, C, Q>(h, W2l, lane, acc2);
     }
 #pragma unroll
     for (int rb = 0; rb < C / 16; ++rb)
@@ -577,7 +693,7 @@ __global__ void __launch_bounds__(64 * NW) k_conv_ln_mlp_mfma(TailArgs a) {
         v4f xn[C / 16][Q];
         ln_acc<C, Q>(acc2, prm + 6 * C + CM, prm + 7 * C + CM, a.heps, g, xn);
         zero_acc<CIN, Q>(hh);
-        gemm_from_acc<C, CIN, Q>(xn, Wht, LDH, g, j, hh);
+        gemm_f16s<C, CIN, Q>(xn, Whl, lane, hh);
       }
 #pragma unroll
       for (int rb = 0; rb < CIN / 16; ++rb)

@@ -139,6 +139,30 @@ def test_conv_ln_mlp_residual_tail(alpha, inplace):
     assert np.abs(got - two).max() <= TOL
 
 
+@pytest.mark.parametrize("scale", [1e-3, 3e5])
+def test_tail_split_fp16_range(scale):
+    """The tail's 1x1 products run as split fp16 on the matrix cores: tiny activations (fp16 low parts
+    below the normal range) keep their accuracy, and activations beyond fp16's range (65504) take the
+    fp32 matrix cores for their k-chunk; both against the fp64 oracle, relative to the output scale."""
+    from conversenet_amd import functional as Fh
+    rng = seeded("tail-range", scale)
+    B, C, Ct, mid, H, W = 1, 64, 128, 128, 16, 20
+    f = lambda *sh, sc=1.0: (rng.standard_normal(sh) * sc).astype(np.float32)
+    t, x = f(B, Ct, H, W, sc=scale), f(B, C, H, W)
+    if scale > 1:
+        t[:, :, :8] *= 1e-5  # mixed: half the pixels in fp16 range, half far beyond it
+    w0, b0 = f(C, Ct, 1, 1, sc=Ct ** -0.5), f(C)
+    lw, lb, w1, b1 = f(C), f(C), f(mid, C, 1, 1, sc=C ** -0.5), f(mid)
+    w2, b2 = f(C, mid, 1, 1, sc=mid ** -0.5), f(C)
+    got = _n(Fh.conv_ln_mlp_residual(_t(t), _t(x), _t(w0), _t(b0), _t(lw), _t(lb), 1e-5, _t(w1), _t(b1), _t(w2),
+                                     _t(b2), None, None))
+    y1 = O.conv1x1(t, w0, b0) + x
+    ref = O.conv1x1(O.gelu(O.conv1x1(O.layernorm_cf(y1, lw, lb, 1e-5), w1, b1)), w2, b2) + y1
+    err = np.abs(got - ref).max()
+    print(f"tail split-fp16 scale {scale:g}: max-abs {err:.3e}, max |ref| {np.abs(ref).max():.3e}")
+    assert err <= max(TOL, 2e-6 * np.abs(ref).max())  # fp32 accumulation at |ref| ~ 1e6: ~1e-6 relative
+
+
 def test_conv_ln_mlp_head_fused():
     """Block tail plus the next block's LN -> 1x1 -> GELU (util_converse.py:278-280) in one kernel."""
     from conversenet_amd import functional as Fh
