@@ -283,74 +283,6 @@ __device__ __forceinline__ int64_t tile_px(int64_t t, int64_t tpb, int Q, int NW
 }
 
 // ------------------------------------------------------------------------------------------------
-// 1x1 conv (+ LN prologue) on MFMA.  Block = NW waves; persistent over pixel tiles.
-// ------------------------------------------------------------------------------------------------
-template <int CIN, int COUT, bool LN, int Q, int NW>
-__global__ void __launch_bounds__(64 * NW) k_conv1x1_mfma(const float* __restrict__ x, int64_t HW, int64_t tpb,
-                                                      int64_t ntiles, const float* __restrict__ W,
-                                                      const float* __restrict__ bias, const float* __restrict__ lw,
-                                                      const float* __restrict__ lb, float eps, int act,
-                                                      const float* residual, const float* __restrict__ res_scale,
-                                                      float* y) {
-  constexpr int LD = COUT + 16;  // (4 ks + g) LD + j + 16 rb: 16 g + j distinct banks
-  __shared__ float Wt[CIN * LD];
-  __shared__ float prm[2 * COUT + 2 * CIN];  // bias, residual scale, LN weight, LN bias
-  stage_wt<COUT, CIN, LD>(W, Wt);
-  stage_vec<COUT>(bias, 0.f, prm);
-  stage_vec<COUT>(res_scale, 1.f, prm + COUT);
-  if (LN) {
-    stage_vec<CIN>(lw, 1.f, prm + 2 * COUT);
-    stage_vec<CIN>(lb, 0.f, prm + 2 * COUT + CIN);
-  }
-  __syncthreads();
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = lane >> 4, j = lane & 15;
-  const uint32_t xoff = (uint32_t)(((int64_t)g * HW + Q * j) * 4);
-  const uint32_t yoff = (uint32_t)(((int64_t)4 * g * HW + Q * j) * 4);
-  for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
-    mem_fence_sched();
-    const int64_t hw = opaque_stride(HW);
-    int64_t b;
-    const int64_t pw = tile_px(t, tpb, Q, NW, wave, &b);
-    const bool inb = pw + Q * j < hw;
-    float xv[CIN / 4][Q];
-    load_tile<CIN, Q>(x + b * CIN * hw + pw, hw, inb, xoff, xv);
-    if (LN) ln_tile<CIN, Q>(xv, g, prm + 2 * COUT, prm + 2 * COUT + CIN, eps);
-    v4f acc[COUT / 16][Q];
-    zero_acc<COUT, Q>(acc);
-    gemm_tile<CIN, COUT, Q>(xv, Wt, LD, g, j, acc);
-    store_tile<COUT, Q>(acc, y + b * COUT * hw + pw, residual ? residual + b * COUT * hw + pw : nullptr, hw, inb,
-                        yoff, g, prm, act, prm + COUT);
-  }
-}
-
-// acc[ob][q] += W[16 ob + j][k] * v[k] over the k-steps kk = 4 rb + r whose B operand is register r of
-// row block rb of v (lane group g supplies channel 16 rb + 4 g + r): the first layer's accumulator
-// layout fed to the next layer.  Wt[k * LD + i] = W[i][k].
-template <int K, int N, int Q>
-__device__ __forceinline__ void gemm_from_acc(const v4f (&v)[K / 16][Q], const float* Wt, int ld, int g, int j,
-                                              v4f (&acc)[N / 16][Q]) {
-  float a[2][N / 16];
-#pragma unroll
-  for (int ob = 0; ob < N / 16; ++ob) a[0][ob] = Wt[(4 * g) * ld + j + 16 * ob];
-#pragma unroll
-  for (int kk = 0; kk < K / 4; ++kk) {
-    const int rb = kk >> 2, r = kk & 3;
-    if (kk + 1 < K / 4) {
-      const int rn = (kk + 1) >> 2, sn = (kk + 1) & 3;
-      const float* wk = Wt + (16 * rn + 4 * g + sn) * ld + j;
-#pragma unroll
-      for (int ob = 0; ob < N / 16; ++ob) a[(kk + 1) & 1][ob] = wk[16 * ob];
-    }
-#pragma unroll
-    for (int ob = 0; ob < N / 16; ++ob)
-#pragma unroll
-      for (int q = 0; q < Q; ++q) acc[ob][q] = mfma4(a[kk & 1][ob], v[rb][q][r], acc[ob][q]);
-    mem_fence_sched();
-  }
-}
-
-// ------------------------------------------------------------------------------------------------
 // fp32 products on the fp16 matrix cores ("split fp16").  Every operand x is split as x = x_h + x_l,
 // x_h = fp16(x) and x_l = fp16(x - x_h), both rounded toward zero (x - x_h is exact in fp32), so
 // |x - x_h - x_l| < 2^-20 |x|; a product is formed as a_l b_h + a_h b_l + a_h b_h (three
@@ -470,79 +402,6 @@ __device__ __forceinline__ void load_acc(const float* w, int64_t hw, bool inb, u
     }
 }
 
-// ConverseBlock conv2 branch: y = x + res_scale * (W2 GELU(W1 LN(x) + b1) + b2)
-template <int C, int CM, int Q, int NW>
-__global__ void __launch_bounds__(64 * NW) k_ln_mlp_mfma(const float* x, int64_t HW, int64_t tpb, int64_t ntiles,
-                                                     const float* __restrict__ lw, const float* __restrict__ lb,
-                                                     float eps, const float* __restrict__ W1,
-                                                     const float* __restrict__ b1, const float* __restrict__ W2,
-                                                     const float* __restrict__ b2,
-                                                     const float* __restrict__ res_scale, float* y) {
-  constexpr int LD1 = CM + 16;  // W1t[k][i], k < C, i < CM; read at (4 ks + g) LD1 + 16 rb + j
-  constexpr int LD2 = C + 4;    // W2t[k][i], k < CM, i < C; read at (16 rb + 4 g + r) LD2 + 16 ob + j
-  __shared__ float W1t[C * LD1];
-  __shared__ float W2t[CM * LD2];
-  __shared__ float prm[CM + 4 * C];  // b1, b2, residual scale, LN weight, LN bias
-  stage_wt<CM, C, LD1>(W1, W1t);
-  stage_wt<C, CM, LD2>(W2, W2t);
-  stage_vec<CM>(b1, 0.f, prm);
-  stage_vec<C>(b2, 0.f, prm + CM);
-  stage_vec<C>(res_scale, 1.f, prm + CM + C);
-  stage_vec<C>(lw, 1.f, prm + CM + 2 * C);
-  stage_vec<C>(lb, 0.f, prm + CM + 3 * C);
-  __syncthreads();
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = lane >> 4, j = lane & 15;
-  const uint32_t xoff = (uint32_t)(((int64_t)g * HW + Q * j) * 4);
-  const uint32_t yoff = (uint32_t)(((int64_t)4 * g * HW + Q * j) * 4);
-  for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
-    mem_fence_sched();
-    const int64_t hw = opaque_stride(HW);
-    int64_t b;
-    const int64_t pw = tile_px(t, tpb, Q, NW, wave, &b);
-    const bool inb = pw + Q * j < hw;
-    const float* xw = x + b * C * hw + pw;
-    float xv[C / 4][Q];
-    load_tile<C, Q>(xw, hw, inb, xoff, xv);
-    ln_tile<C, Q>(xv, g, prm + CM + 2 * C, prm + CM + 3 * C, eps);
-    v4f h[CM / 16][Q];
-    zero_acc<CM, Q>(h);
-    gemm_tile<C, CM, Q>(xv, W1t, LD1, g, j, h);
-    // bias + GELU on the hidden activations (channel 16 rb + 4 g + r)
-#pragma unroll
-    for (int rb = 0; rb < CM / 16; ++rb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float bo = prm[16 * rb + 4 * g + r];
-#pragma unroll
-        for (int q = 0; q < Q; ++q) h[rb][q][r] = gelu_f(h[rb][q][r] + bo);
-      }
-    v4f acc[C / 16][Q];
-    zero_acc<C, Q>(acc);
-    gemm_from_acc<CM, C, Q>(h, W2t, LD2, g, j, acc);  // k-step 4 rb + r: hidden channel 16 rb + 4 g + r
-    store_tile<C, Q>(acc, y + b * C * hw + pw, xw, hw, inb, yoff, g, prm + CM, CVN_ACT_NONE, prm + CM + C);
-  }
-}
-
-// ConverseBlock tail in one kernel: y' = x + s1 (W0 t + b0) (the first branch's last 1x1 and its
-// residual), then  out = y' + s2 (W2 GELU(W1 LN(y') + b1) + b2)  (the second branch).  y' stays in
-// registers in the accumulator layout (lane group g holds channels 16 rb + 4 g + r of pixel block
-// j), which is the B-operand layout of the next layer's k-steps, so neither y' nor LN(y') reaches
-// memory.  out may alias x: every pixel's x is read by the lanes that later write it.  With HEAD,
-// the next block's first layer follows on the same registers: th = GELU(Wh LNh(out) + bh)
-// (CIN channels), so the next block does not read `out` again before its Converse2D.
-struct TailArgs {
-  const float* t;  // (B, CIN, HW)
-  const float* x;  // (B, C, HW)
-  int64_t HW, tpb, ntiles;
-  const float *W0, *b0, *s1, *lw, *lb, *W1, *b1, *W2, *b2, *s2;
-  float eps;
-  float* y;  // (B, C, HW)
-  const float *hlw, *hlb, *Wh, *bh;  // HEAD: next block's LayerNorm and 1x1 (CIN x C)
-  float heps;
-  float* th;  // HEAD: (B, CIN, HW)
-};
-
 // LayerNorm over the C channels of v, held in the accumulator layout (16 per lane for C = 64; the
 // other lane groups of the same pixel block are lanes j + 16, j + 32, j + 48).
 template <int C, int Q>
@@ -579,6 +438,130 @@ __device__ __forceinline__ void ln_acc(const v4f (&v)[C / 16][Q], const float* w
       }
   }
 }
+
+// ------------------------------------------------------------------------------------------------
+// 1x1 conv (+ LN prologue) on MFMA.  Block = NW waves; persistent over pixel tiles.
+// ------------------------------------------------------------------------------------------------
+template <int CIN, int COUT, bool LN, int Q, int NW, bool F16S>
+__global__ void __launch_bounds__(64 * NW) k_conv1x1_mfma(const float* __restrict__ x, int64_t HW, int64_t tpb,
+                                                      int64_t ntiles, const float* __restrict__ W,
+                                                      const float* __restrict__ bias, const float* __restrict__ lw,
+                                                      const float* __restrict__ lb, float eps, int act,
+                                                      const float* residual, const float* __restrict__ res_scale,
+                                                      float* y) {
+  // F16S: split-fp16 products (whole 32-channel input chunks), else fp32 MFMAs
+  constexpr int LD = COUT + 16;  // (4 ks + g) LD + j + 16 rb: 16 g + j distinct banks
+  __shared__ __align__(16) float Wt[F16S ? COUT * CIN : CIN * LD];
+  __shared__ float prm[2 * COUT + 2 * CIN];  // bias, residual scale, LN weight, LN bias
+  if constexpr (F16S) stage_f16s<COUT, CIN>(W, (_Float16*)Wt);
+  else stage_wt<COUT, CIN, LD>(W, Wt);
+  stage_vec<COUT>(bias, 0.f, prm);
+  stage_vec<COUT>(res_scale, 1.f, prm + COUT);
+  if (LN) {
+    stage_vec<CIN>(lw, 1.f, prm + 2 * COUT);
+    stage_vec<CIN>(lb, 0.f, prm + 2 * COUT + CIN);
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, j = lane & 15;
+  const uint32_t xoff = (uint32_t)(((int64_t)g * HW + Q * j) * 4);
+  const uint32_t yoff = (uint32_t)(((int64_t)4 * g * HW + Q * j) * 4);
+  for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+    mem_fence_sched();
+    const int64_t hw = opaque_stride(HW);
+    int64_t b;
+    const int64_t pw = tile_px(t, tpb, Q, NW, wave, &b);
+    const bool inb = pw + Q * j < hw;
+    v4f acc[COUT / 16][Q];
+    zero_acc<COUT, Q>(acc);
+    if constexpr (F16S) {
+      v4f xv[CIN / 16][Q];
+      load_acc<CIN, Q>(x + b * CIN * hw + pw, hw, inb, yoff, xv);
+      if (LN) ln_acc<CIN, Q>(xv, prm + 2 * COUT, prm + 2 * COUT + CIN, eps, g, xv);
+      gemm_f16s<CIN, COUT, Q>(xv, (const _Float16*)Wt, lane, acc);
+    } else {
+      float xv[CIN / 4][Q];
+      load_tile<CIN, Q>(x + b * CIN * hw + pw, hw, inb, xoff, xv);
+      if (LN) ln_tile<CIN, Q>(xv, g, prm + 2 * COUT, prm + 2 * COUT + CIN, eps);
+      gemm_tile<CIN, COUT, Q>(xv, Wt, LD, g, j, acc);
+    }
+    store_tile<COUT, Q>(acc, y + b * COUT * hw + pw, residual ? residual + b * COUT * hw + pw : nullptr, hw, inb,
+                        yoff, g, prm, act, prm + COUT);
+  }
+}
+
+// ConverseBlock conv2 branch: y = x + res_scale * (W2 GELU(W1 LN(x) + b1) + b2)
+template <int C, int CM, int Q, int NW>
+__global__ void __launch_bounds__(64 * NW) k_ln_mlp_mfma(const float* x, int64_t HW, int64_t tpb, int64_t ntiles,
+                                                     const float* __restrict__ lw, const float* __restrict__ lb,
+                                                     float eps, const float* __restrict__ W1,
+                                                     const float* __restrict__ b1, const float* __restrict__ W2,
+                                                     const float* __restrict__ b2,
+                                                     const float* __restrict__ res_scale, float* y) {
+  static_assert(C % 32 == 0 && CM % 32 == 0, "split-fp16 GEMM chunks");
+  __shared__ __align__(16) _Float16 W1l[2 * CM * C];  // stage_f16s layouts
+  __shared__ __align__(16) _Float16 W2l[2 * C * CM];
+  __shared__ float prm[CM + 4 * C];  // b1, b2, residual scale, LN weight, LN bias
+  stage_f16s<CM, C>(W1, W1l);
+  stage_f16s<C, CM>(W2, W2l);
+  stage_vec<CM>(b1, 0.f, prm);
+  stage_vec<C>(b2, 0.f, prm + CM);
+  stage_vec<C>(res_scale, 1.f, prm + CM + C);
+  stage_vec<C>(lw, 1.f, prm + CM + 2 * C);
+  stage_vec<C>(lb, 0.f, prm + CM + 3 * C);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, j = lane & 15;
+  const uint32_t yoff = (uint32_t)(((int64_t)4 * g * HW + Q * j) * 4);
+  for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+    mem_fence_sched();
+    const int64_t hw = opaque_stride(HW);
+    int64_t b;
+    const int64_t pw = tile_px(t, tpb, Q, NW, wave, &b);
+    const bool inb = pw + Q * j < hw;
+    const float* xw = x + b * C * hw + pw;
+    v4f h[CM / 16][Q];
+    {
+      v4f xv[C / 16][Q];
+      load_acc<C, Q>(xw, hw, inb, yoff, xv);
+      ln_acc<C, Q>(xv, prm + CM + 2 * C, prm + CM + 3 * C, eps, g, xv);
+      zero_acc<CM, Q>(h);
+      gemm_f16s<C, CM, Q>(xv, W1l, lane, h);
+    }
+    // bias + GELU on the hidden activations (channel 16 rb + 4 g + r)
+#pragma unroll
+    for (int rb = 0; rb < CM / 16; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float bo = prm[16 * rb + 4 * g + r];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) h[rb][q][r] = gelu_f(h[rb][q][r] + bo);
+      }
+    v4f acc[C / 16][Q];
+    zero_acc<C, Q>(acc);
+    gemm_f16s<CM, C, Q>(h, W2l, lane, acc);
+    store_tile<C, Q>(acc, y + b * C * hw + pw, xw, hw, inb, yoff, g, prm + CM, CVN_ACT_NONE, prm + CM + C);
+  }
+}
+
+// ConverseBlock tail in one kernel: y' = x + s1 (W0 t + b0) (the first branch's last 1x1 and its
+// residual), then  out = y' + s2 (W2 GELU(W1 LN(y') + b1) + b2)  (the second branch).  y' stays in
+// registers in the accumulator layout (lane group g holds channels 16 rb + 4 g + r of pixel block
+// j), which is the B-operand layout of the next layer's k-steps, so neither y' nor LN(y') reaches
+// memory.  out may alias x: every pixel's x is read by the lanes that later write it.  With HEAD,
+// the next block's first layer follows on the same registers: th = GELU(Wh LNh(out) + bh)
+// (CIN channels), so the next block does not read `out` again before its Converse2D.
+struct TailArgs {
+  const float* t;  // (B, CIN, HW)
+  const float* x;  // (B, C, HW)
+  int64_t HW, tpb, ntiles;
+  const float *W0, *b0, *s1, *lw, *lb, *W1, *b1, *W2, *b2, *s2;
+  float eps;
+  float* y;  // (B, C, HW)
+  const float *hlw, *hlb, *Wh, *bh;  // HEAD: next block's LayerNorm and 1x1 (CIN x C)
+  float heps;
+  float* th;  // HEAD: (B, CIN, HW)
+};
 
 // Stores an accumulator-layout tile (channel 16 rb + 4 g + r, Q consecutive pixels per lane).
 template <int N, int Q>
@@ -760,11 +743,10 @@ constexpr int64_t kMaxMfmaHW = (int64_t)1 << 26;
 // spills.
 template <int CIN, int COUT, bool LN>
 struct ConvTile {
-  static constexpr int Q = (CIN + COUT > 192 || (LN && CIN + COUT >= 192)) ? 1 : 2, NW = 16;
-};
-template <>
-struct ConvTile<128, 64, false> {
-  static constexpr int Q = 2, NW = 16;
+  // split-fp16 products for whole 32-channel input chunks (not at 128 x 128, where they would spill)
+  static constexpr bool F16S = CIN % 32 == 0 && CIN + COUT < 256;
+  static constexpr int Q = F16S ? (CIN + COUT >= 192 ? 1 : 2) : (CIN + COUT > 192 || (LN && CIN + COUT >= 192)) ? 1 : 2;
+  static constexpr int NW = 16;
 };
 template <int C, int CM>
 struct MlpTile {
@@ -795,7 +777,7 @@ int launch_mfma(const float* x, int64_t B, int64_t HW, const float* W, const flo
                 hipStream_t st) {
   constexpr int Q = ConvTile<CIN, COUT, LN>::Q, NW = ConvTile<CIN, COUT, LN>::NW;
   const int64_t tpb = (HW + 16 * NW * Q - 1) / (16 * NW * Q), ntiles = B * tpb;
-  auto kern = k_conv1x1_mfma<CIN, COUT, LN, Q, NW>;
+  auto kern = k_conv1x1_mfma<CIN, COUT, LN, Q, NW, ConvTile<CIN, COUT, LN>::F16S>;
   hipLaunchKernelGGL(kern, dim3(persistent_grid(kern, 64 * NW, ntiles)), dim3(64 * NW), 0, st, x, HW, tpb, ntiles,
                      W, bias, lw, lb, eps, act, residual, res_scale, y);
   return check_launch("1x1 conv");
