@@ -170,6 +170,22 @@ def run_cpu_baseline(args, case="cfg3"):
 # ------------------------------------------------------------------------------------------------
 # GPU measurements
 # ------------------------------------------------------------------------------------------------
+def spin_up(torch, fn, seconds):
+    """Runs fn back to back for `seconds` of wall time before anything is measured.  From idle the GPU
+    needs a fraction of a second of sustained load to reach its steady clock: measured on the box, the
+    cfg3 forward went from 0.225 to 0.188 ms per call over its first ~0.5 s of back-to-back calls, so a
+    run of a few dozen calls straight after start-up times the clock ramp, not the kernel.  Returns the
+    number of calls made."""
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            fn()
+        n += 20
+        torch.cuda.synchronize()
+    return n
+
+
 def time_events(torch, fn, iters):
     """Average duration per call from HIP events on the current stream (the library launches on it)."""
     st = torch.cuda.current_stream()
@@ -501,6 +517,7 @@ def only_kernel(torch, Fh, args, dev, x, step):
                                              head=(lw, lb, 1e-5, w1, b1))
     else:
         raise SystemExit(f"unknown --only {args.only}")
+    spin_up(torch, fn, args.spinup)
     for _ in range(args.warmup):
         fn()
     torch.cuda.synchronize()
@@ -517,6 +534,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--spinup", type=float, default=1.5,
+                    help="seconds of back-to-back calls before the warmup steps (GPU clock ramp); 0 for PMC runs")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-model", action="store_true")
     ap.add_argument("--cpu-worker", action="store_true")
@@ -557,6 +576,7 @@ def main():
     if args.only:
         return only_kernel(torch, Fh, args, dev, x, step)
 
+    spun = spin_up(torch, step, args.spinup)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -639,6 +659,9 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "wall_ms_per_step": wall * 1e3,
+        "spinup": {"seconds": args.spinup, "calls": spun,
+                   "note": "back-to-back steps before the warmup steps, so the timed steps run at the GPU's "
+                           "steady clock"},
         "extra": extra,
         "host": platform.node(),
     }

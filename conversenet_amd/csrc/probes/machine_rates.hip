@@ -72,6 +72,7 @@ template <int W, bool WR>
 __global__ void k_lds(float* out, int iters, int stride) {
   extern __shared__ __align__(16) float2 L2[];
   float* L = (float*)L2;
+  float4* L4 = (float4*)L2;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int i = tid; i < 16384; i += blockDim.x) L[i] = i;
   __syncthreads();
@@ -82,11 +83,15 @@ __global__ void k_lds(float* out, int iters, int stride) {
     for (int r = 0; r < 8; ++r) {
       const int idx = (base + lane * stride + r * 1024) % (65536 / W);
       if constexpr (WR) {
-        if constexpr (W == 8) L2[idx] = make_float2(acc, acc);
+        if constexpr (W == 16) L4[idx] = make_float4(acc, acc, acc, acc);
+        else if constexpr (W == 8) L2[idx] = make_float2(acc, acc);
         else L[idx] = acc;
         acc += 1.f;
       } else {
-        if constexpr (W == 8) {
+        if constexpr (W == 16) {
+          const float4 v = L4[idx];
+          acc += v.x * v.y + v.z * v.w;
+        } else if constexpr (W == 8) {
           const float2 v = L2[idx];
           acc += v.x * v.y;
         } else {
@@ -140,14 +145,14 @@ int main() {
     printf("  %-20s %.3f ms\n", names[m], ms);
   }
   printf("LDS, ns per wave instruction per CU (1024 threads, 4 blocks per CU), lane stride in words:\n");
-  printf("  stride  read32  read64  write32  write64\n");
+  printf("  stride  read32  read64  write32  write64  read128  write128\n");
   for (int s : {1, 2, 3, 4, 8, 16, 32, 33, 267}) {
     auto run = [&](auto kern) {
       const float ms = timeit([&] { hipLaunchKernelGGL(kern, dim3(1024), dim3(1024), 65536, 0, out, iters, s); });
       return ms * 1e6 / (4.0 * 16 * iters * 8);
     };
-    printf("  %6d  %6.3f  %6.3f  %7.3f  %7.3f\n", s, run(k_lds<4, false>), run(k_lds<8, false>), run(k_lds<4, true>),
-           run(k_lds<8, true>));
+    printf("  %6d  %6.3f  %6.3f  %7.3f  %7.3f  %7.3f  %8.3f\n", s, run(k_lds<4, false>), run(k_lds<8, false>),
+           run(k_lds<4, true>), run(k_lds<8, true>), run(k_lds<16, false>), run(k_lds<16, true>));
   }
   printf("status: %s\n", hipGetErrorString(hipGetLastError()));
   return 0;
