@@ -90,9 +90,11 @@ struct FusedPlan {
   static constexpr int PARK = (SLOTS + kFT - 1) / kFT;  // rounds of kFT slots parked per thread
   static constexpr int SLOTS_PAD = PARK * kFT;           // group buffer padded to whole rounds
   // the first PARK_LDS rounds are parked in the LDS space left over next to the group buffer
-  // LDS tables: radix-2 twiddles by row position (NH + 2 float2), int16 pa, pb, pos, colsrc, and a
-  // byte per row-pair position saying whether it holds the odd row's bins
-  static constexpr int TAB_BYTES = (NH + 2) * 8 + (2 * NQ + 2 * M) * 2 + RS;
+  // LDS tables: radix-2 twiddles by row position (NH + 2 float2), int16 pa, pb, pos, a byte per
+  // row-pair position saying whether it holds the odd row's bins (these four are compile-time
+  // constants, copied from FusedTabs as one 16-byte-padded block of CONST_BYTES), then int16 colsrc
+  static constexpr int CONST_BYTES = ((NH + 2) * 8 + (2 * NQ + M) * 2 + RS + 16) / 16 * 16;
+  static constexpr int TAB_BYTES = CONST_BYTES + 2 * M;
   static constexpr int PARK_LDS_MAX = (163840 - SLOTS_PAD * 8 - TAB_BYTES - 64) / (kFT * 8);
   static constexpr int PARK_LDS = PARK_LDS_MAX < PARK ? PARK_LDS_MAX : PARK;
   static_assert(R1 * R2 * R3 == M && M % 2 == 0 && NP % 2 == 1, "plan");
@@ -117,6 +119,33 @@ struct FusedPlan {
   }
   static __host__ __device__ constexpr int rfpos(int k) { return (k % Q1) * CS1 + (k % Q2) * CS2 + (k % 2); }
 };
+
+// The fused kernel's plane-independent LDS tables, evaluated at compile time (twiddles in double,
+// rounded once) and copied into LDS by each workgroup: radix-2 twiddles exp(-2 pi i k / N) at row
+// position rfpos(k) (two zero entries past NH for the padding slots), the half-spectrum slot
+// positions pa, pb, the in-row positions pos_in, and the odd-row flag per row-pair position.
+template <class P>
+struct alignas(16) FusedTabs {
+  float w[2 * (P::NH + 2)];
+  short pa[P::NQ], pb[P::NQ], pos[P::M];
+  unsigned char isb[P::RS];
+  unsigned char pad[P::CONST_BYTES - (2 * (P::NH + 2)) * 4 - (2 * P::NQ + P::M) * 2 - P::RS];
+  constexpr FusedTabs() : w(), pa(), pb(), pos(), isb(), pad() {
+    for (int k = 0; k < P::NH; ++k) {
+      const CosSin cs = cos_sin_turn(k, P::N);
+      w[2 * P::rfpos(k)] = (float)cs.c;
+      w[2 * P::rfpos(k) + 1] = (float)-cs.s;
+    }
+    for (int q = 0; q < P::NQ; ++q) {
+      pa[q] = (short)P::pa(q);
+      pb[q] = (short)P::pb(q);
+      isb[P::pb(q)] = 1;
+    }
+    for (int j = 0; j < P::M; ++j) pos[j] = (short)P::pos_in(j);
+  }
+};
+template <class P>
+__device__ const FusedTabs<P> kFusedTabs = FusedTabs<P>();
 
 // Work item w of a row pass -> (row pair t, index i < PER within the row pair).  Row pairs run fastest
 // across the lanes of a wave: with the odd row-pair stride RS, the 64 row pairs of a wave then fall on
@@ -514,8 +543,8 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
   short* pa = (short*)(wtab + P::NH + 2);
   short* pb = pa + P::NQ;
   short* pos = pb + P::NQ;
-  short* colsrc = pos + P::M;
-  unsigned char* isb = (unsigned char*)(colsrc + P::M);  // 1 where a position holds the odd row
+  unsigned char* isb = (unsigned char*)(pos + P::M);  // 1 where a position holds the odd row
+  short* colsrc = (short*)((char*)wtab + P::CONST_BYTES);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t plane = fused_plane(blockIdx.x, a);
@@ -524,22 +553,12 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + plane * (int64_t)a.H * a.W, plane_bytes);
   const __amdgpu_buffer_rsrc_t orsrc = make_rsrc(a.out + plane * (int64_t)a.H * a.W, plane_bytes);
   const __amdgpu_buffer_rsrc_t t4r = make_rsrc(a.tab4 + cp * P::SLOTS, P::SLOTS * 16u);
-  for (int p = tid; p < P::RS; p += kFT) isb[p] = 0;  // spare positions: any in-range value
-  for (int k = tid; k < P::NH + 2; k += kFT) {
-    double sn = 0.0, cs = 0.0;
-    if (k < P::NH) sincospi(-2.0 * (double)k / (double)P::N, &sn, &cs);
-    wtab[k < P::NH ? P::rfpos(k) : k] = make_float2((float)cs, (float)sn);
+  {
+    const v4u32_t* src = (const v4u32_t*)&kFusedTabs<P>;
+    v4u32_t* dst = (v4u32_t*)wtab;
+    for (int i = tid; i < P::CONST_BYTES / 16; i += kFT) dst[i] = src[i];
   }
-  lds_barrier();
-  for (int q = tid; q < P::NQ; q += kFT) {
-    pa[q] = P::pa(q);
-    pb[q] = P::pb(q);
-    isb[P::pb(q)] = 1;
-  }
-  for (int j = tid; j < P::M; j += kFT) {
-    pos[j] = P::pos_in(j);
-    colsrc[j] = fpad_src(j, a.W, a.pad, a.mode);
-  }
+  for (int j = tid; j < P::M; j += kFT) colsrc[j] = fpad_src(j, a.W, a.pad, a.mode);
   int lp[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) lp[c] = P::pos_in(min(a.pad + 4 * lane + c, P::M - 1));

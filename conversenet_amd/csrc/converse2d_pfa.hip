@@ -70,26 +70,6 @@ struct Maps {
 };
 constexpr Maps kM{};
 
-// cos and sin of 2 pi m / n by Taylor series in double at compile time (|angle| <= pi after
-// reduction; 40 terms leave a truncation error far below double rounding).
-struct CosSin {
-  double c, s;
-};
-constexpr CosSin cos_sin_turn(int m, int n) {
-  m %= n;
-  if (2 * m >= n) m -= n;
-  const double x = 2.0 * 3.14159265358979323846 * m / n;
-  double c = 0.0, s = 0.0, term = 1.0;
-  for (int k = 0; k < 40; ++k) {
-    const int r = k & 3;
-    if (r == 0) c += term;
-    if (r == 1) s += term;
-    if (r == 2) c -= term;
-    if (r == 3) s -= term;
-    term = term * x / (k + 1);
-  }
-  return CosSin{c, s};
-}
 // Rader tables: b_q = W67^(2^-q), bf = FFT66(b) / 66 (forward) and bi = FFT66(conj b) / 66 (inverse),
 // natural bin order, evaluated in double at compile time and rounded once.  Their indices are
 // compile-time constants in dft67_pair, so the values become instruction literals.

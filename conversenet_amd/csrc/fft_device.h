@@ -61,6 +61,32 @@ __device__ __forceinline__ int operator/(int a, FastDiv f) {
   return f.d > 1 ? (int)__umulhi((uint32_t)a, f.m) : a;
 }
 
+// cos and sin of 2 pi m / n by Taylor series in double at compile time (|angle| <= pi after
+// reduction; 40 terms leave a truncation error far below double rounding).
+struct CosSin {
+  double c, s;
+};
+constexpr CosSin cos_sin_turn(int m, int n) {
+  m %= n;
+  if (m < 0) m += n;
+  if (4 * m % n == 0) {  // whole quarter turns exactly
+    const int q = 4 * m / n;
+    return CosSin{q == 0 ? 1.0 : q == 2 ? -1.0 : 0.0, q == 1 ? 1.0 : q == 3 ? -1.0 : 0.0};
+  }
+  if (2 * m >= n) m -= n;
+  const double x = 2.0 * 3.14159265358979323846 * m / n;
+  double c = 0.0, s = 0.0, term = 1.0;
+  for (int k = 0; k < 40; ++k) {
+    const int r = k & 3;
+    if (r == 0) c += term;
+    if (r == 1) s += term;
+    if (r == 2) c -= term;
+    if (r == 3) s -= term;
+    term = term * x / (k + 1);
+  }
+  return CosSin{c, s};
+}
+
 // cos / sin of 2 pi m / R, m in [0, R), for the odd prime radices (values computed in double and
 // rounded to float).
 template <int R> struct Roots;
