@@ -23,6 +23,7 @@
 // Each group then runs the inverse column FFT, repacks the row pairs, runs the inverse row FFT
 // (real parts = row a, imaginary parts = row b) and stores the cropped rows.
 #include <math.h>
+#include <stddef.h>
 
 #include "cvn_common.h"
 
@@ -93,7 +94,10 @@ struct FusedPlan {
   // LDS tables: radix-2 twiddles by row position (NH + 2 float2), int16 pa, pb, pos, a byte per
   // row-pair position saying whether it holds the odd row's bins (these four are compile-time
   // constants, copied from FusedTabs as one 16-byte-padded block of CONST_BYTES), then int16 colsrc
-  static constexpr int CONST_BYTES = ((NH + 2) * 8 + (2 * NQ + M) * 2 + RS + 16) / 16 * 16;
+  static constexpr bool kCT = false;  // prime-factor passes, no twiddles
+  static constexpr int TWN = 1;        // row twiddle entries (none used)
+  static constexpr int TAB_TW_OFF = ((NH + 2) * 8 + (2 * NQ + M) * 2 + RS + 3) / 4 * 4;
+  static constexpr int CONST_BYTES = (TAB_TW_OFF + 8 * TWN + 16) / 16 * 16;
   static constexpr int TAB_BYTES = CONST_BYTES + 2 * M;
   static constexpr int PARK_LDS_MAX = (163840 - SLOTS_PAD * 8 - TAB_BYTES - 64) / (kFT * 8);
   static constexpr int PARK_LDS = PARK_LDS_MAX < PARK ? PARK_LDS_MAX : PARK;
@@ -118,6 +122,46 @@ struct FusedPlan {
            ((g * mod_inv((NH / 2) % 2, 2)) % 2);
   }
   static __host__ __device__ constexpr int rfpos(int k) { return (k % Q1) * CS1 + (k % Q2) * CS2 + (k % 2); }
+  // plane row of row position rp of group G (the inverse of rpos_in)
+  static __host__ __device__ constexpr int plane_row(int rp, int G) {
+    return 2 * (((rp / CS1) * (NH / Q1) + ((rp % CS1) >> 1) * (NH / Q2) + (rp & 1) * (NH / 2)) % NH) + G;
+  }
+};
+
+// Cooley-Tukey plan for square planes of side M = A B (a power of two here: 256 = 16 x 16).
+// Rows: sample n = B n1 + n2 sits at position A n2 + n1; pass A (contiguous) takes the A-point DFT
+// over n1 and multiplies output k1 by W_M^(n2 k1); pass B (stride A) takes the B-point DFT over n2,
+// which leaves frequency v at position v.  Columns of a group (NH = M / 2 rows, row pairs of group
+// rows t and t + NP): the radix-2 step across the pair (k1), W_NH^(t k1), then NP = Q1 Q2 points over
+// the row pairs t = t2 + Q2 m as Q1-point DFTs over m with W_NP^(t2 k') (column pass A) and Q2-point
+// DFTs over t2 (column pass B), which leave frequency k = 2 (k' + Q1 k'') + k1 at row pair
+// Q2 k' + k'' (Q1 = Q2).  The inverse runs the same steps backwards with conjugate twiddles.
+template <int A_, int B_, int Q_, int RSX_>
+struct CtPlan {
+  static constexpr bool kCT = true;
+  static constexpr int A = A_, B = B_, M = A_ * B_, N = M;
+  static constexpr int NH = N / 2, NP = NH / 2, Q1 = Q_, Q2 = Q_;
+  static constexpr int RS = M + 2 + RSX_;
+  static constexpr int SLOTS = NP * RS;
+  static constexpr int NQ = M / 2 + 1;
+  static constexpr int PARK = (SLOTS + kFT - 1) / kFT;
+  static constexpr int SLOTS_PAD = PARK * kFT;
+  static constexpr int TWN = M;  // row twiddles W_M^j, j < M (the column twiddles are W_M^(2j), W_M^(4j))
+  static constexpr int TAB_TW_OFF = ((NH + 2) * 8 + (2 * NQ + M) * 2 + RS + 3) / 4 * 4;
+  static constexpr int CONST_BYTES = (TAB_TW_OFF + 8 * TWN + 16) / 16 * 16;
+  static constexpr int TAB_BYTES = CONST_BYTES + 2 * M;
+  static constexpr int PARK_LDS_MAX = (163840 - SLOTS_PAD * 8 - TAB_BYTES - 64) / (kFT * 8);
+  static constexpr int PARK_LDS = PARK_LDS_MAX < PARK ? PARK_LDS_MAX : PARK;
+  static_assert(NP == Q1 * Q2 && M % 4 == 0 && (RS & 1) == 1 && 4 * (Q1 - 1) * (Q2 - 1) < M, "plan");
+  static constexpr size_t LDS_BYTES = (size_t)SLOTS_PAD * 8 + (size_t)PARK_LDS * kFT * 8 + TAB_BYTES;
+  static __host__ __device__ constexpr int pos_in(int n) { return A * (n % B) + n / B; }
+  static __host__ __device__ constexpr int fpos(int v) { return v; }
+  static __host__ __device__ constexpr int pa(int q) { return fpos(q); }
+  static __host__ __device__ constexpr int pb(int q) { return q == 0 ? M : (q == M / 2 ? M + 1 : fpos(M - q)); }
+  static __host__ __device__ constexpr int rfpos(int k) {
+    return 2 * (Q2 * ((k >> 1) % Q1) + (k >> 1) / Q1) + (k & 1);
+  }
+  static __host__ __device__ constexpr int plane_row(int rp, int G) { return 2 * ((rp >> 1) + NP * (rp & 1)) + G; }
 };
 
 // The fused kernel's plane-independent LDS tables, evaluated at compile time (twiddles in double,
@@ -129,8 +173,16 @@ struct alignas(16) FusedTabs {
   float w[2 * (P::NH + 2)];
   short pa[P::NQ], pb[P::NQ], pos[P::M];
   unsigned char isb[P::RS];
-  unsigned char pad[P::CONST_BYTES - (2 * (P::NH + 2)) * 4 - (2 * P::NQ + P::M) * 2 - P::RS];
-  constexpr FusedTabs() : w(), pa(), pb(), pos(), isb(), pad() {
+  float tw[2 * P::TWN];  // Cooley-Tukey plans: W_M^j (at byte offset P::TAB_TW_OFF)
+  unsigned char pad[P::CONST_BYTES - P::TAB_TW_OFF - 8 * P::TWN];
+  constexpr FusedTabs() : w(), pa(), pb(), pos(), isb(), tw(), pad() {
+    if constexpr (P::kCT) {
+      for (int j = 0; j < P::TWN; ++j) {
+        const CosSin cs = cos_sin_turn(j, P::M);
+        tw[2 * j] = (float)cs.c;
+        tw[2 * j + 1] = (float)-cs.s;
+      }
+    }
     for (int k = 0; k < P::NH; ++k) {
       const CosSin cs = cos_sin_turn(k, P::N);
       w[2 * P::rfpos(k)] = (float)cs.c;
@@ -146,6 +198,18 @@ struct alignas(16) FusedTabs {
 };
 template <class P>
 __device__ const FusedTabs<P> kFusedTabs = FusedTabs<P>();
+template <class P>
+constexpr bool tabs_layout_ok() {
+  return sizeof(FusedTabs<P>) == (size_t)P::CONST_BYTES && offsetof(FusedTabs<P>, tw) == (size_t)P::TAB_TW_OFF &&
+         offsetof(FusedTabs<P>, pa) == (size_t)(P::NH + 2) * 8;
+}
+
+// LDS address of the Cooley-Tukey twiddle table W_M^j: after the group buffer, the parked rounds and
+// the table block's first TAB_TW_OFF bytes (the layout k_converse2d_fused sets up).
+template <class P>
+__device__ __forceinline__ const float2* ct_tw(const float2* buf) {
+  return (const float2*)((const char*)buf + (size_t)P::SLOTS_PAD * 8 + (size_t)P::PARK_LDS * kFT * 8 + P::TAB_TW_OFF);
+}
 
 // Work item w of a row pass -> (row pair t, index i < PER within the row pair).  Row pairs run fastest
 // across the lanes of a wave: with the odd row-pair stride RS, the 64 row pairs of a wave then fall on
@@ -156,32 +220,80 @@ __device__ const FusedTabs<P> kFusedTabs = FusedTabs<P>();
 template <class P, int PER>
 __device__ __forceinline__ void row_item(int w, int& t, int& i) {
   constexpr int T0 = P::NP / 64 * 64, RT = P::NP - T0;
-  if (T0 > 0 && w < T0 * PER) {
+  if (RT == 0 || (T0 > 0 && w < T0 * PER)) {
     const int blk = (w >> 6) / PER;
     i = (w >> 6) - blk * PER;
     t = 64 * blk + (w & 63);
   } else {
     const int v = w - T0 * PER;
-    i = v / RT;
+    i = v / (RT > 0 ? RT : 1);
     t = T0 + (v - i * RT);
   }
 }
 
-// Row pass A: radix R3 along the contiguous axis (positions base + m, m < R3).
+// u[m] *= W_M^(i m) (conjugated for the inverse), the table read in two halves behind compiler fences
+// so that at most half of the twiddles are held in registers at a time.
+template <int A, bool INV>
+__device__ __forceinline__ void ct_row_tw(float2 (&u)[A], const float2* tw, int i) {
+  if (!INV) asm volatile("" ::: "memory");
+#pragma unroll
+  for (int m = 1; m < A / 2; ++m) u[m] = cmul(u[m], INV ? cconj(tw[i * m]) : tw[i * m]);
+#pragma unroll
+  for (int m = A / 2; m < A; ++m) u[m] = cmul(u[m], INV ? cconj(tw[i * m]) : tw[i * m]);
+}
+
+// Row pass A: radix R3 along the contiguous axis (positions base + m, m < R3).  Cooley-Tukey plans:
+// the A-point DFT over positions A i + m with the twiddle W_M^(i m) on its outputs (forward) or
+// inputs (inverse); i is wave-uniform (whole blocks of 64 row pairs), so the twiddle reads broadcast.
 template <class P, bool INV>
 __device__ __forceinline__ void row_pass_a(float2* buf, int tid) {
-  constexpr int R = P::R3, PER = P::M / R;
+  if constexpr (P::kCT) {
+    constexpr int A = P::A, PER = P::B;
+    const float2* tw = ct_tw<P>(buf);
 #pragma unroll 1
-  for (int w = tid; w < P::NP * PER; w += kFT) {
-    int t, i;
-    row_item<P, PER>(w, t, i);
-    dft_odd_mem<R, 1, INV>(buf + t * P::RS + i * R);
+    for (int w = tid; w < P::NP * PER; w += kFT) {
+      int t, i;
+      row_item<P, PER>(w, t, i);
+      float2* b = buf + t * P::RS + i * A;
+      float2 u[A];
+#pragma unroll
+      for (int m = 0; m < A; ++m) u[m] = b[m];
+      if (INV) ct_row_tw<A, true>(u, tw, i);
+      Dft<A, INV>::run(u);
+      if (!INV) ct_row_tw<A, false>(u, tw, i);
+#pragma unroll
+      for (int m = 0; m < A; ++m) b[m] = u[m];
+    }
+  } else {
+    constexpr int R = P::R3, PER = P::M / R;
+#pragma unroll 1
+    for (int w = tid; w < P::NP * PER; w += kFT) {
+      int t, i;
+      row_item<P, PER>(w, t, i);
+      dft_odd_mem<R, 1, INV>(buf + t * P::RS + i * R);
+    }
   }
 }
 
 // Row pass B: the R1 x R2 prime-factor sub-grid (strides ST1, ST2) in registers, base = n3.
 template <class P, bool INV>
 __device__ __forceinline__ void row_pass_b(float2* buf, int tid) {
+  if constexpr (P::kCT) {  // the B-point DFT over positions A m + k1, m < B
+    constexpr int A = P::A, B = P::B;
+#pragma unroll 1
+    for (int w = tid; w < P::NP * A; w += kFT) {
+      int t, k1;
+      row_item<P, A>(w, t, k1);
+      float2* b = buf + t * P::RS + k1;
+      float2 u[B];
+#pragma unroll
+      for (int m = 0; m < B; ++m) u[m] = b[m * A];
+      Dft<B, INV>::run(u);
+#pragma unroll
+      for (int m = 0; m < B; ++m) b[m * A] = u[m];
+    }
+    return;
+  } else {
   constexpr int R1 = P::R1, R2 = P::R2, PER = P::R3;
 #pragma unroll 1
   for (int w = tid; w < P::NP * PER; w += kFT) {
@@ -205,14 +317,48 @@ __device__ __forceinline__ void row_pass_b(float2* buf, int tid) {
       for (int m1 = 0; m1 < R1; ++m1) b[m1 * P::ST1 + m2 * P::ST2] = v[m1];
     }
   }
+  }
 }
 
 // Column pass A (forward): Hermitian unpack of the row pairs, the radix-2 pair axis and the
 // radix-Q1 axis (row-pair stride Q2) in registers.  Work item (q, g2); q = 0 also carries the
 // Nyquist column M/2.
+// Cooley-Tukey plans: twiddles of column pass A.  The odd pair output of row pair t = g2 + Q2 m takes
+// W_NH^t = W_NH^g2 W_16^m (NH = 16 Q2) before the Q1-point DFT over m, and output k of both takes
+// W_NP^(g2 k) after it.  The W_16^m are compile-time constants (tw1); the common factor W_NH^g2 commutes
+// with the DFT and is folded into the odd output's table twiddle W_M^(2 g2 (1 + 2 k)) (tw2, whose even
+// output twiddle is W_M^(4 g2 k)); the table reads come after a compiler fence, so they are not hoisted
+// over the DFT and held in registers.
+template <bool INV, int Q>
+__device__ __forceinline__ void ct_col_tw1(float2 (&u)[Q]) {
+  static_assert(Q == 8, "W_16 constants for an 8-point column pass");
+  u[1] = tw16<INV, 1>(u[1]);
+  u[2] = tw16<INV, 2>(u[2]);
+  u[3] = tw16<INV, 3>(u[3]);
+  u[4] = tw16<INV, 4>(u[4]);
+  u[5] = tw16<INV, 5>(u[5]);
+  u[6] = tw16<INV, 6>(u[6]);
+  u[7] = tw16<INV, 7>(u[7]);
+}
+template <class P, bool INV>
+__device__ __forceinline__ void ct_col_tw2(float2 (&u0)[P::Q1], float2 (&u1)[P::Q1], const float2* tw, int g2) {
+  static_assert(P::NH == 16 * P::Q2 && P::M == 2 * P::NH && P::M == 4 * P::NP, "twiddle indices");
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int k = 0; k < P::Q1; ++k) {
+    if (k > 0) {
+      const float2 w0 = tw[4 * g2 * k];
+      u0[k] = cmul(u0[k], INV ? cconj(w0) : w0);
+    }
+    const float2 w1 = tw[2 * g2 * (1 + 2 * k)];
+    u1[k] = cmul(u1[k], INV ? cconj(w1) : w1);
+  }
+}
+
 template <class P>
 __device__ __forceinline__ void col_pass_a_fwd(float2* buf, const short* pa, const short* pb, int tid) {
   constexpr int Q1 = P::Q1, HQ = P::M / 2;
+  const float2* tw = P::kCT ? ct_tw<P>(buf) : nullptr;
 #pragma unroll 1
   for (int w = tid; w < HQ * P::Q2; w += kFT) {
     // row-pair group fastest across lanes: spreads the lanes of a wave over LDS banks
@@ -229,8 +375,10 @@ __device__ __forceinline__ void col_pass_a_fwd(float2* buf, const short* pa, con
         u0[m] = cadd(A, B);
         u1[m] = csub(A, B);
       }
+      if constexpr (P::kCT) ct_col_tw1<false>(u1);
       Dft<Q1, false>::run(u0);
       Dft<Q1, false>::run(u1);
+      if constexpr (P::kCT) ct_col_tw2<P, false>(u0, u1, tw, g2);
 #pragma unroll
       for (int m = 0; m < Q1; ++m) {
         b[m * P::Q2 * P::RS + sa] = u0[m];
@@ -238,7 +386,7 @@ __device__ __forceinline__ void col_pass_a_fwd(float2* buf, const short* pa, con
       }
     } else {
       // DC (slots 0 / M) and Nyquist (slots pa[M/2] / M + 1) columns, one after the other
-#pragma unroll
+#pragma unroll 1
       for (int half = 0; half < 2; ++half) {
         const int src = half ? pa[HQ] : 0;
         const int da = half ? pa[HQ] : 0, db = half ? P::M + 1 : P::M;
@@ -249,8 +397,10 @@ __device__ __forceinline__ void col_pass_a_fwd(float2* buf, const short* pa, con
           d0[m] = make_float2(z.x + z.y, 0.f);
           d1[m] = make_float2(z.x - z.y, 0.f);
         }
+        if constexpr (P::kCT) ct_col_tw1<false>(d1);
         Dft<Q1, false>::run(d0);
         Dft<Q1, false>::run(d1);
+        if constexpr (P::kCT) ct_col_tw2<P, false>(d0, d1, tw, g2);
 #pragma unroll
         for (int m = 0; m < Q1; ++m) {
           float2* r = b + m * P::Q2 * P::RS;
@@ -266,6 +416,7 @@ __device__ __forceinline__ void col_pass_a_fwd(float2* buf, const short* pa, con
 template <class P>
 __device__ __forceinline__ void col_pass_a_inv(float2* buf, const short* pa, const short* pb, int tid) {
   constexpr int Q1 = P::Q1, HQ = P::M / 2;
+  const float2* tw = P::kCT ? ct_tw<P>(buf) : nullptr;
 #pragma unroll 1
   for (int w = tid; w < HQ * P::Q2; w += kFT) {
     // row-pair group fastest across lanes: spreads the lanes of a wave over LDS banks
@@ -279,8 +430,10 @@ __device__ __forceinline__ void col_pass_a_inv(float2* buf, const short* pa, con
         u0[m] = b[m * P::Q2 * P::RS + sa];
         u1[m] = b[m * P::Q2 * P::RS + sb];
       }
+      if constexpr (P::kCT) ct_col_tw2<P, true>(u0, u1, tw, g2);
       Dft<Q1, true>::run(u0);
       Dft<Q1, true>::run(u1);
+      if constexpr (P::kCT) ct_col_tw1<true>(u1);
 #pragma unroll
       for (int m = 0; m < Q1; ++m) {
         const float2 A = cadd(u0[m], u1[m]), B = csub(u0[m], u1[m]);
@@ -289,7 +442,7 @@ __device__ __forceinline__ void col_pass_a_inv(float2* buf, const short* pa, con
       }
     } else {
       // DC (slots 0 / M -> 0) and Nyquist (slots pa[M/2] / M + 1 -> pa[M/2]) columns in turn
-#pragma unroll
+#pragma unroll 1
       for (int half = 0; half < 2; ++half) {
         const int sa = half ? pa[HQ] : 0, sb = half ? P::M + 1 : P::M;
         float2 d0[Q1], d1[Q1];
@@ -299,8 +452,10 @@ __device__ __forceinline__ void col_pass_a_inv(float2* buf, const short* pa, con
           d0[m] = r[sa];
           d1[m] = r[sb];
         }
+        if constexpr (P::kCT) ct_col_tw2<P, true>(d0, d1, tw, g2);
         Dft<Q1, true>::run(d0);
         Dft<Q1, true>::run(d1);
+        if constexpr (P::kCT) ct_col_tw1<true>(d1);
 #pragma unroll
         for (int m = 0; m < Q1; ++m) b[m * P::Q2 * P::RS + sa] = make_float2(d0[m].x + d1[m].x, d0[m].x - d1[m].x);
       }
@@ -318,7 +473,17 @@ __device__ __forceinline__ void col_pass_b(float2* buf, const short* pa, const s
 #pragma unroll 1
   for (int w = tid; w < NPOS * P::Q1; w += kFT) {
     const int g1 = w / NPOS, p = w - g1 * NPOS;
-    dft_odd_mem<Q, P::RS, INV>(buf + g1 * P::Q2 * P::RS + p);
+    if constexpr (P::kCT) {
+      float2* b = buf + g1 * P::Q2 * P::RS + p;
+      float2 u[Q];
+#pragma unroll
+      for (int m = 0; m < Q; ++m) u[m] = b[m * P::RS];
+      Dft<Q, INV>::run(u);
+#pragma unroll
+      for (int m = 0; m < Q; ++m) b[m * P::RS] = u[m];
+    } else {
+      dft_odd_mem<Q, P::RS, INV>(buf + g1 * P::Q2 * P::RS + p);
+    }
   }
 }
 
@@ -365,10 +530,7 @@ struct RowIO {
 // plane row of row position rp of group G (scalar: rp is wave-uniform)
 template <class P>
 __device__ __forceinline__ int plane_row(int rp, int G) {
-  const int g1 = rp / P::CS1, r1 = rp - g1 * P::CS1;
-  const int g2 = r1 >> 1, g3 = r1 & 1;
-  const int g = (g1 * (P::NH / P::Q1) + g2 * (P::NH / P::Q2) + g3 * (P::NH / 2)) % P::NH;
-  return 2 * g + G;
+  return P::plane_row(rp, G);
 }
 
 // Rows wider than the 256 columns the 64 lanes' float4 loads cover (the 260-point plan with no
@@ -417,9 +579,12 @@ __device__ __forceinline__ void group_prefetch(float4 (&v)[RowIO<P>::RPW], __amd
 }
 
 template <class P, bool WIDE = false>
-__device__ __forceinline__ void group_deposit(float2* buf, const float4 (&v)[RowIO<P>::RPW], const int (&lp)[4],
+__device__ __forceinline__ void group_deposit(float2* buf, const float4 (&v)[RowIO<P>::RPW], const short* pos,
                                               const FusedArgs& a, float tail, int wave, int lane) {
   float* fb = (float*)buf;
+  int lp[4];  // in-row positions of this lane's four columns (read here, not held across the kernel)
+#pragma unroll
+  for (int c = 0; c < 4; ++c) lp[c] = pos[min(a.pad + 4 * lane + c, P::M - 1)];
 #pragma unroll
   for (int i = 0; i < RowIO<P>::RPW; ++i) {
     const int rp = wave + i * RowIO<P>::NW;
@@ -484,9 +649,12 @@ __device__ __forceinline__ void group_forward_passes_loading(float2* buf, const 
 
 // Cropped rows of group G (inverse transformed, in LDS) to the output, GELU applied on store.
 template <class P, bool WIDE = false>
-__device__ __forceinline__ void group_store(const float2* buf, const int (&lp)[4], __amdgpu_buffer_rsrc_t orsrc,
+__device__ __forceinline__ void group_store(const float2* buf, const short* pos, __amdgpu_buffer_rsrc_t orsrc,
                                             const FusedArgs& a, int G, int wave, int lane) {
   const float* fb = (const float*)buf;
+  int lp[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) lp[c] = pos[min(a.pad + 4 * lane + c, P::M - 1)];
 #pragma unroll 1
   for (int i = 0; i < RowIO<P>::RPW; ++i) {
     const int rp = wave + i * RowIO<P>::NW;
@@ -515,7 +683,7 @@ __device__ __forceinline__ void group_store(const float2* buf, const int (&lp)[4
 }
 
 template <class P, bool WIDE = false>
-__device__ __forceinline__ void group_inverse_store(float2* buf, const short* pa, const short* pb, const int (&lp)[4],
+__device__ __forceinline__ void group_inverse_store(float2* buf, const short* pa, const short* pb, const short* pos,
                                                     __amdgpu_buffer_rsrc_t orsrc, const FusedArgs& a, int G,
                                                     int wave, int lane, int tid) {
   col_pass_b<P, true>(buf, pa, pb, tid);
@@ -526,7 +694,7 @@ __device__ __forceinline__ void group_inverse_store(float2* buf, const short* pa
   lds_barrier();
   row_pass_a<P, true>(buf, tid);
   lds_barrier();
-  group_store<P, WIDE>(buf, lp, orsrc, a, G, wave, lane);
+  group_store<P, WIDE>(buf, pos, orsrc, a, G, wave, lane);
 }
 
 // Table entries of the combine step are loaded kTabBatch slots at a time.
@@ -545,6 +713,7 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
   short* pos = pb + P::NQ;
   unsigned char* isb = (unsigned char*)(pos + P::M);  // 1 where a position holds the odd row
   short* colsrc = (short*)((char*)wtab + P::CONST_BYTES);
+  static_assert(tabs_layout_ok<P>(), "LDS table block layout");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t plane = fused_plane(blockIdx.x, a);
@@ -559,14 +728,11 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
     for (int i = tid; i < P::CONST_BYTES / 16; i += kFT) dst[i] = src[i];
   }
   for (int j = tid; j < P::M; j += kFT) colsrc[j] = fpad_src(j, a.W, a.pad, a.mode);
-  int lp[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) lp[c] = P::pos_in(min(a.pad + 4 * lane + c, P::M - 1));
   float4 pre[RowIO<P>::RPW];
   group_prefetch<P>(pre, xr, a, 0, wave, lane);
   float tail = tail_load<P, WIDE>(xr, a, 0, tid);
   lds_barrier();
-  group_deposit<P, WIDE>(buf, pre, lp, a, tail, wave, lane);
+  group_deposit<P, WIDE>(buf, pre, pos, a, tail, wave, lane);
   lds_barrier();
   group_pad_cols<P>(buf, pos, colsrc, a.pad, tid);
   lds_barrier();
@@ -582,7 +748,7 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
     else park[i - PL] = v;
   }
   lds_barrier();
-  group_deposit<P, WIDE>(buf, pre, lp, a, tail, wave, lane);
+  group_deposit<P, WIDE>(buf, pre, pos, a, tail, wave, lane);
   lds_barrier();
   group_pad_cols<P>(buf, pos, colsrc, a.pad, tid);
   lds_barrier();
@@ -623,12 +789,12 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
     asm volatile("" ::: "memory");  // the next batch's loads may not be hoisted above this one
   }
   lds_barrier();
-  group_inverse_store<P, WIDE>(buf, pa, pb, lp, orsrc, a, 1, wave, lane, tid);
+  group_inverse_store<P, WIDE>(buf, pa, pb, pos, orsrc, a, 1, wave, lane, tid);
   lds_barrier();
 #pragma unroll
   for (int i = 0; i < P::PARK; ++i) buf[tid + i * kFT] = i < PL ? parkl[i * kFT + tid] : park[i < PL ? 0 : i - PL];
   lds_barrier();
-  group_inverse_store<P, WIDE>(buf, pa, pb, lp, orsrc, a, 0, wave, lane, tid);
+  group_inverse_store<P, WIDE>(buf, pa, pb, pos, orsrc, a, 0, wave, lane, tid);
 }
 
 // ----------------------------------------------------------------------------------------------
@@ -945,15 +1111,12 @@ __global__ void __launch_bounds__(kFT, 8) k_converse2d_fused_up(FusedUpArgs ua) 
     buf[sl] = o1;
   }
   lds_barrier();
-  int lp[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) lp[c] = P::pos_in(min(a.pad + 4 * lane + c, P::M - 1));
-  group_inverse_store<P>(buf, pa, pb, lp, orsrc, a, 1, wave, lane, tid);
+  group_inverse_store<P>(buf, pa, pb, pos, orsrc, a, 1, wave, lane, tid);
   lds_barrier();
 #pragma unroll
   for (int i = 0; i < P::PARK; ++i) buf[tid + i * kFT] = park[i];
   lds_barrier();
-  group_inverse_store<P>(buf, pa, pb, lp, orsrc, a, 0, wave, lane, tid);
+  group_inverse_store<P>(buf, pa, pb, pos, orsrc, a, 0, wave, lane, tid);
 }
 
 // ----------------------------------------------------------------------------------------------
@@ -961,6 +1124,23 @@ __global__ void __launch_bounds__(kFT, 8) k_converse2d_fused_up(FusedUpArgs ua) 
 // ----------------------------------------------------------------------------------------------
 using Plan260 = FusedPlan<260, 4, 5, 13, 5, 13, 5>;   // rows 260 = 4 5 13, columns 130 = 5 13 2
 using Plan132 = FusedPlan<132, 4, 3, 11, 3, 11>;   // rows 132 = 4 3 11, columns 66 = 3 11 2
+using Plan256 = CtPlan<16, 16, 8, 1>;              // rows 256 = 16 16, columns 128 = 2 8 8 (Cooley-Tukey)
+
+// The generic table kernel writes this plan's tables through fused256_phi_index (cvn_common.h):
+// check that map against the plan's slot order (the layout k_phi_fused<Plan256> writes).
+constexpr bool fused256_index_ok() {
+  using P = Plan256;
+  if (P::RS != kF256Rs || P::SLOTS != kF256Slots) return false;
+  for (int u = 0; u < P::N; ++u) {
+    const int rp = P::rfpos(u % P::NH);
+    for (int v = 0; v < P::NQ; v += (v == 0 || v == P::NQ - 2) ? 1 : 37) {
+      const int64_t want = 2 * ((int64_t)(rp >> 1) * P::RS + ((rp & 1) ? P::pb(v) : P::pa(v))) + u / P::NH;
+      if (fused256_phi_index(0, v, u) != want || fused256_phi_index(3, v, u) != want + 2 * 3 * P::SLOTS) return false;
+    }
+  }
+  return true;
+}
+static_assert(fused256_index_ok(), "fused256_phi_index matches Plan256");
 
 // LDS layout of the up kernel after the fused kernel's own regions.
 struct UpLayout {
@@ -1046,6 +1226,7 @@ int fused_query(int H, int W, int pad, int scale, int64_t Cp, size_t* ws_bytes) 
   const int h = H + 2 * pad, w = W + 2 * pad;
   if (h == 260 && w == 260) { *ws_bytes = fused_ws<Plan260>(Cp); return 1; }
   if (h == 132 && w == 132) { *ws_bytes = fused_ws<Plan132>(Cp); return 1; }
+  if (h == 256 && w == 256) { *ws_bytes = fused_ws<Plan256>(Cp); return 1; }
   return 0;
 }
 
@@ -1059,6 +1240,7 @@ int fused_table(const float* psf, const float* bias, float eps, int64_t C, int64
   }
   const int h = H + 2 * pad;
   if (h == 260) return fused_table_run<Plan260>(psf, bias, eps, C, psf_batch, kh, kw, table, st);
+  if (h == 256) return fused_table_run<Plan256>(psf, bias, eps, C, psf_batch, kh, kw, table, st);
   return fused_table_run<Plan132>(psf, bias, eps, C, psf_batch, kh, kw, table, st);
 }
 
@@ -1094,6 +1276,7 @@ int fused_apply(const float* x, int64_t B, int64_t C, int H, int W, int64_t psf_
   }
   const int h = H + 2 * pad;
   if (h == 260) return fused_apply_run<Plan260>(x, B, C, H, W, psf_batch, pad, mode, act, table, out, st);
+  if (h == 256) return fused_apply_run<Plan256>(x, B, C, H, W, psf_batch, pad, mode, act, table, out, st);
   return fused_apply_run<Plan132>(x, B, C, H, W, psf_batch, pad, mode, act, table, out, st);
 }
 

@@ -73,8 +73,15 @@ struct PhiArgs {
   double eps;
   float2* phi;        // module: (Cp, NCs, Hs);  op: A (Cp, Ws, Hs)
   float2* kf;         // op only: K (Cp, Ws, Hs)
-  int q268;           // module at 268 x 268, scale 1: the 268 path's quad layout (pfa268_phi_index)
+  int layout;         // module form: kPhiGeneric (Cp, NCs, Hs), kPhiPfa268 (pfa268_phi_index) or kPhiFused256
 };
+// Output layouts of the module-form tables.
+constexpr int kPhiGeneric = 0, kPhiPfa268 = 1, kPhiFused256 = 2;
+__device__ __forceinline__ int64_t phi_out_index(const PhiArgs& a, int64_t cp, int64_t vb, int u) {
+  if (a.layout == kPhiPfa268) return pfa268_phi_index(cp, (int)vb, u);
+  if (a.layout == kPhiFused256) return fused256_phi_index(cp, (int)vb, u);
+  return (cp * a.NCs + vb) * a.Hs + u;
+}
 
 // P[b][i] = sum_j psf[i][j] exp(-2 pi i v_b (j - kw/2) / Ws), into LDS.
 __device__ void phi_row_sums(const PhiArgs& a, const float* psf, int v0, double2* P) {
@@ -454,7 +461,7 @@ __device__ void phi_tile_rows16(const PhiArgs& a, int op, const PhiTileView& tv,
           a.kf[o] = make_float2((float)k.x, (float)k.y);
           a.phi[o] = make_float2((float)(k.x * rD * norm), (float)(-k.y * rD * norm));
         } else {
-          a.phi[(cp * a.NCs + vb) * Hs + u] = make_float2((float)((k.x + lmb) * rD * norm), (float)(-k.y * rD * norm));
+          a.phi[phi_out_index(a, cp, vb, u)] = make_float2((float)((k.x + lmb) * rD * norm), (float)(-k.y * rD * norm));
         }
       }
     }
@@ -520,7 +527,8 @@ __device__ void phi_tile_rows16(const PhiArgs& a, int op, const PhiTileView& tv,
           } else if (vb <= a.Ws / 2) {
             const double2 hn = dcmul(tv.hH[u], hv);
             const double2 t = dcmul(make_double2(k.x, -k.y), g);
-            a.phi[(cp * a.NCs + vb) * Hs + u] = make_float2((float)((hn.x + t.x) * norm), (float)((hn.y + t.y) * norm));
+            a.phi[phi_out_index(a, cp, vb, u)] =
+                make_float2((float)((hn.x + t.x) * norm), (float)((hn.y + t.y) * norm));
           }
         }
       }
@@ -539,7 +547,7 @@ __global__ void __launch_bounds__(256) k_phi_tile(PhiArgs a, int op, int vc, int
   const int c = (int)(cp % a.C);
   const int Hs = a.Hs, Ws = a.Ws, h = a.h, kh = a.kh;
   const int kh4 = round4(kh);
-  const bool fast = phi_rows16(S, Hs, a.q268 != 0);
+  const bool fast = phi_rows16(S, Hs, a.layout == kPhiPfa268);
   const PhiTileView tv = phi_tile_prep<S>(a, phl, cp, vbeg, nv, vc, fast);
   const double2 *zH = tv.zH, *phH = tv.phH, *hH = tv.hH, *hW = tv.hW, *P = tv.P;
 
@@ -593,8 +601,7 @@ __global__ void __launch_bounds__(256) k_phi_tile(PhiArgs a, int op, int vc, int
         } else {
           const double2 hn = S > 1 ? dcmul(hH[u], hv) : make_double2(1.0, 0.0);
           const double2 t = dcmul(make_double2(k.x, -k.y), g);
-          const int64_t o = a.q268 ? pfa268_phi_index(cp, (int)vb, u) : (cp * a.NCs + vb) * Hs + u;
-          a.phi[o] = make_float2((float)((hn.x + t.x) * norm), (float)((hn.y + t.y) * norm));
+          a.phi[phi_out_index(a, cp, vb, u)] = make_float2((float)((hn.x + t.x) * norm), (float)((hn.y + t.y) * norm));
         }
       }
     }
@@ -1527,13 +1534,16 @@ ModWs module_ws(const Geo& g, const PlanTabs& t) {
   return w;
 }
 
+// Transfer tables.  Returns CVN_ERR_UNSUPPORTED without launching anything when a layout other than
+// the generic one is asked for and the tiled kernel does not apply (the caller then builds it otherwise).
 int launch_phi(const float* psf, const float* bias, float eps, const Geo& g, bool op, float2* phi,
-               float2* kf, hipStream_t st, bool q268 = false) {
+               float2* kf, hipStream_t st, int layout = kPhiGeneric) {
   PhiArgs a;
   a.psf = psf; a.bias = bias; a.Cp = g.Cp; a.C = (int)g.C; a.kh = g.kh; a.kw = g.kw; a.s = g.s;
   a.h = g.h; a.w = g.w; a.Hs = g.Hs; a.Ws = g.Ws; a.NCs = g.NCs; a.eps = (double)eps;
   a.phi = phi; a.kf = kf;
-  a.q268 = q268 ? 1 : 0;
+  a.layout = layout;
+  const bool q268 = layout == kPhiPfa268;
   a.nv0 = (!op && g.s == 1) ? g.NC : g.w;
   // tiled kernel (scales 1..4): about 2048 blocks, chunk size bounded by an LDS budget of 64 KiB
   if (g.s <= 4) {
@@ -1558,7 +1568,7 @@ int launch_phi(const float* psf, const float* bias, float eps, const Geo& g, boo
       return check_launch("transfer table");
     }
   }
-  if (q268) return fail(CVN_ERR_UNSUPPORTED, "268 transfer table needs the tiled kernel");
+  if (layout != kPhiGeneric) return fail(CVN_ERR_UNSUPPORTED, "this table layout needs the tiled kernel");
   const size_t lds = (size_t)g.s * g.kh * sizeof(double2);
   const int64_t blocks = g.Cp * a.nv0;
   if (blocks > 0x7fffffff) return fail(CVN_ERR_UNSUPPORTED, "too many transfer blocks");
@@ -1751,13 +1761,21 @@ extern "C" int cvn_converse2d_table_f32(const float* psf, int64_t psf_batch, int
   if (!table || table_bytes < r.table_bytes)
     return fail(CVN_ERR_WORKSPACE, "table buffer too small: need %zu bytes", r.table_bytes);
   hipStream_t st = (hipStream_t)stream;
-  if (r.id == CVN_ROUTE_FUSED)
+  if (r.id == CVN_ROUTE_FUSED) {
+    // 256 x 256 planes: the split-DFT table kernel writes the fused plan's slot order directly (a
+    // per-sample 25 x 25 psf, Converse-USRNet's data step, is several times faster there than in
+    // k_phi_fused); the fused kernels' own table kernel otherwise
+    if (g.s == 1 && g.h == 256 && g.w == 256 &&
+        launch_phi(psf, bias, eps, g, false, (float2*)table, nullptr, st, kPhiFused256) == CVN_OK)
+      return CVN_OK;
     return fused_table(psf, bias, eps, g.C, g.Cp / g.C, kh, kw, g.H, g.W, g.pad, g.s, table, st);
+  }
   PlanTabs t;
   if (!plan_tabs(g, &t)) return fail(CVN_ERR_UNSUPPORTED, "no FFT plan for this plane size");
   const ModWs ws = module_ws(g, t);
   if ((rc = launch_plan_tabs(t, (char*)table + ws.tabs, st)) != CVN_OK) return rc;
-  return launch_phi(psf, bias, eps, g, false, (float2*)table, nullptr, st, r.id == CVN_ROUTE_PFA268);
+  return launch_phi(psf, bias, eps, g, false, (float2*)table, nullptr, st,
+                    r.id == CVN_ROUTE_PFA268 ? kPhiPfa268 : kPhiGeneric);
 }
 
 extern "C" int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, int64_t H, int64_t W,

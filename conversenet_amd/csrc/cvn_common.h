@@ -150,6 +150,19 @@ __host__ __device__ inline int64_t pfa268_phi_index(int64_t cp, int v, int u) {
   const int r = u & 3;
   return ((cp * 67 + u % 67) * 135 + v) * 4 + (((r & 1) << 1) | (r >> 1));
 }
+// Index (in float2 units) of Phi(u, v) (row frequency u < 256, half-spectrum column v <= 128) in the
+// fused kernel's table for 256 x 256 planes (the Cooley-Tukey plan in converse2d_fused.hip): per psf
+// plane 64 row pairs of 259 slots, two float2 per slot (Phi at k and at k + 128).  Row frequency
+// k = 2 k2 + k1 (k < 128) sits at row pair 8 (k2 mod 8) + k2 / 8, at position v of the pair for k1 = 0
+// and at the odd row's position of v (256 - v; 256 for v = 0, 257 for v = 128) for k1 = 1.
+// converse2d_fused.hip checks this map against its plan at compile time.
+constexpr int kF256Rs = 259, kF256Slots = 64 * kF256Rs;
+__host__ __device__ constexpr int64_t fused256_phi_index(int64_t cp, int v, int u) {
+  const int k = u & 127, k2 = k >> 1;
+  const int rp = 2 * (8 * (k2 & 7) + (k2 >> 3)) + (k & 1);
+  const int pos = (rp & 1) ? (v == 0 ? 256 : (v == 128 ? 257 : 256 - v)) : v;
+  return ((cp * kF256Slots + (int64_t)(rp >> 1) * kF256Rs + pos) << 1) + (u >> 7);
+}
 int pfa268_forward(const float* x, int64_t P, int64_t C, int64_t psf_batch, int H, int W, int pad, int mode, int act,
                    const float2* phi, float2* S, float* out, hipStream_t st);
 // Scratch the 268 path needs between its passes (at least the generic path's S region).

@@ -179,6 +179,47 @@ template <bool INV> struct Dft<8, INV> {
   }
 };
 
+// 16-point DFT as 4 x 4 (Cooley-Tukey): sample 4 n1 + n2, 4-point DFTs over n1, twiddles
+// W16^(n2 k1), 4-point DFTs over n2; natural order in and out.
+template <bool INV, int J>
+__device__ __forceinline__ float2 tw16(float2 x) {
+  if constexpr (J % 16 == 0) {
+    return x;
+  } else if constexpr (J % 16 == 4) {
+    return rot<INV>(x);
+  } else {
+    constexpr CosSin w = cos_sin_turn(J, 16);
+    return cmul(x, make_float2((float)w.c, INV ? (float)w.s : (float)-w.s));
+  }
+}
+template <bool INV> struct Dft<16, INV> {
+  template <int N2>
+  static __device__ __forceinline__ void col(float2 (&a)[4][4]) {
+    a[N2][1] = tw16<INV, N2 * 1>(a[N2][1]);
+    a[N2][2] = tw16<INV, N2 * 2>(a[N2][2]);
+    a[N2][3] = tw16<INV, N2 * 3>(a[N2][3]);
+  }
+  static __device__ __forceinline__ void run(float2* u) {
+    float2 a[4][4];  // a[n2][k1]
+#pragma unroll
+    for (int n2 = 0; n2 < 4; ++n2) {
+#pragma unroll
+      for (int n1 = 0; n1 < 4; ++n1) a[n2][n1] = u[4 * n1 + n2];
+      Dft<4, INV>::run(a[n2]);
+    }
+    col<1>(a);
+    col<2>(a);
+    col<3>(a);
+#pragma unroll
+    for (int k1 = 0; k1 < 4; ++k1) {
+      float2 v[4] = {a[0][k1], a[1][k1], a[2][k1], a[3][k1]};
+      Dft<4, INV>::run(v);
+#pragma unroll
+      for (int k2 = 0; k2 < 4; ++k2) u[k1 + 4 * k2] = v[k2];
+    }
+  }
+};
+
 // Odd prime radix via conjugate-pair sums: X_q = A_q -+ i B_q, X_{R-q} = A_q +- i B_q with
 // A_q = u0 + sum_j cos(2 pi j q / R)(u_j + u_{R-j}),  B_q = sum_j sin(2 pi j q / R)(u_j - u_{R-j}).
 template <int R, bool INV> struct DftOdd {

@@ -77,6 +77,11 @@ def test_route_query_and_environment(monkeypatch):
     assert lib.cvn_converse2d_route(8, 64, 60, 60, 1, 3, 3, 2, 1) == _lib.ROUTE_GENERIC  # 62 -> 124
     assert lib.cvn_converse2d_route(16, 64, 260, 260, 1, 5, 5, 1, 0) == _lib.ROUTE_FUSED  # padded input, op path
     assert lib.cvn_converse2d_route(16, 64, 258, 258, 1, 5, 5, 1, 1) == _lib.ROUTE_GENERIC  # 258 % 4 != 0
+    # 256^2 planes (Converse-USRNet's data steps, per-sample 25 x 25 psf): the Cooley-Tukey fused plan
+    assert lib.cvn_converse2d_route(4, 64, 256, 256, 4, 25, 25, 1, 0) == _lib.ROUTE_FUSED
+    assert lib.cvn_converse2d_route(1, 2, 240, 240, 1, 7, 7, 1, 8) == _lib.ROUTE_FUSED
+    assert lib.cvn_converse2d_route(1, 2, 250, 250, 1, 7, 7, 1, 3) == _lib.ROUTE_GENERIC  # 250 % 4 != 0
+    assert lib.cvn_converse2d_route(4, 64, 64, 64, 4, 25, 25, 4, 0) == _lib.ROUTE_GENERIC  # 64 -> 256: no up plan
     monkeypatch.setenv("CVN_DISABLE_FUSED", "1")
     assert lib.cvn_converse2d_route(16, 64, 256, 256, 1, 5, 5, 1, 2) == _lib.ROUTE_GENERIC
     assert lib.cvn_converse2d_route(8, 128, 256, 256, 1, 7, 7, 1, 6) == _lib.ROUTE_GENERIC

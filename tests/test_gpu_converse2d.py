@@ -182,6 +182,49 @@ def test_transfer_table_cache_follows_in_place_updates():
     assert len(Fh.table_cache.entries) == 0
 
 
+# 256 x 256 planes: the fused kernel's Cooley-Tukey plan (rows 16 x 16, columns 2 x 8 x 8 with twiddles)
+CT256_CASES = [
+    # B, C, H, p, mode, k, per-sample psf, act
+    (2, 3, 256, 0, "circular", 5, False, None),
+    (2, 4, 256, 0, "circular", 25, True, None),      # Converse-USRNet's data step (per-sample 25 x 25 psf)
+    (1, 2, 252, 2, "reflect", 5, False, "gelu"),
+    (1, 2, 240, 8, "replicate", 7, False, None),
+    (1, 3, 248, 4, "constant", 9, True, "gelu"),
+    (3, 2, 244, 6, "circular", 4, False, None),
+]
+
+
+@pytest.mark.parametrize("B,C,H,p,mode,k,ps,act", CT256_CASES)
+def test_fused_256_cooley_tukey(B, C, H, p, mode, k, ps, act, monkeypatch):
+    """256 x 256 padded planes on the fused route against the fp64 oracle and the generic passes."""
+    from conversenet_amd import _lib
+    from conversenet_amd import functional as Fh
+    rng = seeded("ct256", B, C, H, p, mode, k, ps, act)
+    x = rng.standard_normal((B, C, H, H)).astype(np.float32)
+    w = softmax_psf(rng, C, k, batch=B if ps else 1)
+    b = (0.4 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    eps = 1e-3 if ps else 1e-5
+    monkeypatch.delenv("CVN_DISABLE_FUSED", raising=False)
+    assert _lib.load().cvn_converse2d_route(B, C, H, H, w.shape[0], k, k, 1, p) == _lib.ROUTE_FUSED
+    ref = O.converse2d_module(x, w, b, 1, p, mode, eps)
+    if act:
+        ref = O.gelu(ref)
+    dev = torch.device("cuda")
+
+    def run():
+        out = Fh.converse2d_fused(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev),
+                                  torch.from_numpy(b).reshape(-1).to(dev), 1, p, mode, eps, act=act)
+        return out.cpu().numpy()
+
+    fused = run()
+    err = np.abs(fused - ref).max()
+    print(f"fused 256^2 (Cooley-Tukey) B{B} C{C} p{p} {mode} k{k} per-sample {ps} act {act}: max-abs {err:.3e}")
+    assert err <= TOL, err
+    monkeypatch.setenv("CVN_DISABLE_FUSED", "1")
+    generic = run()
+    assert np.abs(fused - generic).max() <= TOL
+
+
 @pytest.mark.parametrize("H,p", [(256, 2), (128, 2)])
 def test_fused_matches_generic_path(H, p, monkeypatch):
     """The fused single-kernel path and the generic multi-pass path agree (both vs the oracle)."""
