@@ -798,6 +798,129 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
 }
 
 // ----------------------------------------------------------------------------------------------
+// Split form for small plane counts (at most kFusedSplitPlanes planes, where one workgroup per plane
+// leaves most of the 256 CUs idle): each row group of a plane gets a workgroup of its own.
+//   k_converse2d_fused_fwd: group G's rows -> its forward passes -> its spectrum (SLOTS_PAD slots in
+//     the group buffer's order) to the caller's scratch.
+//   k_converse2d_fused_inv: both groups' spectra -> the radix-2 step across the groups and the transfer
+//     function, keeping group G's half (E' for G0, O' for G1) -> G's inverse passes and store.
+// The two workgroups of a plane are 16 j + r and 16 j + 8 + r (plane 8 j + r), so they run on the
+// same XCD (workgroup i goes to XCD i % 8) and the second kernel reads both spectra where the first
+// wrote them.  The LDS layout is the fused kernel's; the parked rounds stay unused.
+// ----------------------------------------------------------------------------------------------
+__device__ __forceinline__ bool split_item(int64_t blk, int64_t planes, int64_t& plane, int& G) {
+  const int r = (int)(blk & 15);
+  G = r >> 3;
+  plane = 8 * (blk >> 4) + (r & 7);
+  return plane < planes;
+}
+typedef unsigned int v2u32_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void bstore2(float2 v, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, v), r, voff, soff, 0);
+}
+
+template <class P, bool WIDE>
+__global__ void __launch_bounds__(kFT) k_converse2d_fused_fwd(FusedArgs a, float2* spec) {
+  extern __shared__ float2 smem[];
+  float2* buf = smem;
+  float2* wtab = smem + P::SLOTS_PAD + P::PARK_LDS * kFT;
+  short* pa = (short*)(wtab + P::NH + 2);
+  short* pb = pa + P::NQ;
+  short* pos = pb + P::NQ;
+  short* colsrc = (short*)((char*)wtab + P::CONST_BYTES);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int64_t plane;
+  int G;
+  if (!split_item(blockIdx.x, a.B * a.C, plane, G)) return;  // whole workgroup: no barrier is left waiting
+  const uint32_t plane_bytes = (uint32_t)(a.H * a.W) * 4u;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + plane * (int64_t)a.H * a.W, plane_bytes);
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(spec + (2 * plane + G) * P::SLOTS_PAD, P::SLOTS_PAD * 8u);
+  float4 pre[RowIO<P>::RPW];
+  group_prefetch<P>(pre, xr, a, G, wave, lane);
+  const float tail = tail_load<P, WIDE>(xr, a, G, tid);
+  {
+    const v4u32_t* src = (const v4u32_t*)&kFusedTabs<P>;
+    v4u32_t* dst = (v4u32_t*)wtab;
+    for (int i = tid; i < P::CONST_BYTES / 16; i += kFT) dst[i] = src[i];
+  }
+  for (int j = tid; j < P::M; j += kFT) colsrc[j] = fpad_src(j, a.W, a.pad, a.mode);
+  lds_barrier();
+  group_deposit<P, WIDE>(buf, pre, pos, a, tail, wave, lane);
+  lds_barrier();
+  group_pad_cols<P>(buf, pos, colsrc, a.pad, tid);
+  lds_barrier();
+  group_forward_passes<P>(buf, pa, pb, tid);
+  col_pass_b<P, false>(buf, pa, pb, tid);
+  lds_barrier();
+#pragma unroll
+  for (int i = 0; i < P::PARK; ++i) bstore2(buf[tid + i * kFT], sr, 8u * tid, 8u * i * kFT);
+}
+
+template <class P, bool WIDE>
+__global__ void __launch_bounds__(kFT) k_converse2d_fused_inv(FusedArgs a, const float2* spec) {
+  extern __shared__ float2 smem[];
+  float2* buf = smem;
+  float2* wtab = smem + P::SLOTS_PAD + P::PARK_LDS * kFT;
+  short* pa = (short*)(wtab + P::NH + 2);
+  short* pb = pa + P::NQ;
+  short* pos = pb + P::NQ;
+  unsigned char* isb = (unsigned char*)(pos + P::M);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int64_t plane;
+  int G;
+  if (!split_item(blockIdx.x, a.B * a.C, plane, G)) return;
+  const int64_t cp = (a.psf_batch == 1) ? (plane % a.C) : plane;
+  const uint32_t plane_bytes = (uint32_t)(a.H * a.W) * 4u;
+  const __amdgpu_buffer_rsrc_t orsrc = make_rsrc(a.out + plane * (int64_t)a.H * a.W, plane_bytes);
+  const __amdgpu_buffer_rsrc_t t4r = make_rsrc(a.tab4 + cp * P::SLOTS, P::SLOTS * 16u);
+  const __amdgpu_buffer_rsrc_t er = make_rsrc(spec + 2 * plane * P::SLOTS_PAD, P::SLOTS_PAD * 8u);
+  const __amdgpu_buffer_rsrc_t orr = make_rsrc(spec + (2 * plane + 1) * P::SLOTS_PAD, P::SLOTS_PAD * 8u);
+  // slot rounds in batches of SB (all of them at once when there are few), the next batch's loads in
+  // flight while the current one is combined
+  constexpr int SB = P::PARK <= 8 ? P::PARK : kTabBatch, NB = (P::PARK + SB - 1) / SB;
+  float4 f4[2][SB];
+  float2 e[2][SB], o[2][SB];
+  auto load = [&](int bt, int j) {
+#pragma unroll
+    for (int i = 0; i < SB; ++i) {
+      const uint32_t r = (uint32_t)(bt * SB + i) * kFT;
+      f4[j][i] = bload4(t4r, 16u * tid, 16u * r);
+      e[j][i] = bload2(er, 8u * tid, 8u * r);
+      o[j][i] = bload2(orr, 8u * tid, 8u * r);
+    }
+  };
+  load(0, 0);
+  {
+    const v4u32_t* src = (const v4u32_t*)&kFusedTabs<P>;
+    v4u32_t* dst = (v4u32_t*)wtab;
+    for (int i = tid; i < P::CONST_BYTES / 16; i += kFT) dst[i] = src[i];
+  }
+  lds_barrier();
+#pragma unroll
+  for (int bt = 0; bt < NB; ++bt) {
+    const int j = bt & 1;
+    if (bt + 1 < NB) load(bt + 1, j ^ 1);
+#pragma unroll
+    for (int i = 0; i < SB; ++i) {
+      const int s = tid + (bt * SB + i) * kFT;
+      if (bt * SB + i < P::PARK && s < P::SLOTS) {  // slots past SLOTS are padding (never read back)
+        const int t = s / P::RS;
+        const float2 w = wtab[2 * t + isb[s - t * P::RS]];
+        const float2 wo = cmul(w, o[j][i]);
+        const float2 y0 = cmul(make_float2(f4[j][i].x, f4[j][i].y), cadd(e[j][i], wo));
+        const float2 y1 = cmul(make_float2(f4[j][i].z, f4[j][i].w), csub(e[j][i], wo));
+        buf[s] = G == 0 ? cadd(y0, y1) : cmul(cconj(w), csub(y0, y1));
+      }
+    }
+    asm volatile("" ::: "memory");  // the batch after next may not be hoisted above this one
+  }
+  lds_barrier();
+  group_inverse_store<P, WIDE>(buf, pa, pb, pos, orsrc, a, G, wave, lane, tid);
+}
+
+// ----------------------------------------------------------------------------------------------
 // Transfer table in the fused kernel's slot order (fp64).  One block per (psf plane, column q);
 // threads over the column sub-frequency k in [0, N/2).
 //   Phi(u, q) = (conj K + lambda) / (|K|^2 + lambda) / (N M),
@@ -1189,21 +1312,45 @@ int fused_table_run(const float* psf, const float* bias, float eps, int64_t C, i
 }
 
 template <class P>
+size_t fused_split_bytes(int64_t planes) {
+  return align_up((size_t)planes * 2 * P::SLOTS_PAD * sizeof(float2));
+}
+
+template <class P, bool WIDE>
+void fused_split_launch(const FusedArgs& fa, void* scratch, hipStream_t st) {
+  const unsigned grid = (unsigned)(16 * ((fa.B * fa.C + 7) / 8));
+  hipLaunchKernelGGL((k_converse2d_fused_fwd<P, WIDE>), dim3(grid), dim3(kFT), P::LDS_BYTES, st, fa,
+                     (float2*)scratch);
+  hipLaunchKernelGGL((k_converse2d_fused_inv<P, WIDE>), dim3(grid), dim3(kFT), P::LDS_BYTES, st, fa,
+                     (const float2*)scratch);
+}
+
+template <class P>
 int fused_apply_run(const float* x, int64_t B, int64_t C, int H, int W, int64_t psf_batch, int pad, int mode,
-                    int act, const void* table, float* out, hipStream_t st) {
+                    int act, const void* table, void* scratch, float* out, hipStream_t st) {
   static std::atomic<uint64_t> attr{0};
   once_per_device(attr, [] {
-    (void)hipFuncSetAttribute((const void*)k_converse2d_fused<P, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)P::LDS_BYTES);
-    if constexpr (RowTail<P>::kAny)
-      (void)hipFuncSetAttribute((const void*)k_converse2d_fused<P, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)P::LDS_BYTES);
+    for (const void* k : {(const void*)k_converse2d_fused<P, false>, (const void*)k_converse2d_fused_fwd<P, false>,
+                          (const void*)k_converse2d_fused_inv<P, false>})
+      (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)P::LDS_BYTES);
+    if constexpr (RowTail<P>::kAny) {
+      for (const void* k : {(const void*)k_converse2d_fused<P, true>, (const void*)k_converse2d_fused_fwd<P, true>,
+                            (const void*)k_converse2d_fused_inv<P, true>})
+        (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)P::LDS_BYTES);
+    }
     (void)hipGetLastError();
   });
   const float4* t4 = (const float4*)table;
   FusedArgs fa{x, t4, out, B, C, psf_batch, H, W, pad, mode, act};
   bool wide = false;
   if constexpr (RowTail<P>::kAny) wide = W > 256;
+  if (scratch && B * C <= kFusedSplitPlanes) {
+    if constexpr (RowTail<P>::kAny) {
+      if (wide) fused_split_launch<P, true>(fa, scratch, st);
+    }
+    if (!wide) fused_split_launch<P, false>(fa, scratch, st);
+    return check_launch("fused converse2d (split)");
+  }
   if constexpr (RowTail<P>::kAny) {
     if (wide)
       hipLaunchKernelGGL((k_converse2d_fused<P, true>), dim3((unsigned)(B * C)), dim3(kFT), P::LDS_BYTES, st, fa);
@@ -1230,6 +1377,15 @@ int fused_query(int H, int W, int pad, int scale, int64_t Cp, size_t* ws_bytes) 
   return 0;
 }
 
+size_t fused_scratch(int64_t planes, int H, int W, int pad, int scale) {
+  if (scale != 1 || planes > kFusedSplitPlanes) return 0;
+  const int h = H + 2 * pad;
+  if (h == 260) return fused_split_bytes<Plan260>(planes);
+  if (h == 256) return fused_split_bytes<Plan256>(planes);
+  if (h == 132) return fused_split_bytes<Plan132>(planes);
+  return 0;
+}
+
 int fused_table(const float* psf, const float* bias, float eps, int64_t C, int64_t psf_batch, int kh, int kw,
                 int H, int W, int pad, int scale, void* table, hipStream_t st) {
   if (scale != 1) {
@@ -1245,7 +1401,7 @@ int fused_table(const float* psf, const float* bias, float eps, int64_t C, int64
 }
 
 int fused_apply(const float* x, int64_t B, int64_t C, int H, int W, int64_t psf_batch, int pad, int mode, int act,
-                int scale, const void* table, float* out, hipStream_t st) {
+                int scale, const void* table, void* scratch, float* out, hipStream_t st) {
   if (scale != 1) {
     using P = Plan132;
     static std::atomic<uint64_t> attr{0};
@@ -1275,9 +1431,9 @@ int fused_apply(const float* x, int64_t B, int64_t C, int H, int W, int64_t psf_
     return check_launch("fused converse2d (scale > 1)");
   }
   const int h = H + 2 * pad;
-  if (h == 260) return fused_apply_run<Plan260>(x, B, C, H, W, psf_batch, pad, mode, act, table, out, st);
-  if (h == 256) return fused_apply_run<Plan256>(x, B, C, H, W, psf_batch, pad, mode, act, table, out, st);
-  return fused_apply_run<Plan132>(x, B, C, H, W, psf_batch, pad, mode, act, table, out, st);
+  if (h == 260) return fused_apply_run<Plan260>(x, B, C, H, W, psf_batch, pad, mode, act, table, scratch, out, st);
+  if (h == 256) return fused_apply_run<Plan256>(x, B, C, H, W, psf_batch, pad, mode, act, table, scratch, out, st);
+  return fused_apply_run<Plan132>(x, B, C, H, W, psf_batch, pad, mode, act, table, scratch, out, st);
 }
 
 }  // namespace cvn

@@ -1648,7 +1648,7 @@ int module_route(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch, 
   r->id = want;
   if (want == CVN_ROUTE_FUSED) {
     r->table_bytes = fws;
-    r->scratch_bytes = 0;
+    r->scratch_bytes = fused_scratch(g->P, g->H, g->W, g->pad, g->s);
     return CVN_OK;
   }
   PlanTabs t;
@@ -1797,7 +1797,11 @@ extern "C" int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, in
     if (((uintptr_t)x & 15) || ((uintptr_t)out & 15))
       return fail(CVN_ERR_ARG, "the fused kernel needs 16-byte aligned input and output");
     if (B * C > 0x7fffffff) return fail(CVN_ERR_UNSUPPORTED, "too many planes");
-    return fused_apply(x, B, C, g.H, g.W, g.Cp / g.C, pad, pad_mode, act, g.s, table, out, st);
+    // scratch is optional here: with it, a few planes run split over twice the workgroups
+    if (scratch && scratch_bytes < r.scratch_bytes)
+      return fail(CVN_ERR_WORKSPACE, "scratch too small: need %zu bytes", r.scratch_bytes);
+    return fused_apply(x, B, C, g.H, g.W, g.Cp / g.C, pad, pad_mode, act, g.s, table,
+                       r.scratch_bytes > 0 ? scratch : nullptr, out, st);
   }
   if (!scratch || scratch_bytes < r.scratch_bytes)
     return fail(CVN_ERR_WORKSPACE, "scratch too small: need %zu bytes", r.scratch_bytes);

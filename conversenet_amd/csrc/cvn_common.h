@@ -137,8 +137,13 @@ inline bool make_plan(int L, FftPlan* plan) {
 int fused_query(int H, int W, int pad, int scale, int64_t Cp, size_t* ws_bytes);
 int fused_table(const float* psf, const float* bias, float eps, int64_t C, int64_t psf_batch, int kh, int kw,
                 int H, int W, int pad, int scale, void* table, hipStream_t st);
+// Scratch that lets fused_apply split each plane over two workgroups (one per row group; at most
+// kFusedSplitPlanes planes, where one workgroup per plane leaves most CUs idle); 0 where no split applies.
+constexpr int64_t kFusedSplitPlanes = 128;
+size_t fused_scratch(int64_t planes, int H, int W, int pad, int scale);
+// scratch: null, or at least fused_scratch(B C, ...) bytes (then small plane counts run split)
 int fused_apply(const float* x, int64_t B, int64_t C, int H, int W, int64_t psf_batch, int pad, int mode, int act,
-                int scale, const void* table, float* out, hipStream_t st);
+                int scale, const void* table, void* scratch, float* out, hipStream_t st);
 // 268 x 268 planes at scale 1 (converse2d_pfa.hip): in-place prime-factor FFTs 268 = 4 * 67 with an
 // in-register Rader 67-point DFT.
 bool pfa268_applies(int h, int w, int s);

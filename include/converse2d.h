@@ -106,7 +106,9 @@ int cvn_converse2d_supported(int64_t B, int64_t C, int64_t H, int64_t W, int64_t
  * route's table), so a table is never read in a layout it was not written in.  The table depends on
  * (psf, psf_batch, bias, eps, C, H, W, scale, pad, route) and, for psf_batch = B, on B.
  * cvn_converse2d_fwd_f32 == table into workspace[0, align256(table_bytes)) + apply with the rest, on
- * the route cvn_converse2d_route() picks. */
+ * the route cvn_converse2d_route() picks.  On CVN_ROUTE_FUSED the scratch may be null: with at most
+ * 128 planes (B C) the route asks for scratch_bytes > 0 so that each plane's two row groups can run in
+ * workgroups of their own (twice the CUs busy); given null, the apply runs one workgroup per plane. */
 size_t cvn_converse2d_table_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch,
                                   int kh, int kw, int scale, int pad, int route);
 size_t cvn_converse2d_scratch_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch,

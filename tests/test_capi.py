@@ -108,6 +108,15 @@ def test_explicit_route_must_serve_geometry_and_table_size_is_checked():
     rc = lib.cvn_converse2d_apply_f32(dummy, B, C, H, W, pb, kh, kw, s, p, 3, 0, _lib.ROUTE_GENERIC, dummy, tb - 1,
                                       dummy, sb, dummy, None)
     assert rc == _lib.CVN_ERR_ARG and b"table" in lib.cvn_last_error()
+    # the fused route asks for scratch only where it splits planes over two workgroups (<= 128 planes)
+    assert lib.cvn_converse2d_scratch_bytes(1, 64, 128, 128, 1, 5, 5, 1, 2, _lib.ROUTE_FUSED) > 0
+    assert lib.cvn_converse2d_scratch_bytes(2, 64, 128, 128, 1, 5, 5, 1, 2, _lib.ROUTE_FUSED) > 0
+    assert lib.cvn_converse2d_scratch_bytes(3, 43, 128, 128, 1, 5, 5, 1, 2, _lib.ROUTE_FUSED) == 0
+    assert lib.cvn_converse2d_scratch_bytes(16, 64, 256, 256, 1, 5, 5, 1, 2, _lib.ROUTE_FUSED) == 0
+    assert lib.cvn_converse2d_scratch_bytes(8, 64, 64, 64, 1, 3, 3, 2, 1, _lib.ROUTE_FUSED) == 0  # scale 2
+    g1 = (1, 64, 128, 128, 1, 5, 5, 1, 2)
+    assert lib.cvn_converse2d_fwd_workspace(*g1) >= (lib.cvn_converse2d_table_bytes(*g1, _lib.ROUTE_FUSED)
+                                                     + lib.cvn_converse2d_scratch_bytes(*g1, _lib.ROUTE_FUSED))
     # the fused (260^2) and 268 tables differ from the generic table of the same geometry
     g260 = (16, 64, 256, 256, 1, 5, 5, 1, 2)
     assert lib.cvn_converse2d_table_bytes(*g260, _lib.ROUTE_FUSED) != lib.cvn_converse2d_table_bytes(

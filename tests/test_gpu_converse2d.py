@@ -225,6 +225,61 @@ def test_fused_256_cooley_tukey(B, C, H, p, mode, k, ps, act, monkeypatch):
     assert np.abs(fused - generic).max() <= TOL
 
 
+SPLIT_CASES = [
+    # B, C, H, p, mode, k, per-sample psf, act (padded sides 132, 256 and 260)
+    (1, 5, 128, 2, "circular", 5, False, None),      # 5 planes: a partly filled block of 8
+    (2, 64, 128, 2, "reflect", 3, False, "gelu"),    # 128 planes: the largest split
+    (1, 129, 128, 2, "circular", 5, False, None),    # 129 planes: one workgroup per plane
+    (3, 3, 252, 2, "replicate", 5, True, None),      # Cooley-Tukey 256 plan, per-sample psf
+    (1, 130, 252, 2, "circular", 5, False, None),    # ... above the split limit
+    (1, 9, 256, 2, "circular", 5, False, None),      # 260 plan
+    (2, 3, 260, 0, "constant", 5, False, "gelu"),    # 260 plan, rows past 256 columns
+]
+
+
+@pytest.mark.parametrize("B,C,H,p,mode,k,ps,act", SPLIT_CASES)
+def test_fused_split_small_plane_counts(B, C, H, p, mode, k, ps, act, monkeypatch):
+    """At most 128 planes on the fused route: the route asks for scratch, and with it each plane's two
+    row groups run in workgroups of their own (a forward kernel writing the group spectra, an inverse
+    kernel combining them); given no scratch, the apply runs one workgroup per plane.  Both against the
+    fp64 oracle, and against each other."""
+    from conversenet_amd import _lib
+    from conversenet_amd import functional as Fh
+    lib = _lib.load()
+    rng = seeded("split", B, C, H, p, mode, k, ps, act)
+    x = rng.standard_normal((B, C, H, H)).astype(np.float32)
+    w = softmax_psf(rng, C, k, batch=B if ps else 1)
+    b = (0.4 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    eps = 1e-3 if ps else 1e-5
+    pb = w.shape[0]
+    monkeypatch.delenv("CVN_DISABLE_FUSED", raising=False)
+    geo = (B, C, H, H, pb, k, k, 1, p)
+    assert lib.cvn_converse2d_route(*geo) == _lib.ROUTE_FUSED
+    sb = lib.cvn_converse2d_scratch_bytes(*geo, _lib.ROUTE_FUSED)
+    assert (sb > 0) == (B * C <= 128)
+    ref = O.converse2d_module(x, w, b, 1, p, mode, eps)
+    if act:
+        ref = O.gelu(ref)
+    dev = torch.device("cuda")
+    xt, wt, bt = (torch.from_numpy(a).to(dev) for a in (x, w, b.reshape(-1)))
+    split = Fh.converse2d_fused(xt, wt, bt, 1, p, mode, eps, act=act).cpu().numpy()
+    tb = lib.cvn_converse2d_table_bytes(*geo, _lib.ROUTE_FUSED)
+    table = torch.empty(tb, dtype=torch.uint8, device=dev)
+    out = torch.empty_like(xt)
+    st = torch.cuda.current_stream().cuda_stream
+    assert lib.cvn_converse2d_table_f32(wt.data_ptr(), pb, k, k, bt.data_ptr(), eps, B, C, H, H, 1, p,
+                                        _lib.ROUTE_FUSED, table.data_ptr(), tb, st) == 0
+    assert lib.cvn_converse2d_apply_f32(xt.data_ptr(), B, C, H, H, pb, k, k, 1, p, _lib.PAD_MODES[mode],
+                                        _lib.ACT_GELU if act else _lib.ACT_NONE, _lib.ROUTE_FUSED,
+                                        table.data_ptr(), tb, None, 0, out.data_ptr(), st) == 0
+    whole = out.cpu().numpy()
+    e_split, e_whole = np.abs(split - ref).max(), np.abs(whole - ref).max()
+    print(f"fused {H + 2 * p}^2 B{B} C{C} {mode} k{k} per-sample {ps} act {act}: split {e_split:.3e}, "
+          f"one workgroup per plane {e_whole:.3e}")
+    assert e_split <= TOL and e_whole <= TOL
+    assert np.abs(split - whole).max() <= 1e-5
+
+
 @pytest.mark.parametrize("H,p", [(256, 2), (128, 2)])
 def test_fused_matches_generic_path(H, p, monkeypatch):
     """The fused single-kernel path and the generic multi-pass path agree (both vs the oracle)."""
