@@ -755,28 +755,32 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
   group_forward_passes<P>(buf, pa, pb, tid);
   // radix-2 across the groups, transfer function, inverse radix-2.  Table entries come in batches
   // of kTabBatch slots; the first batch is requested before G1's last pass.
-  float4 f4[kTabBatch];
+  // Batches are double-buffered: batch b + 1 is requested before batch b is combined.
+  constexpr int NB = (P::PARK + kTabBatch - 1) / kTabBatch;
+  float4 f4[2][kTabBatch];
 #pragma unroll
-  for (int i = 0; i < kTabBatch; ++i) f4[i] = bload4(t4r, 16u * tid, 16u * i * kFT);
+  for (int i = 0; i < kTabBatch; ++i) f4[0][i] = bload4(t4r, 16u * tid, 16u * i * kFT);
   col_pass_b<P, false>(buf, pa, pb, tid);
   lds_barrier();
 #pragma unroll
-  for (int i0 = 0; i0 < P::PARK; i0 += kTabBatch) {
-    if (i0 > 0) {
+  for (int bt = 0; bt < NB; ++bt) {
+    const int j = bt & 1;
+    if (bt + 1 < NB) {
 #pragma unroll
-      for (int i = 0; i < kTabBatch; ++i) f4[i] = bload4(t4r, 16u * tid, 16u * (i0 + i) * kFT);
+      for (int i = 0; i < kTabBatch; ++i)
+        f4[j ^ 1][i] = bload4(t4r, 16u * tid, 16u * ((bt + 1) * kTabBatch + i) * kFT);
     }
 #pragma unroll
     for (int i = 0; i < kTabBatch; ++i) {
-      const int ii = i0 + i;
+      const int ii = bt * kTabBatch + i;
       if (ii < P::PARK) {
         const int s = tid + ii * kFT;
         const int t = s / P::RS;
         const float2 w = wtab[2 * t + isb[s - t * P::RS]];  // radix-2 twiddle of the slot's row frequency
         const float2 e = ii < PL ? parkl[ii * kFT + tid] : park[ii < PL ? 0 : ii - PL], o = buf[s];
         const float2 wo = cmul(w, o);
-        const float2 y0 = cmul(make_float2(f4[i].x, f4[i].y), cadd(e, wo));
-        const float2 y1 = cmul(make_float2(f4[i].z, f4[i].w), csub(e, wo));
+        const float2 y0 = cmul(make_float2(f4[j][i].x, f4[j][i].y), cadd(e, wo));
+        const float2 y1 = cmul(make_float2(f4[j][i].z, f4[j][i].w), csub(e, wo));
         float2 ne = cadd(y0, y1);
         // materialise E' here: otherwise the compiler sinks its arithmetic to the unpark and keeps
         // e, o and the table entry alive across the G1 inverse
@@ -786,7 +790,7 @@ __global__ void __launch_bounds__(kFT) k_converse2d_fused(FusedArgs a) {
         buf[s] = cmul(cconj(w), csub(y0, y1));
       }
     }
-    asm volatile("" ::: "memory");  // the next batch's loads may not be hoisted above this one
+    asm volatile("" ::: "memory");  // the batch after next may not be hoisted above this one
   }
   lds_barrier();
   group_inverse_store<P, WIDE>(buf, pa, pb, pos, orsrc, a, 1, wave, lane, tid);

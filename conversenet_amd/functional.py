@@ -7,6 +7,8 @@ kernels on torch's current stream.  No CPU fallback exists here: a missing libra
 """
 from __future__ import annotations
 
+import os
+
 import torch
 
 from . import _lib, composite
@@ -28,9 +30,10 @@ def _need_hip(*ts):
             raise RuntimeError("conversenet_amd HIP path computes in float32")
 
 
-def _workspace(dev, nbytes: int):
-    """A reusable uint8 scratch tensor per (device, stream); grows monotonically."""
-    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+def _workspace(dev, nbytes: int, stream=None):
+    """A reusable uint8 scratch tensor per (device, stream); grows monotonically.  stream: the current
+    stream's handle when the caller has it already."""
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream if stream is None else stream)
     buf = _ws_cache.get(key)
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
@@ -122,6 +125,27 @@ def _cache_key(kind, weight, bias, eps, geo, route, dev):
             dev.index)
 
 
+_plan_memo: dict = {}
+
+
+def _module_plan(lib, B, C, H, W, pb, kh, kw, s, p):
+    """(route, table bytes, scratch bytes) of a module-level call: the library's answers depend only on
+    the geometry and CVN_DISABLE_FUSED, so they are asked once per geometry (three queries cost about as
+    much host time as a small layer's kernels)."""
+    key = (B, C, H, W, pb, kh, kw, s, p, os.environ.get("CVN_DISABLE_FUSED"))
+    plan = _plan_memo.get(key)
+    if plan is None:
+        route = lib.cvn_converse2d_route(B, C, H, W, pb, kh, kw, s, p)
+        if route < 0:
+            _lib.check(route, "converse2d_fused")
+        plan = (route, lib.cvn_converse2d_table_bytes(B, C, H, W, pb, kh, kw, s, p, route),
+                lib.cvn_converse2d_scratch_bytes(B, C, H, W, pb, kh, kw, s, p, route))
+        if len(_plan_memo) >= 1024:
+            _plan_memo.clear()
+        _plan_memo[key] = plan
+    return plan
+
+
 def converse2d_fused(x, weight, bias, scale=1, padding=2, padding_mode="circular", eps=1e-5, act=None,
                      cache=True):
     """Converse2D.forward (util_converse.py:142-192) in one library call: pad, solve, crop.
@@ -154,11 +178,7 @@ def converse2d_fused(x, weight, bias, scale=1, padding=2, padding_mode="circular
     if B == 0:
         return out
     p = int(padding)
-    route = lib.cvn_converse2d_route(B, C, H, W, pb, kh, kw, s, p)
-    if route < 0:
-        _lib.check(route, "converse2d_fused")
-    tb = lib.cvn_converse2d_table_bytes(B, C, H, W, pb, kh, kw, s, p, route)
-    sb = lib.cvn_converse2d_scratch_bytes(B, C, H, W, pb, kh, kw, s, p, route)
+    route, tb, sb = _module_plan(lib, B, C, H, W, pb, kh, kw, s, p)
     st = _stream(dev)
     key = None
     table = None
@@ -173,7 +193,7 @@ def converse2d_fused(x, weight, bias, scale=1, padding=2, padding_mode="circular
                                                 s, p, route, table.data_ptr(), tb, st), "converse2d transfer table")
         if key is not None:
             table_cache.put(key, table, (weight, bias))
-    scratch = _workspace(dev, sb) if sb > 0 else None
+    scratch = _workspace(dev, sb, st) if sb > 0 else None
     rc = lib.cvn_converse2d_apply_f32(
         x.data_ptr(), B, C, H, W, pb, kh, kw, s, p, _lib.PAD_MODES[padding_mode],
         _lib.ACT_GELU if act == "gelu" else _lib.ACT_NONE, route, table.data_ptr(), tb,
