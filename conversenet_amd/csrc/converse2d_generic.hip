@@ -290,10 +290,15 @@ __device__ PhiTileView phi_tile_prep(const PhiArgs& a, unsigned char* phl, int64
   t.P = (double2*)(phl + L.P);
   float* ps = (float*)(phl + L.psf);
 
+  // the psf's first kPsfRegs words per thread are requested here and written to LDS after the
+  // twiddle tables below, which do not depend on them, so the load latency overlaps their sincos work
+  constexpr int kPsfRegs = 4;
   const float* psf = a.psf + cp * kh * kw;
-  for (int e = tid; e < kh * kw4; e += nth) {
-    const int i = e / kw4, j = e - i * kw4;
-    ps[e] = j < kw ? psf[i * kw + j] : 0.f;
+  float pv[kPsfRegs];
+#pragma unroll
+  for (int r = 0; r < kPsfRegs; ++r) {
+    const int e = tid + r * nth, i = e / kw4, j = e - i * kw4;
+    pv[r] = (e < kh * kw4 && j < kw) ? psf[i * kw + j] : 0.f;
   }
   if (fast) {
     // split-DFT form: z^u only (Hs a multiple of 4: a quarter by sincospi, the rest by the exact
@@ -319,6 +324,13 @@ __device__ PhiTileView phi_tile_prep(const PhiArgs& a, unsigned char* phl, int64
     t.zW[e] = dexpi((double)vb, (double)Ws);
     t.phW[e] = dexpi(-(double)((vb * (kw / 2)) % Ws), (double)Ws);
     t.hW[e] = hold(S, vb, Ws);
+  }
+#pragma unroll
+  for (int r = 0; r < kPsfRegs; ++r)
+    if (tid + r * nth < kh * kw4) ps[tid + r * nth] = pv[r];
+  for (int e = tid + kPsfRegs * nth; e < kh * kw4; e += nth) {
+    const int i = e / kw4, j = e - i * kw4;
+    ps[e] = j < kw ? psf[i * kw + j] : 0.f;
   }
   __syncthreads();
   if (S > 1 && fast)
