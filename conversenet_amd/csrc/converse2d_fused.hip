@@ -1113,6 +1113,22 @@ template <> struct LrRadices<66> { static constexpr int n = 3, r0 = 2, r1 = 3, r
 template <> struct LrRadices<44> { static constexpr int n = 2, r0 = 4, r1 = 11, r2 = 1; };
 template <> struct LrRadices<33> { static constexpr int n = 2, r0 = 3, r1 = 11, r2 = 1; };
 
+// LR twiddles exp(-2 pi i m / L), m < L, twice (the row and the column transform of a square LR
+// plane), evaluated at compile time in double and rounded once.
+template <int L>
+struct alignas(16) LrTwTab {
+  float v[4 * L];
+  constexpr LrTwTab() : v() {
+    for (int m = 0; m < L; ++m) {
+      const CosSin cs = cos_sin_turn(m, L);
+      v[2 * m] = v[2 * (m + L)] = (float)cs.c;
+      v[2 * m + 1] = v[2 * (m + L) + 1] = (float)-cs.s;
+    }
+  }
+};
+template <int L>
+__device__ const LrTwTab<L> kLrTw = LrTwTab<L>();
+
 // The LR transform of `ntr` rows of length L (a -> b -> ...), compile-time radices; returns the buffer
 // holding the result.
 template <int L>
@@ -1145,13 +1161,14 @@ __global__ void __launch_bounds__(kFT, 8) k_converse2d_fused_up(FusedUpArgs ua) 
   short* pa = (short*)(wtab + P::NH + 2);
   short* pb = pa + P::NQ;
   short* pos = pb + P::NQ;
-  unsigned char* isb = (unsigned char*)(pos + 2 * P::M);
+  unsigned char* isb = (unsigned char*)(pos + P::M);  // the fused kernel's table block layout
   char* base = (char*)smem;
   float2* Y = (float2*)(base + ua.y_off);      // LR half spectrum, column-major: Y[v h + u]
   float2* twl = (float2*)(base + ua.tw_off);   // exp(-2 pi i m / w), m < w
   float2* twh = twl + w;                       // exp(-2 pi i m / h), m < h
   short* kof = (short*)(base + ua.idx_off);    // column frequency k of row position rp
   short* qof = kof + P::NH;                    // half-spectrum column q of a row-pair position
+  static_assert(tabs_layout_ok<P>() && w == h, "table block layout, square LR plane");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t plane = fused_plane(blockIdx.x, a);
@@ -1160,29 +1177,20 @@ __global__ void __launch_bounds__(kFT, 8) k_converse2d_fused_up(FusedUpArgs ua) 
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + plane * (int64_t)ua.Hl * ua.Wl, in_bytes);
   const __amdgpu_buffer_rsrc_t orsrc = make_rsrc(a.out + plane * (int64_t)a.H * a.W, out_bytes);
   const __amdgpu_buffer_rsrc_t t4r = make_rsrc(a.tab4 + cp * P::SLOTS, P::SLOTS * 16u);
-  // tables: radix-2 twiddles, slot positions, LR twiddles
-  for (int p = tid; p < P::RS; p += kFT) isb[p] = 0;
-  for (int k = tid; k < P::NH + 2; k += kFT) {
-    double sn = 0.0, cs = 0.0;
-    if (k < P::NH) sincospi(-2.0 * (double)k / (double)P::N, &sn, &cs);
-    wtab[k < P::NH ? P::rfpos(k) : k] = make_float2((float)cs, (float)sn);
-    if (k < P::NH) kof[P::rfpos(k)] = (short)k;
+  // tables: the compile-time block (radix-2 twiddles by row position, slot and in-row positions, the
+  // odd-row flags) and the LR twiddles, copied; the slot -> (k, q) maps
+  {
+    const v4u32_t* src = (const v4u32_t*)&kFusedTabs<P>;
+    v4u32_t* dst = (v4u32_t*)wtab;
+    for (int i = tid; i < P::CONST_BYTES / 16; i += kFT) dst[i] = src[i];
+    const float2* lt = (const float2*)kLrTw<w>.v;
+    for (int m = tid; m < w + h; m += kFT) twl[m] = lt[m];
   }
-  for (int m = tid; m < w + h; m += kFT) {
-    const int L = m < w ? w : h, mm = m < w ? m : m - w;
-    double sn, cs;
-    sincospi(-2.0 * (double)mm / (double)L, &sn, &cs);
-    twl[m] = make_float2((float)cs, (float)sn);
-  }
-  lds_barrier();
+  for (int k = tid; k < P::NH; k += kFT) kof[P::rfpos(k)] = (short)k;
   for (int q = tid; q < P::NQ; q += kFT) {
-    pa[q] = P::pa(q);
-    pb[q] = P::pb(q);
-    isb[P::pb(q)] = 1;
     qof[P::pa(q)] = (short)q;
     qof[P::pb(q)] = (short)q;
   }
-  for (int j = tid; j < P::M; j += kFT) pos[j] = P::pos_in(j);
   // LR padded plane as complex row pairs (row 2t in .x, 2t + 1 in .y) in buf
   float2* A = buf;
   float2* Bw = buf + npl * w;
