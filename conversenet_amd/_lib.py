@@ -66,9 +66,9 @@ SIGNATURES = {
                                   _ptr, _ptr]),
     "cvn_ln_mlp_residual_f32": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _f32, _ptr, _ptr, _i64, _ptr, _ptr,
                                        _ptr, _ptr, _ptr]),
-    "cvn_conv_ln_mlp_residual_f32": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr,
-                                            _f32, _ptr, _ptr, _i64, _ptr, _ptr, _ptr, _ptr, _ptr]),
-    "cvn_conv_ln_mlp_head_f32": (_int, [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr, _f32,
+    "cvn_conv_ln_mlp_residual_f32": (_int, [_ptr, _int, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _i64, _ptr,
+                                            _ptr, _f32, _ptr, _ptr, _i64, _ptr, _ptr, _ptr, _ptr, _ptr]),
+    "cvn_conv_ln_mlp_head_f32": (_int, [_ptr, _int, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _i64, _ptr, _ptr, _f32,
                                         _ptr, _ptr, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _f32, _ptr, _ptr,
                                         _ptr, _ptr]),
     "cvn_copy_f32": (_int, [_ptr, _ptr, _i64, _ptr]),

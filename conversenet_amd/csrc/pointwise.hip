@@ -565,6 +565,7 @@ struct TailArgs {
   const float *hlw, *hlb, *Wh, *bh;  // HEAD: next block's LayerNorm and 1x1 (CIN x C)
   float heps;
   float* th;  // HEAD: (B, CIN, HW)
+  int t_act;  // CVN_ACT_GELU: the first layer's input is GELU(t)
 };
 
 // Stores an accumulator-layout tile (channel 16 rb + 4 g + r, Q consecutive pixels per lane).
@@ -581,7 +582,7 @@ __device__ __forceinline__ void store_acc(const v4f (&v)[N / 16][Q], float* yw, 
     }
 }
 
-template <int CIN, int C, int CM, int Q, int NW, bool HEAD>
+template <int CIN, int C, int CM, int Q, int NW, bool HEAD, bool GIN>
 __global__ void __launch_bounds__(64 * NW) k_conv_ln_mlp_mfma(TailArgs a) {
   static_assert(CIN % 32 == 0 && C % 32 == 0 && CM % 32 == 0, "split-fp16 GEMM chunks");
   constexpr int NP = 6 * C + CM + (HEAD ? 2 * C + CIN : 0);
@@ -621,6 +622,14 @@ __global__ void __launch_bounds__(64 * NW) k_conv_ln_mlp_mfma(TailArgs a) {
     {
       v4f tv[CIN / 16][Q];
       load_acc<CIN, Q>(a.t + b * CIN * hw + pw, hw, inb, yoff, tv);
+      if (GIN) {  // t is the Converse2D output before its GELU
+#pragma unroll
+        for (int rb = 0; rb < CIN / 16; ++rb)
+#pragma unroll
+          for (int q = 0; q < Q; ++q)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) tv[rb][q][r] = gelu_f(tv[rb][q][r]);
+      }
       zero_acc<C, Q>(acc);
       gemm_f16s<CIN, C, Q>(tv, W0l, lane, acc);
     }
@@ -804,13 +813,15 @@ int launch_tail(TailArgs a, int64_t B, hipStream_t st) {
   constexpr int Q = 1, NW = 16;
   a.tpb = (a.HW + 16 * NW * Q - 1) / (16 * NW * Q);
   a.ntiles = B * a.tpb;
-  if (a.th) {
-    auto kern = k_conv_ln_mlp_mfma<CIN, C, CM, Q, NW, true>;
+  auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(persistent_grid(kern, 64 * NW, a.ntiles)), dim3(64 * NW), 0, st, a);
-  } else {
-    auto kern = k_conv_ln_mlp_mfma<CIN, C, CM, Q, NW, false>;
-    hipLaunchKernelGGL(kern, dim3(persistent_grid(kern, 64 * NW, a.ntiles)), dim3(64 * NW), 0, st, a);
-  }
+  };
+  if (a.th)
+    a.t_act == CVN_ACT_GELU ? go(k_conv_ln_mlp_mfma<CIN, C, CM, Q, NW, true, true>)
+                            : go(k_conv_ln_mlp_mfma<CIN, C, CM, Q, NW, true, false>);
+  else
+    a.t_act == CVN_ACT_GELU ? go(k_conv_ln_mlp_mfma<CIN, C, CM, Q, NW, false, true>)
+                            : go(k_conv_ln_mlp_mfma<CIN, C, CM, Q, NW, false, false>);
   return check_launch("fused block tail");
 }
 
@@ -922,6 +933,7 @@ static int tail_impl(TailArgs a, int64_t B, int64_t Ct, int64_t C, int64_t Cmid,
   if (!a.t || !a.W0 || !a.b0 || !a.x || !a.lw || !a.lb || !a.W1 || !a.b1 || !a.W2 || !a.b2 || !a.y)
     return fail(CVN_ERR_ARG, "null pointer");
   if (a.th && (!a.hlw || !a.hlb || !a.Wh || !a.bh)) return fail(CVN_ERR_ARG, "null pointer");
+  if (a.t_act != CVN_ACT_NONE && a.t_act != CVN_ACT_GELU) return fail(CVN_ERR_ARG, "bad activation %d", a.t_act);
   if (B < 0 || a.HW < 0) return fail(CVN_ERR_ARG, "bad shape");
   if (B > 65535) return fail(CVN_ERR_UNSUPPORTED, "batch exceeds 65535");
   if (a.t == a.y || (a.th && (a.th == a.x || a.th == a.y)))
@@ -934,25 +946,26 @@ static int tail_impl(TailArgs a, int64_t B, int64_t Ct, int64_t C, int64_t Cmid,
   return fail(CVN_ERR_UNSUPPORTED, "fused tail supports (Ct, C, Cmid) = (128, 64, 128)");
 }
 
-extern "C" int cvn_conv_ln_mlp_residual_f32(const float* t, int64_t B, int64_t Ct, int64_t HW, const float* w0,
-                                            const float* b0, const float* res_scale1, const float* x, int64_t C,
-                                            const float* ln_w, const float* ln_b, float ln_eps, const float* w1,
-                                            const float* b1, int64_t Cmid, const float* w2, const float* b2,
-                                            const float* res_scale2, float* y, cvn_stream_t stream) {
+extern "C" int cvn_conv_ln_mlp_residual_f32(const float* t, int t_act, int64_t B, int64_t Ct, int64_t HW,
+                                            const float* w0, const float* b0, const float* res_scale1,
+                                            const float* x, int64_t C, const float* ln_w, const float* ln_b,
+                                            float ln_eps, const float* w1, const float* b1, int64_t Cmid,
+                                            const float* w2, const float* b2, const float* res_scale2, float* y,
+                                            cvn_stream_t stream) {
   TailArgs a{t, x, HW, 0, 0, w0, b0, res_scale1, ln_w, ln_b, w1, b1, w2, b2, res_scale2, ln_eps, y,
-             nullptr, nullptr, nullptr, nullptr, 0.f, nullptr};
+             nullptr, nullptr, nullptr, nullptr, 0.f, nullptr, t_act};
   return tail_impl(a, B, Ct, C, Cmid, (hipStream_t)stream);
 }
 
-extern "C" int cvn_conv_ln_mlp_head_f32(const float* t, int64_t B, int64_t Ct, int64_t HW, const float* w0,
-                                        const float* b0, const float* res_scale1, const float* x, int64_t C,
-                                        const float* ln_w, const float* ln_b, float ln_eps, const float* w1,
-                                        const float* b1, int64_t Cmid, const float* w2, const float* b2,
-                                        const float* res_scale2, float* y, const float* head_ln_w,
+extern "C" int cvn_conv_ln_mlp_head_f32(const float* t, int t_act, int64_t B, int64_t Ct, int64_t HW,
+                                        const float* w0, const float* b0, const float* res_scale1, const float* x,
+                                        int64_t C, const float* ln_w, const float* ln_b, float ln_eps,
+                                        const float* w1, const float* b1, int64_t Cmid, const float* w2,
+                                        const float* b2, const float* res_scale2, float* y, const float* head_ln_w,
                                         const float* head_ln_b, float head_ln_eps, const float* head_w,
                                         const float* head_b, float* t_next, cvn_stream_t stream) {
   TailArgs a{t, x, HW, 0, 0, w0, b0, res_scale1, ln_w, ln_b, w1, b1, w2, b2, res_scale2, ln_eps, y,
-             head_ln_w, head_ln_b, head_w, head_b, head_ln_eps, t_next};
+             head_ln_w, head_ln_b, head_w, head_b, head_ln_eps, t_next, t_act};
   if (!t_next) return fail(CVN_ERR_ARG, "null pointer");
   return tail_impl(a, B, Ct, C, Cmid, (hipStream_t)stream);
 }

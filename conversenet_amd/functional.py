@@ -146,6 +146,13 @@ def _module_plan(lib, B, C, H, W, pb, kh, kw, s, p):
     return plan
 
 
+def module_route(shape, weight, scale, padding):
+    """The library's route (_lib.ROUTE_*) for a module-level call on an input of `shape` (B, C, H, W)."""
+    B, C, H, W = (int(v) for v in shape)
+    return _module_plan(_lib.load(), B, C, H, W, int(weight.shape[0]), int(weight.shape[2]), int(weight.shape[3]),
+                        int(scale), int(padding))[0]
+
+
 def converse2d_fused(x, weight, bias, scale=1, padding=2, padding_mode="circular", eps=1e-5, act=None,
                      cache=True):
     """Converse2D.forward (util_converse.py:142-192) in one library call: pad, solve, crop.
@@ -421,8 +428,9 @@ TAIL_SHAPES = {(128, 64, 128)}  # (Ct, C, Cmid) of cvn_conv_ln_mlp_residual_f32
 
 
 def conv_ln_mlp_residual(t, x, w0, b0, ln_w, ln_b, ln_eps, w1, b1, w2, b2, res_scale1=None, res_scale2=None,
-                         out=None, head=None):
-    """ConverseBlock tail: y' = x + res_scale1 (W0 t + b0); y = y' + res_scale2 (W2 GELU(W1 LN(y') + b1) + b2).
+                         out=None, head=None, t_act=None):
+    """ConverseBlock tail: y' = x + res_scale1 (W0 a(t) + b0); y = y' + res_scale2 (W2 GELU(W1 LN(y') + b1) + b2),
+    a(t) = GELU(t) for t_act='gelu' (t the Converse2D output before the block's GELU), else t.
     With head = (ln_w, ln_b, ln_eps, w, b) of the next block, also returns its Converse2D input
     GELU(w LN(y) + b): (y, t_next); otherwise y."""
     lib = _lib.load()
@@ -434,7 +442,8 @@ def conv_ln_mlp_residual(t, x, w0, b0, ln_w, ln_b, ln_eps, w1, b1, w2, b2, res_s
     W0, W1, W2 = _wmat(w0), _wmat(w1), _wmat(w2)
     y = out if out is not None else torch.empty_like(x)
     ptr = lambda v: v.contiguous().data_ptr() if v is not None else None
-    common = (t.data_ptr(), B, Ct, H * W, W0.data_ptr(), ptr(b0), ptr(res_scale1), x.data_ptr(), C, ptr(ln_w),
+    act = _lib.ACT_GELU if t_act == "gelu" else _lib.ACT_NONE
+    common = (t.data_ptr(), act, B, Ct, H * W, W0.data_ptr(), ptr(b0), ptr(res_scale1), x.data_ptr(), C, ptr(ln_w),
               ptr(ln_b), float(ln_eps), W1.data_ptr(), ptr(b1), W1.shape[0], W2.data_ptr(), ptr(b2), ptr(res_scale2),
               y.data_ptr())
     if head is None:

@@ -239,15 +239,27 @@ def _block_head(parts, x):
     return functional.conv1x1(x, c11.weight, c11.bias, act="gelu", ln=(ln1.weight, ln1.bias, ln1.eps))
 
 
-def _block_converse(parts, t):
+def _block_converse(parts, t, act="gelu"):
     cv = parts[2]
     cv.biaseps = None  # read lazily from the current bias
     return functional.converse2d_fused(t, cv.weight, cv.bias.reshape(-1), cv.scale, cv.padding, cv.padding_mode,
-                                       cv.eps, act="gelu")
+                                       cv.eps, act=act)
 
 
-def _block_tail(parts, t, x, next_parts=None):
+def _gelu_in_tail(parts, t_shape, x):
+    """Whether the block's GELU after its Converse2D (util_converse.py:281) is applied as the fused
+    tail loads its input instead of as the Converse2D stores its output: on the 268 path, whose
+    inverse row pass is bound by VALU issue at three waves per SIMD (there the GELU costs about 24 us
+    of a 0.47 ms layer at Converse-DnCNN's shape; in the tail, about 10 us)."""
+    _, _, cv, c15, _, c21, _, _ = parts
+    if (c15.in_channels, c15.out_channels, c21.out_channels) not in functional.TAIL_SHAPES or x.data_ptr() % 16:
+        return False
+    return functional.module_route(t_shape, cv.weight, cv.scale, cv.padding) == _lib.ROUTE_PFA268
+
+
+def _block_tail(parts, t, x, next_parts=None, t_act=None):
     """1x1 + residual and the LN-MLP branch + residual; with next_parts also the next block's head.
+    t_act='gelu': t is the Converse2D output before the block's GELU.
     Returns (block output, next block's Converse2D input or None)."""
     _, _, _, c15, ln2, c21, c23, (s1, s2) = parts
     mid, C = c15.in_channels, c15.out_channels
@@ -257,10 +269,13 @@ def _block_tail(parts, t, x, next_parts=None):
             nln, nc11 = next_parts[0], next_parts[1]
             return functional.conv_ln_mlp_residual(t, x, c15.weight, c15.bias, ln2.weight, ln2.bias, ln2.eps,
                                                    c21.weight, c21.bias, c23.weight, c23.bias, s1, s2,
-                                                   head=(nln.weight, nln.bias, nln.eps, nc11.weight, nc11.bias))
+                                                   head=(nln.weight, nln.bias, nln.eps, nc11.weight, nc11.bias),
+                                                   t_act=t_act)
         y = functional.conv_ln_mlp_residual(t, x, c15.weight, c15.bias, ln2.weight, ln2.bias, ln2.eps,
-                                            c21.weight, c21.bias, c23.weight, c23.bias, s1, s2)
+                                            c21.weight, c21.bias, c23.weight, c23.bias, s1, s2, t_act=t_act)
         return y, None
+    if t_act == "gelu":
+        t = torch.nn.functional.gelu(t)
     x = functional.conv1x1(t, c15.weight, c15.bias, residual=x, res_scale=s1)
     y = functional.ln_mlp_residual(x, ln2.weight, ln2.bias, ln2.eps, c21.weight, c21.bias, c23.weight, c23.bias,
                                    res_scale=s2, out=x)
@@ -280,7 +295,9 @@ def _fused_block_forward(blk, x, alpha1=None, alpha2=None):
     parts = _block_parts(blk)
     if parts is None or (x.shape[2] * x.shape[3]) % 4 != 0 or not _parts_supported(parts, x):
         return None
-    return _block_tail(parts, _block_converse(parts, _block_head(parts, x)), x)[0]
+    t = _block_head(parts, x)
+    gin = _gelu_in_tail(parts, t.shape, x)
+    return _block_tail(parts, _block_converse(parts, t, None if gin else "gelu"), x, t_act="gelu" if gin else None)[0]
 
 
 def run_blocks(blocks, x):
@@ -299,8 +316,9 @@ def run_blocks(blocks, x):
         return x
     t = _block_head(parts[0], x)
     for i, p in enumerate(parts):
-        t = _block_converse(p, t)
-        x, t_next = _block_tail(p, t, x, parts[i + 1] if i + 1 < len(parts) else None)
+        gin = _gelu_in_tail(p, t.shape, x)
+        t = _block_converse(p, t, None if gin else "gelu")
+        x, t_next = _block_tail(p, t, x, parts[i + 1] if i + 1 < len(parts) else None, "gelu" if gin else None)
         t = t_next if t_next is not None else (_block_head(parts[i + 1], x) if i + 1 < len(parts) else None)
     return x
 

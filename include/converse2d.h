@@ -192,26 +192,28 @@ int cvn_ln_mlp_residual_f32(const float* x, int64_t B, int64_t C, int64_t HW, co
                             const float* res_scale, float* y, cvn_stream_t stream);
 
 /* The ConverseBlock tail in one call (util_converse.py:279-293; alpha-scaled :309-323): the first
- * branch's last 1x1 and residual, y' = x + res_scale1 * (w0 t + b0), then the conv2 branch,
- * y = y' + res_scale2 * (W2 GELU(W1 LN(y') + b1) + b2); y' never reaches memory.  t: (B,Ct,HW)
- * (the GELU of the Converse2D output), x, y: (B,C,HW) (y may alias x, not t), w0: (C,Ct),
+ * branch's last 1x1 and residual, y' = x + res_scale1 * (w0 a(t) + b0), then the conv2 branch,
+ * y = y' + res_scale2 * (W2 GELU(W1 LN(y') + b1) + b2); y' never reaches memory.  t: (B,Ct,HW);
+ * t_act = CVN_ACT_GELU: a(t) = GELU(t) (t is the Converse2D output, the block's GELU applied here
+ * instead of on the Converse2D's store), CVN_ACT_NONE: a(t) = t (t already holds that GELU).
+ * x, y: (B,C,HW) (y may alias x, not t), w0: (C,Ct),
  * w1: (Cmid,C), w2: (C,Cmid), res_scale1/2: (C) or NULL.  Instantiated for (Ct, C, Cmid) =
  * (128, 64, 128), the shape of Converse-DnCNN's and Converse-USRNet's blocks; other shapes return
  * CVN_ERR_UNSUPPORTED (use cvn_conv1x1_f32 + cvn_ln_mlp_residual_f32). */
-int cvn_conv_ln_mlp_residual_f32(const float* t, int64_t B, int64_t Ct, int64_t HW, const float* w0,
-                                 const float* b0, const float* res_scale1, const float* x, int64_t C,
-                                 const float* ln_w, const float* ln_b, float ln_eps, const float* w1,
-                                 const float* b1, int64_t Cmid, const float* w2, const float* b2,
-                                 const float* res_scale2, float* y, cvn_stream_t stream);
+int cvn_conv_ln_mlp_residual_f32(const float* t, int t_act, int64_t B, int64_t Ct, int64_t HW,
+                                 const float* w0, const float* b0, const float* res_scale1, const float* x,
+                                 int64_t C, const float* ln_w, const float* ln_b, float ln_eps,
+                                 const float* w1, const float* b1, int64_t Cmid, const float* w2,
+                                 const float* b2, const float* res_scale2, float* y, cvn_stream_t stream);
 /* The same tail followed by the next block's first layer (util_converse.py:278-280, LN -> 1x1 -> GELU),
  * for chains of blocks (converse_dncnn.py:24, converse_usrnet.py:19-33): additionally
  * t_next = GELU(head_w LN_head(y) + head_b), (B,Ct,HW), head_w: (Ct,C).  t_next may alias
  * neither x nor y. */
-int cvn_conv_ln_mlp_head_f32(const float* t, int64_t B, int64_t Ct, int64_t HW, const float* w0,
-                             const float* b0, const float* res_scale1, const float* x, int64_t C,
-                             const float* ln_w, const float* ln_b, float ln_eps, const float* w1,
-                             const float* b1, int64_t Cmid, const float* w2, const float* b2,
-                             const float* res_scale2, float* y, const float* head_ln_w,
+int cvn_conv_ln_mlp_head_f32(const float* t, int t_act, int64_t B, int64_t Ct, int64_t HW,
+                             const float* w0, const float* b0, const float* res_scale1, const float* x,
+                             int64_t C, const float* ln_w, const float* ln_b, float ln_eps,
+                             const float* w1, const float* b1, int64_t Cmid, const float* w2,
+                             const float* b2, const float* res_scale2, float* y, const float* head_ln_w,
                              const float* head_ln_b, float head_ln_eps, const float* head_w,
                              const float* head_b, float* t_next, cvn_stream_t stream);
 

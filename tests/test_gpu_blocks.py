@@ -184,6 +184,33 @@ def test_conv_ln_mlp_head_fused():
     assert np.abs(_n(tn) - tref).max() <= TOL
 
 
+@pytest.mark.parametrize("head", [False, True])
+def test_conv_ln_mlp_gelu_on_input(head):
+    """t_act='gelu': the tail applies the block's GELU to t as it loads it (the 268 path's Converse2D
+    then stores its output without GELU), against the oracle on GELU(t)."""
+    from conversenet_amd import functional as Fh
+    rng = seeded("tail-gelu-in", head)
+    B, C, Ct, mid, H, W = 2, 64, 128, 128, 20, 26
+    f = lambda *sh, sc=1.0: (rng.standard_normal(sh) * sc).astype(np.float32)
+    t, x = f(B, Ct, H, W, sc=2.0), f(B, C, H, W)
+    w0, b0 = f(C, Ct, 1, 1, sc=Ct ** -0.5), f(C)
+    lw, lb, w1, b1 = f(C), f(C), f(mid, C, 1, 1, sc=C ** -0.5), f(mid)
+    w2, b2, s1, s2 = f(C, mid, 1, 1, sc=mid ** -0.5), f(C), f(C), f(C)
+    hlw, hlb, wh, bh = f(C), f(C), f(Ct, C, 1, 1, sc=C ** -0.5), f(Ct)
+    hd = (_t(hlw), _t(hlb), 1e-6, _t(wh), _t(bh)) if head else None
+    got = Fh.conv_ln_mlp_residual(_t(t), _t(x), _t(w0), _t(b0), _t(lw), _t(lb), 1e-5, _t(w1), _t(b1), _t(w2),
+                                  _t(b2), _t(s1), _t(s2), head=hd, t_act="gelu")
+    y, tn = got if head else (got, None)
+    y1 = s1[None, :, None, None] * O.conv1x1(O.gelu(t), w0, b0) + x
+    ref = s2[None, :, None, None] * O.conv1x1(O.gelu(O.conv1x1(O.layernorm_cf(y1, lw, lb, 1e-5), w1, b1)), w2, b2) + y1
+    err = np.abs(_n(y) - ref).max()
+    print(f"tail with GELU on its input, head {head}: max-abs {err:.3e}")
+    assert err <= TOL
+    if head:
+        tref = O.gelu(O.conv1x1(O.layernorm_cf(ref, hlw, hlb, 1e-6), wh, bh))
+        assert np.abs(_n(tn) - tref).max() <= TOL
+
+
 # ------------------------------------------------------------------------------------------------
 # a15 ConverseBlock / ConverseBlockAlphaVariant (fused block path on the GPU)
 # ------------------------------------------------------------------------------------------------
