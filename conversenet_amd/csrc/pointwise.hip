@@ -708,34 +708,63 @@ __global__ void __launch_bounds__(64 * NW) k_conv_ln_mlp_mfma(TailArgs a) {
 // or pixel counts that are not a multiple of 4).  Thread = one pixel and a group of kOutGroup
 // output channels (grid z); each input channel value is loaded once and feeds the whole group.
 constexpr int kOutGroup = 8;
+template <int PX>
 __global__ void __launch_bounds__(256) k_conv1x1_any(const float* __restrict__ x, int64_t HW, int Cin,
                                                      const float* __restrict__ W, const float* __restrict__ bias,
                                                      int Cout, int act, const float* residual,
                                                      const float* __restrict__ res_scale, float* y) {
-  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  // PX consecutive pixels per thread (4: one float4 per channel when HW % 4 == 0 and the buffers are
+  // 16-byte aligned); the input-channel loop is unrolled so that several loads are in flight at once
+  const int64_t p = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * PX;
   if (p >= HW) return;
   const int64_t b = blockIdx.y;
   const int o0 = blockIdx.z * kOutGroup;
   const int no = min(kOutGroup, Cout - o0);
   const float* xb = x + b * Cin * HW + p;
-  float acc[kOutGroup];
+  float acc[kOutGroup][PX];
 #pragma unroll
-  for (int k = 0; k < kOutGroup; ++k) acc[k] = (k < no && bias) ? bias[o0 + k] : 0.f;
+  for (int k = 0; k < kOutGroup; ++k)
+#pragma unroll
+    for (int j = 0; j < PX; ++j) acc[k][j] = (k < no && bias) ? bias[o0 + k] : 0.f;
+#pragma unroll 8
   for (int c = 0; c < Cin; ++c) {
-    const float xv = xb[(int64_t)c * HW];
+    float xv[PX];
+    if constexpr (PX == 4) {
+      const float4 v = *(const float4*)(xb + (int64_t)c * HW);
+      xv[0] = v.x; xv[1] = v.y; xv[2] = v.z; xv[3] = v.w;
+    } else {
+      xv[0] = xb[(int64_t)c * HW];
+    }
 #pragma unroll
     for (int k = 0; k < kOutGroup; ++k)
-      if (k < no) acc[k] = fmaf(W[(o0 + k) * Cin + c], xv, acc[k]);
+      if (k < no) {
+        const float wk = W[(o0 + k) * Cin + c];
+#pragma unroll
+        for (int j = 0; j < PX; ++j) acc[k][j] = fmaf(wk, xv[j], acc[k][j]);
+      }
   }
 #pragma unroll
   for (int k = 0; k < kOutGroup; ++k) {
     if (k >= no) break;
     const int o = o0 + k;
-    float v = acc[k];
-    if (act == CVN_ACT_GELU) v = gelu_f(v);
     const int64_t oi = (b * Cout + o) * HW + p;
-    if (residual) v = fmaf(res_scale ? res_scale[o] : 1.f, v, residual[oi]);
-    y[oi] = v;
+    float v[PX];
+#pragma unroll
+    for (int j = 0; j < PX; ++j) {
+      v[j] = acc[k][j];
+      if (act == CVN_ACT_GELU) v[j] = gelu_f(v[j]);
+    }
+    if (residual) {
+      const float sc = res_scale ? res_scale[o] : 1.f;
+      if constexpr (PX == 4) {
+        const float4 r = *(const float4*)(residual + oi);
+        v[0] = fmaf(sc, v[0], r.x); v[1] = fmaf(sc, v[1], r.y); v[2] = fmaf(sc, v[2], r.z); v[3] = fmaf(sc, v[3], r.w);
+      } else {
+        v[0] = fmaf(sc, v[0], residual[oi]);
+      }
+    }
+    if constexpr (PX == 4) *(float4*)(y + oi) = make_float4(v[0], v[1], v[2], v[3]);
+    else y[oi] = v[0];
   }
 }
 
@@ -888,9 +917,15 @@ static int conv_impl(const float* x, int64_t B, int64_t Cin, int64_t HW, const f
   }
   if (ln_w) return fail(CVN_ERR_UNSUPPORTED, "LayerNorm-fused 1x1 conv needs an MFMA tile shape");
   if ((Cout + kOutGroup - 1) / kOutGroup > 65535) return fail(CVN_ERR_UNSUPPORTED, "too many output channels");
-  dim3 grid((unsigned)((HW + 255) / 256), (unsigned)B, (unsigned)((Cout + kOutGroup - 1) / kOutGroup));
-  hipLaunchKernelGGL(k_conv1x1_any, grid, dim3(256), 0, st, x, HW, (int)Cin, weight, bias, (int)Cout, act,
-                     residual, res_scale, y);
+  const bool vec = HW % 4 == 0 && aligned16(x) && aligned16(y) && (!residual || aligned16(residual));
+  const int px = vec ? 4 : 1;
+  dim3 grid((unsigned)((HW / px + 255) / 256), (unsigned)B, (unsigned)((Cout + kOutGroup - 1) / kOutGroup));
+  if (vec)
+    hipLaunchKernelGGL(k_conv1x1_any<4>, grid, dim3(256), 0, st, x, HW, (int)Cin, weight, bias, (int)Cout, act,
+                       residual, res_scale, y);
+  else
+    hipLaunchKernelGGL(k_conv1x1_any<1>, grid, dim3(256), 0, st, x, HW, (int)Cin, weight, bias, (int)Cout, act,
+                       residual, res_scale, y);
   return check_launch("1x1 conv");
 }
 

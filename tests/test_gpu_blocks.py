@@ -63,6 +63,28 @@ def test_conv1x1(cin, cout, act):
     assert np.abs(got - ref).max() <= TOL
 
 
+@pytest.mark.parametrize("cin,cout", [(1, 64), (64, 1), (3, 64), (64, 3)])
+@pytest.mark.parametrize("HW,res", [((15, 17), False), ((16, 16), True), ((15, 17), True)])
+def test_conv1x1_generic_kernel_paths(cin, cout, HW, res):
+    """The VALU 1x1 kernel for channel counts without an MFMA tile: four pixels per thread (float4)
+    when HW % 4 == 0, one otherwise; with and without a scaled residual."""
+    from conversenet_amd import functional as Fh
+    rng = seeded("c11-any", cin, cout, HW, res)
+    B = 2
+    x = rng.standard_normal((B, cin) + HW).astype(np.float32)
+    w = (rng.standard_normal((cout, cin, 1, 1)) / np.sqrt(cin)).astype(np.float32)
+    b = rng.standard_normal(cout).astype(np.float32)
+    r = rng.standard_normal((B, cout) + HW).astype(np.float32)
+    a = rng.standard_normal(cout).astype(np.float32)
+    if res:
+        got = _n(Fh.conv1x1(_t(x), _t(w), _t(b), residual=_t(r), res_scale=_t(a)))
+        ref = a[None, :, None, None] * O.conv1x1(x, w, b) + r
+    else:
+        got = _n(Fh.conv1x1(_t(x), _t(w), _t(b), act="gelu"))
+        ref = O.gelu(O.conv1x1(x, w, b))
+    assert np.abs(got - ref).max() <= TOL
+
+
 @pytest.mark.parametrize("HW", [(16, 16), (15, 17)])  # vector (HW % 4 == 0) and scalar paths
 def test_conv1x1_residual_scale_and_ln_prologue(HW):
     from conversenet_amd import functional as Fh
