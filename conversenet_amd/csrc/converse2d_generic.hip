@@ -548,7 +548,10 @@ __device__ void phi_tile_rows16(const PhiArgs& a, int op, const PhiTileView& tv,
   }
 }
 
-template <int S>
+// FAST: the split-DFT form (phi_rows16 holds; the host checks it), a separate instantiation so that
+// the Horner form's registers (S^2 complex K values per item) do not set its occupancy: at S = 4,
+// 130 instead of 220 VGPRs, three waves per SIMD instead of two.
+template <int S, bool FAST>
 __global__ void __launch_bounds__(256) k_phi_tile(PhiArgs a, int op, int vc, int nchunk) {
   extern __shared__ __align__(16) unsigned char phl[];
   const int tid = threadIdx.x, nth = blockDim.x;
@@ -559,16 +562,14 @@ __global__ void __launch_bounds__(256) k_phi_tile(PhiArgs a, int op, int vc, int
   const int c = (int)(cp % a.C);
   const int Hs = a.Hs, Ws = a.Ws, h = a.h, kh = a.kh;
   const int kh4 = round4(kh);
-  const bool fast = phi_rows16(S, Hs, a.layout == kPhiPfa268);
-  const PhiTileView tv = phi_tile_prep<S>(a, phl, cp, vbeg, nv, vc, fast);
+  const PhiTileView tv = phi_tile_prep<S>(a, phl, cp, vbeg, nv, vc, FAST);
   const double2 *zH = tv.zH, *phH = tv.phH, *hH = tv.hH, *hW = tv.hW, *P = tv.P;
 
   const double lmb = lambda_of(a, c);
-  if constexpr (S != 3) {
-    if (fast) {
-      phi_tile_rows16<S>(a, op, tv, (double*)(phl + phi_tile_lds(S, Hs, kh, a.kw, vc, true).part), cp, vbeg, nv, lmb);
-      return;
-    }
+  if constexpr (FAST) {
+    static_assert(S != 3, "the split-DFT form serves scales 1, 2 and 4");
+    phi_tile_rows16<S>(a, op, tv, (double*)(phl + phi_tile_lds(S, Hs, kh, a.kw, vc, true).part), cp, vbeg, nv, lmb);
+    return;
   }
   const double norm = 1.0 / ((double)Hs * (double)Ws);
   const double inv_s2 = 1.0 / (double)(S * S);
@@ -1571,11 +1572,12 @@ int launch_phi(const float* psf, const float* bias, float eps, const Geo& g, boo
     if (lds <= kTileLds && g.Cp * nchunk <= 0x7fffffff) {
       const dim3 grid((unsigned)(g.Cp * nchunk));
       const int o = op ? 1 : 0;
+      auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(kThreads), (size_t)lds, st, a, o, vc, nchunk); };
       switch (g.s) {
-        case 1: hipLaunchKernelGGL(k_phi_tile<1>, grid, dim3(kThreads), (size_t)lds, st, a, o, vc, nchunk); break;
-        case 2: hipLaunchKernelGGL(k_phi_tile<2>, grid, dim3(kThreads), (size_t)lds, st, a, o, vc, nchunk); break;
-        case 3: hipLaunchKernelGGL(k_phi_tile<3>, grid, dim3(kThreads), (size_t)lds, st, a, o, vc, nchunk); break;
-        default: hipLaunchKernelGGL(k_phi_tile<4>, grid, dim3(kThreads), (size_t)lds, st, a, o, vc, nchunk); break;
+        case 1: fast ? go(k_phi_tile<1, true>) : go(k_phi_tile<1, false>); break;
+        case 2: fast ? go(k_phi_tile<2, true>) : go(k_phi_tile<2, false>); break;
+        case 3: go(k_phi_tile<3, false>); break;  // phi_rows16 needs s in {1, 2, 4}
+        default: fast ? go(k_phi_tile<4, true>) : go(k_phi_tile<4, false>); break;
       }
       return check_launch("transfer table");
     }
