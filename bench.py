@@ -282,7 +282,7 @@ def make_usrnet(torch, dev, batch=4):
     return m, torch.stack(xs).to(dev), torch.stack(ks).to(dev)
 
 
-def bench_model(torch, dev, iters=3):
+def bench_model(torch, dev, iters=6):
     """Converse-DnCNN (cfg4) images/s."""
     m, x = make_dncnn(torch, dev)
     with torch.no_grad():
@@ -293,7 +293,7 @@ def bench_model(torch, dev, iters=3):
             "images_per_s": 8 / t, "params": sum(p.numel() for p in m.parameters()), "iters": iters}
 
 
-def bench_usrnet(torch, dev, iters=3):
+def bench_usrnet(torch, dev, iters=6):
     """Converse-USRNet (cfg5) images/s."""
     m, x, k = make_usrnet(torch, dev)
     with torch.no_grad():
