@@ -452,10 +452,12 @@ __device__ __forceinline__ void phi_rows16_k(const PhiTileView& tv, int Hs, int 
 // op: K, and conj K rD / (Hs Ws).  At scale S > 1 a thread's 16 rows hold 16 / S whole alias classes
 // (rows u0 + a h, h = (16 / S) H1), and the S column members of a class are the block's threads
 // (v, b, u1) for b < S, which exchange their partial sums through LDS.
-template <int S>
+// LAYOUT: the table layout the S = 1 entries are written in, fixed at compile time (kPhiFused256
+// also fixes Hs = 256), so that each entry's index is a per-thread base plus a constant.
+template <int S, int LAYOUT = -1>
 __device__ void phi_tile_rows16(const PhiArgs& a, int op, const PhiTileView& tv, double* part, int64_t cp, int vbeg,
                                 int nv, double lmb) {
-  const int Hs = a.Hs, kh4 = round4(a.kh), H1 = Hs >> 4;
+  const int Hs = LAYOUT == kPhiFused256 ? 256 : a.Hs, kh4 = round4(a.kh), H1 = Hs >> 4;
   const double norm = 1.0 / ((double)Hs * (double)a.Ws);
   if constexpr (S == 1) {
     for (int it = threadIdx.x; it < nv * H1; it += blockDim.x) {
@@ -473,7 +475,10 @@ __device__ void phi_tile_rows16(const PhiArgs& a, int op, const PhiTileView& tv,
           a.kf[o] = make_float2((float)k.x, (float)k.y);
           a.phi[o] = make_float2((float)(k.x * rD * norm), (float)(-k.y * rD * norm));
         } else {
-          a.phi[phi_out_index(a, cp, vb, u)] = make_float2((float)((k.x + lmb) * rD * norm), (float)(-k.y * rD * norm));
+          const int64_t o = LAYOUT == kPhiFused256 ? fused256_phi_index(cp, (int)vb, u)
+                            : LAYOUT == kPhiGeneric ? (cp * a.NCs + vb) * Hs + u
+                                                    : phi_out_index(a, cp, vb, u);
+          a.phi[o] = make_float2((float)((k.x + lmb) * rD * norm), (float)(-k.y * rD * norm));
         }
       }
     }
@@ -568,7 +573,13 @@ __global__ void __launch_bounds__(256) k_phi_tile(PhiArgs a, int op, int vc, int
   const double lmb = lambda_of(a, c);
   if constexpr (FAST) {
     static_assert(S != 3, "the split-DFT form serves scales 1, 2 and 4");
-    phi_tile_rows16<S>(a, op, tv, (double*)(phl + phi_tile_lds(S, Hs, kh, a.kw, vc, true).part), cp, vbeg, nv, lmb);
+    double* part = (double*)(phl + phi_tile_lds(S, Hs, kh, a.kw, vc, true).part);
+    if (S == 1 && !op && a.layout == kPhiFused256 && Hs == 256)
+      phi_tile_rows16<S, kPhiFused256>(a, op, tv, part, cp, vbeg, nv, lmb);
+    else if (S == 1 && !op && a.layout == kPhiGeneric)
+      phi_tile_rows16<S, kPhiGeneric>(a, op, tv, part, cp, vbeg, nv, lmb);
+    else
+      phi_tile_rows16<S>(a, op, tv, part, cp, vbeg, nv, lmb);
     return;
   }
   const double norm = 1.0 / ((double)Hs * (double)Ws);
