@@ -544,8 +544,8 @@ __device__ void phi_tile_rows16(const PhiArgs& a, int op, const PhiTileView& tv,
           } else if (vb <= a.Ws / 2) {
             const double2 hn = dcmul(tv.hH[u], hv);
             const double2 t = dcmul(make_double2(k.x, -k.y), g);
-            a.phi[phi_out_index(a, cp, vb, u)] =
-                make_float2((float)((hn.x + t.x) * norm), (float)((hn.y + t.y) * norm));
+            const int64_t o = LAYOUT == kPhiGeneric ? (cp * a.NCs + vb) * Hs + u : phi_out_index(a, cp, vb, u);
+            a.phi[o] = make_float2((float)((hn.x + t.x) * norm), (float)((hn.y + t.y) * norm));
           }
         }
       }
@@ -576,7 +576,7 @@ __global__ void __launch_bounds__(256) k_phi_tile(PhiArgs a, int op, int vc, int
     double* part = (double*)(phl + phi_tile_lds(S, Hs, kh, a.kw, vc, true).part);
     if (S == 1 && !op && a.layout == kPhiFused256 && Hs == 256)
       phi_tile_rows16<S, kPhiFused256>(a, op, tv, part, cp, vbeg, nv, lmb);
-    else if (S == 1 && !op && a.layout == kPhiGeneric)
+    else if (!op && a.layout == kPhiGeneric)
       phi_tile_rows16<S, kPhiGeneric>(a, op, tv, part, cp, vbeg, nv, lmb);
     else
       phi_tile_rows16<S>(a, op, tv, part, cp, vbeg, nv, lmb);
