@@ -63,11 +63,11 @@ def test_conv1x1(cin, cout, act):
     assert np.abs(got - ref).max() <= TOL
 
 
-@pytest.mark.parametrize("cin,cout", [(1, 64), (64, 1), (3, 64), (64, 3)])
+@pytest.mark.parametrize("cin,cout", [(1, 64), (64, 1), (3, 64), (64, 3), (2100, 3)])
 @pytest.mark.parametrize("HW,res", [((15, 17), False), ((16, 16), True), ((15, 17), True)])
 def test_conv1x1_generic_kernel_paths(cin, cout, HW, res):
     """The VALU 1x1 kernel for channel counts without an MFMA tile: four pixels per thread (float4)
-    when HW % 4 == 0, one otherwise; with and without a scaled residual."""
+    when HW % 4 == 0, one otherwise; with and without a scaled residual; up to 2100 input channels."""
     from conversenet_amd import functional as Fh
     rng = seeded("c11-any", cin, cout, HW, res)
     B = 2
