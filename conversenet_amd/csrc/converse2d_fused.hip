@@ -1268,7 +1268,10 @@ constexpr bool fused256_index_ok() {
   if (P::RS != kF256Rs || P::SLOTS != kF256Slots) return false;
   for (int u = 0; u < P::N; ++u) {
     const int rp = P::rfpos(u % P::NH);
-    for (int v = 0; v < P::NQ; v += (v == 0 || v == P::NQ - 2) ? 1 : 37) {
+    // sampled columns: DC, the first bins, interior bins, and the last two (v = NQ - 1 is the Nyquist
+    // column, whose odd-row slot is the pos = M + 1 special case of pb)
+    constexpr int kV[] = {0, 1, 2, 37, 64, 100, P::NQ - 3, P::NQ - 2, P::NQ - 1};
+    for (int v : kV) {
       const int64_t want = 2 * ((int64_t)(rp >> 1) * P::RS + ((rp & 1) ? P::pb(v) : P::pa(v))) + u / P::NH;
       if (fused256_phi_index(0, v, u) != want || fused256_phi_index(3, v, u) != want + 2 * 3 * P::SLOTS) return false;
     }

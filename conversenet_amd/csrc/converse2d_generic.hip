@@ -1891,6 +1891,10 @@ struct OpLayout {
   size_t kf, A, table;       // table regions
   size_t S, S0, SH, scratch;  // scratch regions
 };
+size_t op_col_lds(const Geo& g, const OpLayout& L) {
+  return align_up((size_t)(3 * g.h + g.Hs + 2 * g.s * g.Hs) * sizeof(float2), 16) +
+         rader_lds_bytes(L.t.plan[kTabH]) + rader_lds_bytes(L.t.plan[kTabHs]);
+}
 int op_layout(int64_t B, int64_t C, int64_t h, int64_t w, int kh, int kw, int scale, Geo* g, OpLayout* L) {
   int rc = module_geo(B, C, h, w, 1, kh, kw, scale, 0, g);
   if (rc != CVN_OK) return rc;
@@ -1904,11 +1908,11 @@ int op_layout(int64_t B, int64_t C, int64_t h, int64_t w, int kh, int kw, int sc
   L->S0 = o; o += align_up((size_t)g->P * g->NCs * g->Hs * sizeof(float2));
   L->SH = o; o += align_up((size_t)g->P * g->NCs * g->Hs * sizeof(float2));
   L->scratch = o;
+  // the apply's launch limits, checked here so that every query (table, scratch, workspace) answers
+  // 0 for a geometry the apply would reject
+  if (g->P > 65535) return fail(CVN_ERR_UNSUPPORTED, "B*C exceeds 65535");
+  if (op_col_lds(*g, *L) > kLdsLimit) return fail(CVN_ERR_UNSUPPORTED, "column class does not fit in LDS");
   return CVN_OK;
-}
-size_t op_col_lds(const Geo& g, const OpLayout& L) {
-  return align_up((size_t)(3 * g.h + g.Hs + 2 * g.s * g.Hs) * sizeof(float2), 16) +
-         rader_lds_bytes(L.t.plan[kTabH]) + rader_lds_bytes(L.t.plan[kTabHs]);
 }
 }  // namespace
 
@@ -1962,9 +1966,7 @@ extern "C" int cvn_converse2d_op_apply_f32(const float* x, const float* x0, int6
   if (B == 0) return CVN_OK;
   if (!scratch || scratch_bytes < L.scratch)
     return fail(CVN_ERR_WORKSPACE, "scratch too small: need %zu bytes", L.scratch);
-  if (g.P > 65535) return fail(CVN_ERR_UNSUPPORTED, "B*C exceeds 65535");
-  const size_t lds = op_col_lds(g, L);
-  if (lds > kLdsLimit) return fail(CVN_ERR_UNSUPPORTED, "column class does not fit in LDS");
+  const size_t lds = op_col_lds(g, L);  // within kLdsLimit (op_layout)
   set_lds_attrs();
   hipStream_t st = (hipStream_t)stream;
   const char* tabs = (const char*)table;

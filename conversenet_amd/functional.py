@@ -8,12 +8,17 @@ kernels on torch's current stream.  No CPU fallback exists here: a missing libra
 from __future__ import annotations
 
 import os
+import threading
 
 import torch
 
 from . import _lib, composite
 
+# The op is callable from any host thread (the reference guards its OTF cache with a mutex,
+# converse2d.cpp:56,70,90): the workspace map, the plan memo and the table cache each take a lock
+# around their dict updates.  Kernel launches and table builds run outside the locks.
 _ws_cache: dict = {}
+_ws_lock = threading.Lock()
 
 
 def _stream(dev):
@@ -34,15 +39,17 @@ def _workspace(dev, nbytes: int, stream=None):
     """A reusable uint8 scratch tensor per (device, stream); grows monotonically.  stream: the current
     stream's handle when the caller has it already."""
     key = (dev.index, torch.cuda.current_stream(dev).cuda_stream if stream is None else stream)
-    buf = _ws_cache.get(key)
-    if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
-        _ws_cache[key] = buf
+    with _ws_lock:
+        buf = _ws_cache.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+            _ws_cache[key] = buf
     return buf
 
 
 def release_workspace():
-    _ws_cache.clear()
+    with _ws_lock:
+        _ws_cache.clear()
 
 
 class TableCache:
@@ -63,6 +70,7 @@ class TableCache:
         from collections import OrderedDict
 
         self.entries = OrderedDict()
+        self._lock = threading.RLock()
         self.latest = {}  # key without version counters -> full key
         self.max_entries = max_entries
         self.max_bytes = max_bytes
@@ -75,15 +83,16 @@ class TableCache:
         return key[:2] + key[3:4] + key[5:]
 
     def get(self, key):
-        e = self.entries.get(key)
-        if e is None:
-            self.misses += 1
-            return None
-        self.entries.move_to_end(key)
-        self.hits += 1
-        return e[0]
+        with self._lock:
+            e = self.entries.get(key)
+            if e is None:
+                self.misses += 1
+                return None
+            self.entries.move_to_end(key)
+            self.hits += 1
+            return e[0]
 
-    def _drop(self, key):
+    def _drop(self, key):  # caller holds self._lock
         t, _ = self.entries.pop(key)
         self.bytes -= t.numel()
         stem = self._stem(key)
@@ -91,19 +100,24 @@ class TableCache:
             del self.latest[stem]
 
     def put(self, key, table, refs):
-        old = self.latest.get(self._stem(key))
-        if old is not None and old in self.entries:
-            self._drop(old)  # the same tensors at an older version: never hit again
-        self.entries[key] = (table, refs)
-        self.latest[self._stem(key)] = key
-        self.bytes += table.numel()
-        while self.entries and (len(self.entries) > self.max_entries or self.bytes > self.max_bytes):
-            self._drop(next(iter(self.entries)))
+        with self._lock:
+            old = self.latest.get(self._stem(key))
+            if old is not None and old in self.entries:
+                self._drop(old)  # the same tensors at an older version: never hit again
+            prev = self.entries.pop(key, None)
+            if prev is not None:  # another thread built the same table meanwhile: keep one copy
+                self.bytes -= prev[0].numel()
+            self.entries[key] = (table, refs)
+            self.latest[self._stem(key)] = key
+            self.bytes += table.numel()
+            while self.entries and (len(self.entries) > self.max_entries or self.bytes > self.max_bytes):
+                self._drop(next(iter(self.entries)))
 
     def clear(self):
-        self.entries.clear()
-        self.latest.clear()
-        self.bytes = 0
+        with self._lock:
+            self.entries.clear()
+            self.latest.clear()
+            self.bytes = 0
 
 
 table_cache = TableCache()
@@ -126,6 +140,7 @@ def _cache_key(kind, weight, bias, eps, geo, route, dev):
 
 
 _plan_memo: dict = {}
+_plan_lock = threading.Lock()
 
 
 def _module_plan(lib, B, C, H, W, pb, kh, kw, s, p):
@@ -140,9 +155,10 @@ def _module_plan(lib, B, C, H, W, pb, kh, kw, s, p):
             _lib.check(route, "converse2d_fused")
         plan = (route, lib.cvn_converse2d_table_bytes(B, C, H, W, pb, kh, kw, s, p, route),
                 lib.cvn_converse2d_scratch_bytes(B, C, H, W, pb, kh, kw, s, p, route))
-        if len(_plan_memo) >= 1024:
-            _plan_memo.clear()
-        _plan_memo[key] = plan
+        with _plan_lock:
+            if len(_plan_memo) >= 1024:
+                _plan_memo.clear()
+            _plan_memo[key] = plan
     return plan
 
 
@@ -220,6 +236,25 @@ def supported(x, weight, scale, padding, grad_x=False, grad_weight=False, shape=
     return lib.cvn_converse2d_supported(B, C, H, W, int(weight.shape[0]), int(weight.shape[2]),
                                         int(weight.shape[3]), int(scale), int(padding), int(bool(grad_x)),
                                         int(bool(grad_weight))) == _lib.CVN_OK
+
+
+def op_supported(x, x0, weight, scale) -> bool:
+    """Whether the library's operator path serves this call (its table and scratch queries are
+    non-zero for the geometry); shapes it does not serve go to the PyTorch composition.  Malformed
+    arguments also answer False here and are then rejected by the composition's checks."""
+    if x.dim() != 4 or x0.dim() != 4 or weight.dim() != 4:
+        return False
+    s = int(scale)
+    B, C, h, w = (int(v) for v in x.shape)
+    if s < 1 or tuple(x0.shape) != (B, C, h * s, w * s) or weight.shape[0] != 1 or weight.shape[1] != C:
+        return False
+    if (s == 1 and x0.data_ptr() == x.data_ptr() and x0.stride() == x.stride() and B > 0
+            and supported(x, weight, 1, 0)):
+        return True  # served by the module route on the padded plane (converse2d_op)
+    lib = _lib.load()
+    kh, kw = int(weight.shape[2]), int(weight.shape[3])
+    return (lib.cvn_converse2d_op_table_bytes(C, h, w, kh, kw, s) > 0
+            and lib.cvn_converse2d_op_scratch_bytes(B, C, h, w, s) > 0)
 
 
 def converse2d_backward(grad_out, x, weight, bias, scale=1, padding=2, padding_mode="circular", eps=1e-5,
@@ -346,6 +381,8 @@ def converse2d_fwd_oneshot(x, weight, bias, scale=1, padding=2, padding_mode="ci
     s, p = int(scale), int(padding)
     kh, kw, pb = int(weight.shape[2]), int(weight.shape[3]), int(weight.shape[0])
     x, wc, bc = x.contiguous(), weight.contiguous(), bias.contiguous()
+    if x.data_ptr() % 16:  # the fused route reads rows as 16-byte vectors
+        x = x.clone()
     out = torch.empty((B, C, H * s, W * s), dtype=torch.float32, device=x.device)
     nb = lib.cvn_converse2d_fwd_workspace(B, C, H, W, pb, kh, kw, s, p)
     ws = _workspace(x.device, max(nb, 1))

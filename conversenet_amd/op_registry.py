@@ -32,13 +32,15 @@ def _hip_ok(*ts) -> bool:
 
 
 def _forward(x, x0, weight, bias, scale, eps=1e-5):
-    if _hip_ok(x, x0, weight, bias):
+    # geometries past the library's limits (e.g. a padded side above 4096, too many planes for the
+    # multi-pass grid) run the composition, which has none, instead of raising CVN_ERR_UNSUPPORTED
+    if _hip_ok(x, x0, weight, bias) and functional.op_supported(x, x0, weight, scale):
         return functional.converse2d_op(x, x0, weight, bias, scale, eps)
     return composite.converse2d_op(x, x0, weight, bias, scale, eps)
 
 
 def _forward_fused(x, weight, bias, scale, padding, padding_mode, eps=1e-5, act="none"):
-    if _hip_ok(x, weight, bias):
+    if _hip_ok(x, weight, bias) and functional.supported(x, weight, scale, padding):
         return functional.converse2d_fused(x, weight, bias.reshape(-1), scale, padding, padding_mode, eps,
                                            act if act != "none" else None)
     out = composite.converse2d_module(x, weight, bias.reshape(1, -1, 1, 1), scale, padding, padding_mode, eps)

@@ -4,8 +4,11 @@
  * Every entry point takes plain device pointers, sizes and a HIP stream, enqueues its kernels on
  * that stream and returns without synchronising.  The caller owns all buffers; entry points that
  * need scratch memory take a caller-provided workspace whose size a matching *_workspace() query
- * returns (no entry point allocates device memory).  Entry points are re-entrant and keep no
- * mutable global state apart from the per-thread error string.  Tensors are fp32, NCHW,
+ * returns (no entry point allocates device memory).  Entry points are re-entrant; the library's
+ * mutable global state is the per-thread error string and, for cvn_converse2d_fwd_noalloc_f32 only,
+ * a file-scope device array of CVN_NOALLOC_SCRATCH_BYTES (64 MiB) that the code object reserves on
+ * every device of every process that loads the library, whether or not that entry point is called
+ * (calls of that entry point that overlap on one device race on it).  Tensors are fp32, NCHW,
  * contiguous.  Return value: CVN_OK, or a negative CVN_ERR_* code with a message retrievable
  * through cvn_last_error() on the calling thread.
  *
@@ -170,7 +173,11 @@ int cvn_layernorm_cf_f32(const float* x, int64_t B, int64_t C, int64_t HW, const
 /* y[b,o,p] = act(sum_c W[o,c] x[b,c,p] + bias[o]);  then, if residual != NULL,
  * y = (res_scale ? res_scale[o] : 1) * y + residual[b,o,p].  x: (B,Cin,HW), W: (Cout,Cin),
  * bias: (Cout) or NULL, residual: (B,Cout,HW) or NULL, res_scale: (Cout) or NULL.
- * y may alias residual.  Uses fp32 MFMA. */
+ * y may alias residual.  Channel counts with a matrix-core tile run on the MFMA units: in whole
+ * 32-channel chunks as split-fp16 products (each fp32 operand x = x_h + x_l, two fp16 parts; three
+ * fp16 MFMAs accumulating in fp32; relative error per product below 2^-20, a chunk whose activations
+ * leave fp16's range falls back to fp32 MFMAs), otherwise as fp32 MFMAs; 1 or 3 channels, and pixel
+ * counts not a multiple of 4, run on a VALU kernel in fp32. */
 int cvn_conv1x1_f32(const float* x, int64_t B, int64_t Cin, int64_t HW, const float* weight,
                     const float* bias, int64_t Cout, int act, const float* residual,
                     const float* res_scale, float* y, cvn_stream_t stream);

@@ -185,3 +185,26 @@ def test_outside_library_limits_runs_the_composition():
     xs = torch.randn(1, 2, 6, 7, device=DEV)
     up(xs).sum().backward()  # weight gradients at s = 5: composition under autograd
     assert up.weight.grad is not None and torch.isfinite(up.weight.grad).all()
+
+
+def test_registered_ops_outside_library_limits_run_the_composition():
+    """converse2d::forward and converse2d::forward_fused on HIP tensors whose geometry the library does
+    not serve (a padded side above 4096) run the PyTorch composition instead of raising
+    CVN_ERR_UNSUPPORTED (the reference op has no such limits, converse2d.cpp:165-209)."""
+    import conversenet_amd  # noqa: F401  (registers torch.ops.converse2d)
+    torch.manual_seed(6)
+    w = torch.softmax(torch.randn(1, 1, 9), -1).reshape(1, 1, 3, 3).to(DEV)
+    b = torch.zeros(1, 1, 1, 1, device=DEV)
+    xp = torch.randn(1, 1, 4100, 6, device=DEV)  # already padded, as the op takes it
+    x0 = torch.randn(1, 1, 4100, 6, device=DEV)
+    with torch.no_grad():
+        got = torch.ops.converse2d.forward(xp, x0, w, b, 1, 1e-5).cpu().numpy()
+        fused = torch.ops.converse2d.forward_fused(xp[..., 1:-1, 1:-1].contiguous(), w, b, 1, 1, "circular",
+                                                   1e-5).cpu().numpy()
+    ref = O.converse2d_op(xp.cpu().numpy(), x0.cpu().numpy(), w.cpu().numpy(), b.cpu().numpy(), 1, 1e-5)
+    ref_f = O.converse2d_module(xp[..., 1:-1, 1:-1].cpu().numpy(), w.cpu().numpy(), b.cpu().numpy(), 1, 1,
+                                "circular", 1e-5)
+    err, err_f = np.abs(got - ref).max(), np.abs(fused - ref_f).max()
+    print(f"op 4100x6 on the composition: max-abs {err:.3e}; forward_fused {err_f:.3e}")
+    assert got.shape == (1, 1, 4100, 6) and fused.shape == (1, 1, 4098, 4)
+    assert err <= 1e-2 and err_f <= 1e-2  # the reference's fp32 op order (see above)

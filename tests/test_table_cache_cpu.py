@@ -61,3 +61,40 @@ def test_unsupported_geometries_are_routed_to_the_composition():
     assert not Fh.supported(torch.empty(1, 3, 8, 8), w, 5, 1, grad_weight=True)
     assert Fh.supported(torch.empty(1, 3, 8, 8), w, 5, 1, grad_x=True)
     assert Fh.supported(None, w, 1, 1, shape=(1, 3, 64, 64))
+
+
+def test_concurrent_callers_keep_the_cache_consistent():
+    """The op may be called from any host thread (the reference's cache is mutex-guarded,
+    converse2d.cpp:56,70,90): eight threads hitting, filling and invalidating (in-place updates) one
+    cache leave its byte count, entry bound and latest-version map consistent and raise nothing."""
+    import random
+    import threading
+
+    c = Fh.TableCache(max_entries=16, max_bytes=1 << 30)
+    params = [(torch.ones(1, 1, 1, 1), torch.zeros(1, 1, 1, 1)) for _ in range(40)]
+    errors = []
+    start = threading.Barrier(8)
+
+    def worker(seed):
+        rng = random.Random(seed)
+        start.wait()
+        try:
+            for _ in range(3000):
+                w, b = params[rng.randrange(len(params))]
+                k = _key(w, b)
+                if c.get(k) is None:
+                    c.put(k, torch.empty(rng.choice((10, 20, 30)), dtype=torch.uint8), (w, b))
+                if rng.random() < 0.05:
+                    w.add_(0)  # an in-place update: bumps the version counter
+        except Exception as e:  # noqa: BLE001
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(8)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors[:3]
+    assert len(c.entries) <= 16
+    assert c.bytes == sum(t.numel() for t, _ in c.entries.values())
+    assert all(c.latest[c._stem(k)] == k for k in c.entries)

@@ -16,9 +16,10 @@ DEV = torch.device("cuda")
 # (B, C, H, W, k, s, pad, mode) pairs: larger first, smaller second
 PAIRS = {
     "fused": [(4, 64, 256, 256, 5, 1, 2, "circular"), (1, 8, 128, 128, 5, 1, 2, "reflect")],
-    "generic": [(8, 64, 64, 64, 3, 2, 1, "circular"), (2, 3, 30, 26, 5, 3, 2, "replicate")],
+    "generic": [(2, 16, 64, 64, 3, 1, 1, "circular"), (2, 3, 30, 26, 5, 3, 2, "replicate")],
     "pfa268": [(2, 8, 256, 256, 7, 1, 6, "circular"), (1, 2, 256, 256, 5, 1, 6, "constant")],
 }
+ROUTE_IDS = {"fused": _lib.ROUTE_FUSED, "generic": _lib.ROUTE_GENERIC, "pfa268": _lib.ROUTE_PFA268}
 
 
 def _inputs(B, C, H, W, k, s, p, mode):
@@ -50,6 +51,7 @@ def test_noalloc_matches_workspace_entry_point(route):
     lib = _lib.load()
     for i, (B, C, H, W, k, s, p, mode) in enumerate(PAIRS[route]):
         print(f"noalloc {route} call {i}: B{B} C{C} {H}x{W} k{k} s{s} p{p} {mode}", flush=True)
+        assert lib.cvn_converse2d_route(B, C, H, W, 1, k, k, s, p) == ROUTE_IDS[route]
         x, w, b = _inputs(B, C, H, W, k, s, p, mode)
         act = _lib.ACT_GELU if i == 1 else _lib.ACT_NONE
         ref, got = _both(lib, x, w, b, s, p, mode, act)
