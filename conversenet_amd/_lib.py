@@ -21,6 +21,7 @@ CVN_ERR_HIP = -4
 
 PAD_MODES = {"constant": 0, "zeros": 0, "reflect": 1, "replicate": 2, "circular": 3}
 ROUTE_AUTO, ROUTE_FUSED, ROUTE_PFA268, ROUTE_GENERIC = 0, 1, 2, 3
+ROUTE_OP_PLANNED = 4  # operator path on compile-time plans (cvn_converse2d_op_route)
 NOALLOC_SCRATCH_BYTES = 64 << 20  # CVN_NOALLOC_SCRATCH_BYTES
 ACT_NONE = 0
 ACT_GELU = 1
@@ -51,6 +52,7 @@ SIGNATURES = {
     "cvn_converse2d_op_workspace": (_size, [_i64, _i64, _i64, _i64, _int, _int, _int]),
     "cvn_converse2d_op_f32": (_int, [_ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _int, _int, _ptr, _f32, _int, _ptr,
                                      _ptr, _size, _ptr]),
+    "cvn_converse2d_op_route": (_int, [_i64, _i64, _int]),
     "cvn_converse2d_op_table_bytes": (_size, [_i64, _i64, _i64, _int, _int, _int]),
     "cvn_converse2d_op_scratch_bytes": (_size, [_i64, _i64, _i64, _i64, _int]),
     "cvn_converse2d_op_table_f32": (_int, [_ptr, _int, _int, _ptr, _f32, _i64, _i64, _i64, _int, _ptr, _size, _ptr]),

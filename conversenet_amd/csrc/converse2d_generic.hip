@@ -1916,6 +1916,11 @@ int op_layout(int64_t B, int64_t C, int64_t h, int64_t w, int kh, int kw, int sc
 }
 }  // namespace
 
+extern "C" int cvn_converse2d_op_route(int64_t h, int64_t w, int scale) {
+  if (h < 1 || w < 1 || h > kMaxFftLen || w > kMaxFftLen) return CVN_ROUTE_GENERIC;
+  return op_ct_supported((int)h, (int)w, scale) ? CVN_ROUTE_OP_PLANNED : CVN_ROUTE_GENERIC;
+}
+
 extern "C" size_t cvn_converse2d_op_table_bytes(int64_t C, int64_t h, int64_t w, int kh, int kw, int scale) {
   Geo g;
   OpLayout L;
@@ -1976,6 +1981,10 @@ extern "C" int cvn_converse2d_op_apply_f32(const float* x, const float* x0, int6
   float2* S = (float2*)(sc + L.S);
   float2* S0 = (float2*)(sc + L.S0);
   float2* SH = (float2*)(sc + L.SH);
+  if (op_ct_supported(g.h, g.w, g.s) && (uintptr_t)x % 16 == 0 && (uintptr_t)x0 % 16 == 0 && (uintptr_t)out % 16 == 0)
+    return launch_op_ct(x, x0, g.P, g.C, g.h, g.w, g.s, (const float2*)(tabs + L.t.off[kTabW]),
+                        (const float2*)(tabs + L.t.off[kTabH]), (const float2*)(tabs + L.t.off[kTabHs]),
+                        (const float2*)(tabs + L.t.off[kTabWs]), kf, Am, S, S0, SH, out, st);
   if ((rc = launch_rows_fwd(x, g.P, g.h, g.w, 0, CVN_PAD_ZEROS, g.h, g.w, tabs + L.t.off[kTabW], S, st)) != CVN_OK)
     return rc;
   if ((rc = launch_rows_fwd(x0, g.P, g.Hs, g.Ws, 0, CVN_PAD_ZEROS, g.Hs, g.Ws, tabs + L.t.off[kTabWs], S0, st)) !=

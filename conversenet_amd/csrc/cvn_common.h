@@ -191,4 +191,12 @@ void once_per_device(std::atomic<uint64_t>& done, F fn) {
   done.fetch_or(bit, std::memory_order_release);
 }
 
+// Operator path on compile-time transform lengths (converse2d_opct.hip): the LR rows (w), columns
+// (h) and the HR rows / columns (w s, h s) have fixed plans.  Same scratch and table layouts as the
+// generic op path; tw_* are the twiddle tables (exp(-2 pi i m / L), m < L) of each length.
+bool op_ct_supported(int h, int w, int s);
+int launch_op_ct(const float* x, const float* x0, int64_t P, int64_t C, int h, int w, int s, const float2* tw_w,
+                 const float2* tw_h, const float2* tw_Hs, const float2* tw_Ws, const float2* kf, const float2* A,
+                 float2* S, float2* S0, float2* SH, float* out, hipStream_t st);
+
 }  // namespace cvn

@@ -150,6 +150,14 @@ int cvn_converse2d_op_f32(const float* x, const float* x0, int64_t B, int64_t C,
                           int64_t w, const float* psf, int kh, int kw, const float* bias,
                           float eps, int scale, float* out, void* workspace,
                           size_t workspace_bytes, cvn_stream_t stream);
+/* Which kernels cvn_converse2d_op_apply_f32 runs for (h, w, scale) with 16-byte aligned x, x0 and out:
+ * CVN_ROUTE_OP_PLANNED (scale 2-4, h in {64, 128, 256}, w and w * scale in {64, 128, 192, 256, 384, 512,
+ * 768, 1024}: three passes on compile-time transform plans, one column block per mirrored pair of
+ * alias classes) or CVN_ROUTE_GENERIC (runtime plans).  Both compute the same solve; misaligned
+ * buffers always take the generic kernels.  No reference counterpart: converse2d.cpp:165-209 has one
+ * code path. */
+enum { CVN_ROUTE_OP_PLANNED = 4 };
+int cvn_converse2d_op_route(int64_t h, int64_t w, int scale);
 size_t cvn_converse2d_op_table_bytes(int64_t C, int64_t h, int64_t w, int kh, int kw, int scale);
 size_t cvn_converse2d_op_scratch_bytes(int64_t B, int64_t C, int64_t h, int64_t w, int scale);
 int cvn_converse2d_op_table_f32(const float* psf, int kh, int kw, const float* bias, float eps, int64_t C,

@@ -153,6 +153,19 @@ def test_op_split_sizes_add_up():
     assert lib.cvn_converse2d_op_table_bytes(3, 5000, 8, 3, 3, 1) == 0
 
 
+def test_op_route_query():
+    """The op path runs the compile-time-plan kernels exactly for scale 2-4, h in {64, 128, 256} and w,
+    w * scale in the planned lengths; everything else (scale 1 included) takes the generic kernels."""
+    lib = _lib.load()
+    planned, generic = _lib.ROUTE_OP_PLANNED, _lib.ROUTE_GENERIC
+    for h, w, s in [(256, 256, 2), (256, 256, 3), (256, 256, 4), (64, 64, 2), (128, 64, 3), (64, 256, 4),
+                    (256, 128, 3), (128, 192, 2), (64, 64, 3), (128, 128, 2)]:
+        assert lib.cvn_converse2d_op_route(h, w, s) == planned, (h, w, s)
+    for h, w, s in [(256, 256, 1), (256, 256, 5), (260, 256, 2), (256, 260, 2), (32, 64, 2), (256, 40, 2),
+                    (96, 96, 2), (20, 22, 3), (0, 64, 2), (5000, 64, 2)]:
+        assert lib.cvn_converse2d_op_route(h, w, s) == generic, (h, w, s)
+
+
 def test_noalloc_limit_and_rejection_without_device():
     lib = _lib.load()
     text = open(HEADER).read()

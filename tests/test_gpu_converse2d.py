@@ -424,6 +424,42 @@ def test_data_step_per_sample_psf(B, C, h, w, s):
     assert err <= TOL
 
 
+# (B, C, h, w, s, k, x0): shapes the op path runs on compile-time plans (every planned row length and
+# every (h, s) column plan at least once), then the reference's timing grid (test_speed.py:137-146,
+# 253-271: B8 C8 256x256, x0 = nearest(x)) at s = 2 and 3
+OP_PLANNED = [(1, 2, 64, 64, 2, 3, "rand"), (2, 3, 64, 128, 3, 5, "rand"), (1, 2, 128, 64, 4, 5, "rand"),
+              (1, 1, 128, 192, 2, 7, "rand"), (2, 2, 256, 64, 2, 5, "rand"), (1, 2, 64, 256, 4, 3, "rand"),
+              (1, 2, 256, 128, 3, 4, "rand"), (1, 2, 128, 128, 3, 6, "rand"), (1, 2, 64, 64, 3, 2, "rand"),
+              (1, 2, 256, 256, 4, 5, "nearest"),
+              (8, 8, 256, 256, 2, 5, "nearest"), (8, 8, 256, 256, 3, 3, "nearest"), (8, 8, 256, 256, 3, 7, "rand")]
+
+
+@pytest.mark.parametrize("B,C,h,w,s,k,x0kind", OP_PLANNED)
+def test_op_level_planned(B, C, h, w, s, k, x0kind):
+    """converse2d::forward (converse2d.cpp:165-209) with arbitrary x0 on the compile-time-plan kernels,
+    against the fp64 oracle (one batch element at a time), max-abs <= 1e-4."""
+    from conversenet_amd import _lib
+    from conversenet_amd import functional as Fh
+    lib = _lib.load()
+    assert lib.cvn_converse2d_op_route(h, w, s) == _lib.ROUTE_OP_PLANNED
+    rng = seeded("op-planned", B, C, h, w, s, k, x0kind)
+    x = rng.standard_normal((B, C, h, w)).astype(np.float32)
+    if x0kind == "nearest":
+        x0 = np.repeat(np.repeat(x, s, axis=2), s, axis=3)
+    else:
+        x0 = rng.standard_normal((B, C, h * s, w * s)).astype(np.float32)
+    wt = softmax_psf(rng, C, k)
+    b = (0.3 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    dev = torch.device("cuda")
+    got = Fh.converse2d_op(*(torch.from_numpy(a).to(dev) for a in (x, x0, wt, b)), s, 1e-5).cpu().numpy()
+    err = 0.0
+    for i in range(B):
+        ref = O.converse2d_op(x[i:i + 1], x0[i:i + 1], wt, b, s, 1e-5)
+        err = max(err, float(np.abs(got[i:i + 1] - ref).max()))
+    print(f"op planned B{B} C{C} {h}x{w} s{s} k{k} x0={x0kind}: max-abs {err:.3e}")
+    assert err <= TOL
+
+
 @pytest.mark.parametrize("s,h,w", [(1, 30, 26), (4, 30, 26), (1, 32, 48), (2, 24, 20), (4, 16, 12)])
 def test_op_level_large_psf(s, h, w):
     from conversenet_amd import functional as Fh
