@@ -362,7 +362,10 @@ def bench_speed_grid(torch, dev, iters):
     k in {3, 5, 7}, fp32, psf softmax-normalised (torch.manual_seed(0) as there), throughput
     B * (H s) * (W s) / t in Gpix/s (channels not counted, as there).  Forward only."""
     import torch.nn.functional as F
-    out = {}
+    from conversenet_amd import _lib
+    lib = _lib.load()
+    out = {"note": "op-level bytes = x (B C H W) + x0 and out (B C Hs Ws each), fp32; route: fused (s = 1, "
+                   "x0 is x), op_planned (compile-time plans) or generic"}
     B, C, H, W = 8, 8, 256, 256
     for s in (1, 2, 3):
         for k in (3, 5, 7):
@@ -373,7 +376,11 @@ def bench_speed_grid(torch, dev, iters):
             b = torch.zeros(1, C, 1, 1, device=dev)
             with torch.no_grad():
                 t = time_events(torch, lambda: torch.ops.converse2d.forward(x, x0, w, b, s, 1e-5), iters)
-            out[f"s{s}_k{k}"] = {"fwd_ms": t * 1e3, "fwd_gpix_per_s": B * H * s * W * s / t / 1e9}
+            nbytes = 4 * B * C * H * W * (1 + (2 * s * s if s > 1 else 1))
+            route = "fused" if s == 1 else {_lib.ROUTE_OP_PLANNED: "op_planned", _lib.ROUTE_GENERIC: "generic"}.get(
+                lib.cvn_converse2d_op_route(H, W, s), "?")
+            out[f"s{s}_k{k}"] = {"fwd_ms": t * 1e3, "fwd_gpix_per_s": B * H * s * W * s / t / 1e9, "route": route,
+                                 "bytes": nbytes, "frac_hbm": nbytes / t / HBM_PEAK}
     return out
 
 
@@ -495,15 +502,16 @@ def only_kernel(torch, Fh, args, dev, x, step):
         torch.set_grad_enabled(False)
         fn = lambda: torch.ops.converse2d.forward(y, y, step.w, b4, 1, c["eps"])
     elif args.only == "grid":
-        # one point of the reference's speed grid: B8 C8 256x256, s = 2, k = 5, x0 = nearest(x)
+        # one point of the reference's speed grid: B8 C8 256x256, s = --grid-scale, k = 5, x0 = nearest(x)
         import torch.nn.functional as F
         torch.manual_seed(0)
+        gs = args.grid_scale
         xg = torch.randn(8, 8, 256, 256, device=dev)
-        x0 = F.interpolate(xg, scale_factor=2, mode="nearest")
+        x0 = xg if gs == 1 else F.interpolate(xg, scale_factor=gs, mode="nearest")
         wg = torch.softmax(torch.randn(1, 8, 25, device=dev), dim=-1).view(1, 8, 5, 5).contiguous()
         bg = torch.zeros(1, 8, 1, 1, device=dev)
         torch.set_grad_enabled(False)
-        fn = lambda: torch.ops.converse2d.forward(xg, x0, wg, bg, 2, 1e-5)
+        fn = lambda: torch.ops.converse2d.forward(xg, x0, wg, bg, gs, 1e-5)
     elif args.only == "tail":
         # the block tail with the next block's head at Converse-DnCNN's shape (B8, 64 / 128 channels, 256x256)
         g = torch.Generator(device=dev).manual_seed(3)
@@ -546,6 +554,8 @@ def main():
     ap.add_argument("--only", choices=["converse2d", "layernorm", "conv1x1", "copy", "dncnn", "usrnet", "backward",
                                        "cfg1", "cfg2", "pfa268", "tail", "oppath", "grid"],
                     help="run one kernel family alone (for rocprofv3)")
+    ap.add_argument("--grid-scale", type=int, default=2, choices=[1, 2, 3],
+                    help="scale of the speed-grid point --only grid runs")
     args = ap.parse_args()
 
     if args.cpu_worker:

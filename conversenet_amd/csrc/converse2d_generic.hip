@@ -1842,6 +1842,10 @@ extern "C" int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, in
   float2* SH = (float2*)(base + ws.SH);
   if (r.id == CVN_ROUTE_PFA268)
     return pfa268_forward(x, g.P, g.C, g.Cp / g.C, g.H, g.W, g.pad, pad_mode, act, phi, S, out, st);
+  if (module_ct_supported(g.h, g.w, g.s, g.pad) && (uintptr_t)x % 16 == 0 && (uintptr_t)out % 16 == 0)
+    return launch_module_ct(x, g.P, g.C, g.Cp / g.C, g.h, g.w, g.s, act, (const float2*)(tabs + t.off[kTabW]),
+                            (const float2*)(tabs + t.off[kTabH]), (const float2*)(tabs + t.off[kTabHs]),
+                            (const float2*)(tabs + t.off[kTabWs]), phi, S, SH, out, st);
   if ((rc = launch_rows_fwd(x, g.P, g.H, g.W, g.pad, pad_mode, g.h, g.w, tabs + t.off[kTabW], S, st)) != CVN_OK)
     return rc;
   ColModArgs ca;

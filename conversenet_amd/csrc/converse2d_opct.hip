@@ -210,7 +210,7 @@ __global__ void __launch_bounds__(kOpT) k_oprows_fwd(const float* __restrict__ x
 template <int L, int RPB>
 __global__ void __launch_bounds__(kOpT) k_oprows_inv(const float2* __restrict__ SH, int nrows, int nblk,
                                                      int64_t nitems, const float2* __restrict__ twg,
-                                                     float* __restrict__ out) {
+                                                     float* __restrict__ out, int act) {
   constexpr int NTR = RPB / 2, NC = L / 2 + 1, Q = L / 4, NST = NTR * Q;
   extern __shared__ float2 sm[];
   float2* tw = sm;
@@ -260,7 +260,13 @@ __global__ void __launch_bounds__(kOpT) k_oprows_inv(const float2* __restrict__ 
     const int t = idx / Q, c4 = idx - t * Q;
     const int ra = r0 + 2 * t;
     const float2* z = Z + lp(t * L + 4 * c4);  // four consecutive slots
-    const float2 z0 = z[0], z1 = z[1], z2 = z[2], z3 = z[3];
+    float2 z0 = z[0], z1 = z[1], z2 = z[2], z3 = z[3];
+    if (act == CVN_ACT_GELU) {
+      z0 = make_float2(gelu_fast(z0.x), gelu_fast(z0.y));
+      z1 = make_float2(gelu_fast(z1.x), gelu_fast(z1.y));
+      z2 = make_float2(gelu_fast(z2.x), gelu_fast(z2.y));
+      z3 = make_float2(gelu_fast(z3.x), gelu_fast(z3.y));
+    }
     if (ra < nrows) *(float4*)(op + (int64_t)ra * L + 4 * c4) = make_float4(z0.x, z1.x, z2.x, z3.x);
     if (ra + 1 < nrows) *(float4*)(op + (int64_t)(ra + 1) * L + 4 * c4) = make_float4(z0.y, z1.y, z2.y, z3.y);
   }
@@ -390,6 +396,85 @@ __global__ void __launch_bounds__(kOpT) k_opcols(OpColCtArgs a) {
   }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Columns, module form (x0 = nearest(y), util_converse.py:165-190): per (plane, CPB consecutive HR
+// columns v of the stored half), X(u, v) = Phi(u, v) Y(u mod H, v mod w) with Y the LR spectrum,
+// then the inverse HR column transform; the same product and table as k_cols_module.
+// ------------------------------------------------------------------------------------------------
+struct ModColCtArgs {
+  const float2* S;    // (P, w/2+1, H) LR row spectra
+  const float2* phi;  // (Cp, Ws/2+1, Hs) module table
+  float2* SH;         // (P, Ws/2+1, Hs)
+  const float2* tw_h; // LR column twiddles (H entries)
+  const float2* tw_H; // HR column twiddles (Hs entries)
+  int64_t C, psf_batch, nitems;  // nitems = P * nblk
+  int w, Ws, nblk;               // nblk = column blocks per plane
+};
+
+template <int H, int S, int CPB>
+__global__ void __launch_bounds__(kOpT) k_modcols(ModColCtArgs a) {
+  constexpr int HS = H * S;
+  extern __shared__ float2 sm[];
+  float2* twh = sm;
+  float2* twH = twh + H;
+  float2* Y = twH + HS;              // CPB LR columns
+  float2* X = Y + lp_size(CPB * H);  // CPB HR columns
+  const int tid = threadIdx.x;
+  const int NC = a.w / 2 + 1, NCs = a.Ws / 2 + 1;
+  // work item (plane, column block), planes of one channel adjacent (they share the table when
+  // psf_batch is 1): item = (c, b, block) with the block fastest
+  const int64_t item = xcd_item(blockIdx.x, a.nitems);
+  const int64_t pidx = item / a.nblk;
+  const int vbeg = (int)(item - pidx * a.nblk) * CPB;
+  const int64_t B = a.nitems / a.nblk / a.C;
+  const int64_t c = pidx / B, bi = pidx - c * B;
+  const int64_t plane = bi * a.C + c;
+  const int64_t cp = a.psf_batch == 1 ? c : plane;
+  const int ncol = min(CPB, NCs - vbeg);
+  const float2* Sp = a.S + plane * (int64_t)NC * H;
+  const float2* ph = a.phi + cp * (int64_t)NCs * HS;
+  constexpr int ITY = (CPB * H + kOpT - 1) / kOpT, ITX = (CPB * HS + kOpT - 1) / kOpT;
+  float2 ly[ITY], lf[ITX];
+#pragma unroll
+  for (int k = 0; k < ITY; ++k) {
+    const int idx = tid + k * kOpT;
+    const int cl = idx / H, u = idx - cl * H;
+    ly[k] = make_float2(0.f, 0.f);
+    if (idx < CPB * H && cl < ncol) {
+      const int vv = (vbeg + cl) % a.w;  // row spectra of real rows are Hermitian in the column
+      ly[k] = vv <= a.w / 2 ? Sp[(int64_t)vv * H + u] : cconj(Sp[(int64_t)(a.w - vv) * H + u]);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < ITX; ++k) {
+    const int idx = tid + k * kOpT;
+    const int cl = idx / HS, u = idx - cl * HS;
+    lf[k] = (idx < CPB * HS && cl < ncol) ? ph[(int64_t)(vbeg + cl) * HS + u] : make_float2(0.f, 0.f);
+  }
+  copy_tw(twh, a.tw_h, H, tid);
+  copy_tw(twH, a.tw_H, HS, tid);
+#pragma unroll
+  for (int k = 0; k < ITY; ++k)
+    if (tid + k * kOpT < CPB * H) Y[lp(tid + k * kOpT)] = ly[k];
+  __syncthreads();
+  op_fft<H, 0, false, CPB>(Y, twh, tid);
+#pragma unroll
+  for (int k = 0; k < ITX; ++k) {
+    const int idx = tid + k * kOpT;
+    if (idx < CPB * HS) {
+      const int cl = idx / HS, u = idx - cl * HS;
+      X[lp(idx)] = cmul(Y[lp(cl * H + u % H)], lf[k]);
+    }
+  }
+  __syncthreads();
+  op_fft<HS, 0, true, CPB>(X, twH, tid);
+  float2* SHp = a.SH + plane * (int64_t)NCs * HS;
+  for (int idx = tid; idx < ncol * HS; idx += kOpT) {
+    const int cl = idx / HS, u = idx - cl * HS;
+    SHp[(int64_t)(vbeg + cl) * HS + u] = X[lp(idx)];
+  }
+}
+
 // Rows per block of the row passes, by length (LDS: about L + RPB L complex values, at most ~72 KB).
 template <int L>
 constexpr int op_rpb() {
@@ -422,14 +507,14 @@ int launch_oprows_fwd(const float* x, int64_t P, int nrows, const float2* tw, fl
 }
 
 template <int L>
-int launch_oprows_inv(const float2* SH, int64_t P, int nrows, const float2* tw, float* out, hipStream_t st) {
+int launch_oprows_inv(const float2* SH, int64_t P, int nrows, const float2* tw, float* out, int act, hipStream_t st) {
   constexpr int RPB = op_rpb<L>();
   const size_t lds = (size_t)(L + lp_size(RPB / 2 * L) + op_inv_bf<L>()) * sizeof(float2);
   static std::atomic<uint64_t> done{0};
   raise_lds_limit(k_oprows_inv<L, RPB>, done);
   const int nblk = (nrows + RPB - 1) / RPB;
   hipLaunchKernelGGL((k_oprows_inv<L, RPB>), dim3((unsigned)(nblk * P)), dim3(kOpT), lds, st, SH, nrows, nblk,
-                     (int64_t)nblk * P, tw, out);
+                     (int64_t)nblk * P, tw, out, act);
   return check_launch("op row inverse pass (compile-time plan)");
 }
 
@@ -441,6 +526,18 @@ int launch_opcols(const OpColCtArgs& a, int64_t P, hipStream_t st) {
   raise_lds_limit(k_opcols<H, S>, done);
   hipLaunchKernelGGL((k_opcols<H, S>), dim3((unsigned)a.nitems), dim3(kOpT), lds, st, a);
   return check_launch("op column pass (compile-time plan)");
+}
+
+template <int H, int S>
+int launch_modcols(ModColCtArgs a, int64_t P, hipStream_t st) {
+  constexpr int HS = H * S, CPB = HS >= 512 ? 1 : (HS >= 256 ? 2 : 4);
+  const size_t lds = (size_t)(H + HS + lp_size(CPB * H) + lp_size(CPB * HS)) * sizeof(float2);
+  a.nblk = (a.Ws / 2 + 1 + CPB - 1) / CPB;
+  a.nitems = P * a.nblk;
+  static std::atomic<uint64_t> done{0};
+  raise_lds_limit(k_modcols<H, S, CPB>, done);
+  hipLaunchKernelGGL((k_modcols<H, S, CPB>), dim3((unsigned)a.nitems), dim3(kOpT), lds, st, a);
+  return check_launch("module column pass (compile-time plan)");
 }
 
 bool op_len_ok(int L) {
@@ -464,15 +561,16 @@ int rows_fwd_any(int L, const float* x, int64_t P, int nrows, const float2* tw, 
   }
 }
 
-int rows_inv_any(int L, const float2* SH, int64_t P, int nrows, const float2* tw, float* out, hipStream_t st) {
+int rows_inv_any(int L, const float2* SH, int64_t P, int nrows, const float2* tw, float* out, int act,
+                 hipStream_t st) {
   switch (L) {
-    case 128: return launch_oprows_inv<128>(SH, P, nrows, tw, out, st);
-    case 192: return launch_oprows_inv<192>(SH, P, nrows, tw, out, st);
-    case 256: return launch_oprows_inv<256>(SH, P, nrows, tw, out, st);
-    case 384: return launch_oprows_inv<384>(SH, P, nrows, tw, out, st);
-    case 512: return launch_oprows_inv<512>(SH, P, nrows, tw, out, st);
-    case 768: return launch_oprows_inv<768>(SH, P, nrows, tw, out, st);
-    case 1024: return launch_oprows_inv<1024>(SH, P, nrows, tw, out, st);
+    case 128: return launch_oprows_inv<128>(SH, P, nrows, tw, out, act, st);
+    case 192: return launch_oprows_inv<192>(SH, P, nrows, tw, out, act, st);
+    case 256: return launch_oprows_inv<256>(SH, P, nrows, tw, out, act, st);
+    case 384: return launch_oprows_inv<384>(SH, P, nrows, tw, out, act, st);
+    case 512: return launch_oprows_inv<512>(SH, P, nrows, tw, out, act, st);
+    case 768: return launch_oprows_inv<768>(SH, P, nrows, tw, out, act, st);
+    case 1024: return launch_oprows_inv<1024>(SH, P, nrows, tw, out, act, st);
     default: return fail(CVN_ERR_UNSUPPORTED, "no compile-time row plan for length %d", L);
   }
 }
@@ -493,6 +591,21 @@ int cols_any(int h, int s, const OpColCtArgs& a, int64_t P, hipStream_t st) {
   }
 }
 
+int modcols_any(int h, int s, const ModColCtArgs& a, int64_t P, hipStream_t st) {
+  switch (h * 8 + s) {
+    case 64 * 8 + 2: return launch_modcols<64, 2>(a, P, st);
+    case 64 * 8 + 3: return launch_modcols<64, 3>(a, P, st);
+    case 64 * 8 + 4: return launch_modcols<64, 4>(a, P, st);
+    case 128 * 8 + 2: return launch_modcols<128, 2>(a, P, st);
+    case 128 * 8 + 3: return launch_modcols<128, 3>(a, P, st);
+    case 128 * 8 + 4: return launch_modcols<128, 4>(a, P, st);
+    case 256 * 8 + 2: return launch_modcols<256, 2>(a, P, st);
+    case 256 * 8 + 3: return launch_modcols<256, 3>(a, P, st);
+    case 256 * 8 + 4: return launch_modcols<256, 4>(a, P, st);
+    default: return fail(CVN_ERR_UNSUPPORTED, "no compile-time column plan for h = %d, s = %d", h, s);
+  }
+}
+
 bool opct_disabled() {
   static const bool off = [] {
     const char* e = getenv("CVN_DISABLE_OPCT");
@@ -502,6 +615,23 @@ bool opct_disabled() {
 }
 
 }  // namespace
+
+bool module_ct_supported(int h, int w, int s, int pad) { return pad == 0 && op_ct_supported(h, w, s); }
+
+int launch_module_ct(const float* x, int64_t P, int64_t C, int64_t psf_batch, int h, int w, int s, int act,
+                     const float2* tw_w, const float2* tw_h, const float2* tw_Hs, const float2* tw_Ws,
+                     const float2* phi, float2* S, float2* SH, float* out, hipStream_t st) {
+  if (!module_ct_supported(h, w, s, 0)) return fail(CVN_ERR_UNSUPPORTED, "module path: no compile-time plan");
+  if ((uintptr_t)x % 16 || (uintptr_t)out % 16)
+    return fail(CVN_ERR_UNSUPPORTED, "module path: compile-time kernels need 16-byte aligned planes");
+  int rc;
+  if ((rc = rows_fwd_any(w, x, P, h, tw_w, S, st)) != CVN_OK) return rc;
+  ModColCtArgs ca;
+  ca.S = S; ca.phi = phi; ca.SH = SH; ca.tw_h = tw_h; ca.tw_H = tw_Hs;
+  ca.C = C; ca.psf_batch = psf_batch; ca.w = w; ca.Ws = w * s; ca.nblk = 0; ca.nitems = 0;
+  if ((rc = modcols_any(h, s, ca, P, st)) != CVN_OK) return rc;
+  return rows_inv_any(w * s, SH, P, h * s, tw_Ws, out, act, st);
+}
 
 bool op_ct_supported(int h, int w, int s) {
   if (opct_disabled() || s < 2 || s > 4) return false;
@@ -523,7 +653,7 @@ int launch_op_ct(const float* x, const float* x0, int64_t P, int64_t C, int h, i
   ca.S = S; ca.S0 = S0; ca.kf = kf; ca.A = A; ca.SH = SH; ca.tw_h = tw_h; ca.tw_H = tw_Hs;
   ca.B = P / C; ca.C = C; ca.nitems = P * (w / 2 + 1); ca.w = w; ca.Ws = w * s;
   if ((rc = cols_any(h, s, ca, P, st)) != CVN_OK) return rc;
-  return rows_inv_any(w * s, SH, P, h * s, tw_Ws, out, st);
+  return rows_inv_any(w * s, SH, P, h * s, tw_Ws, out, CVN_ACT_NONE, st);
 }
 
 }  // namespace cvn

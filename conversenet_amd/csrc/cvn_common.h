@@ -198,5 +198,12 @@ bool op_ct_supported(int h, int w, int s);
 int launch_op_ct(const float* x, const float* x0, int64_t P, int64_t C, int h, int w, int s, const float2* tw_w,
                  const float2* tw_h, const float2* tw_Hs, const float2* tw_Ws, const float2* kf, const float2* A,
                  float2* S, float2* S0, float2* SH, float* out, hipStream_t st);
+// Module path (x0 = nearest(y)) at scale 2-4 with no padding on the same compile-time plans: LR rows,
+// the module column pass (Phi times the tiled LR spectrum, inverse HR columns), HR rows with act.
+// Same scratch (S, SH) and table (kPhiGeneric layout) as the generic module path.
+bool module_ct_supported(int h, int w, int s, int pad);
+int launch_module_ct(const float* x, int64_t P, int64_t C, int64_t psf_batch, int h, int w, int s, int act,
+                     const float2* tw_w, const float2* tw_h, const float2* tw_Hs, const float2* tw_Ws,
+                     const float2* phi, float2* S, float2* SH, float* out, hipStream_t st);
 
 }  // namespace cvn

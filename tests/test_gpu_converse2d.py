@@ -460,6 +460,39 @@ def test_op_level_planned(B, C, h, w, s, k, x0kind):
     assert err <= TOL
 
 
+# (B, C, h, w, s, k, psf batch, act): module-level calls on the generic route with no padding and
+# compile-time plans for h, w, h s and w s (the module column kernel k_modcols); the first is
+# Converse-USRNet's first data step (converse_usrnet.py:205, 64^2 -> 256^2, per-sample 25 x 25 psf)
+MODULE_PLANNED = [(4, 8, 64, 64, 4, 25, 4, None), (2, 3, 64, 128, 2, 5, 1, "gelu"), (1, 2, 128, 64, 3, 7, 1, None),
+                  (2, 2, 256, 256, 2, 3, 2, None), (1, 2, 128, 192, 2, 4, 1, "gelu"), (1, 1, 256, 64, 4, 9, 1, None),
+                  (1, 2, 64, 256, 3, 5, 1, None)]
+
+
+@pytest.mark.parametrize("B,C,h,w,s,k,pb,act", MODULE_PLANNED)
+def test_module_planned_scale(B, C, h, w, s, k, pb, act):
+    """Converse2D module path (util_converse.py:142-192) at scale > 1 without padding on the compile-time
+    plans, against the fp64 oracle, max-abs <= 1e-4."""
+    from conversenet_amd import _lib
+    from conversenet_amd import functional as Fh
+    lib = _lib.load()
+    assert lib.cvn_converse2d_route(B, C, h, w, pb, k, k, s, 0) == _lib.ROUTE_GENERIC
+    assert lib.cvn_converse2d_op_route(h, w, s) == _lib.ROUTE_OP_PLANNED  # the lengths have plans
+    rng = seeded("module-planned", B, C, h, w, s, k, pb, act)
+    x = rng.standard_normal((B, C, h, w)).astype(np.float32)
+    wt = (0.05 * rng.standard_normal((pb, C, k, k))).astype(np.float32) if pb > 1 else softmax_psf(rng, C, k)
+    b = (0.3 * rng.standard_normal((1, C, 1, 1))).astype(np.float32)
+    dev = torch.device("cuda")
+    got = Fh.converse2d_fused(torch.from_numpy(x).to(dev), torch.from_numpy(wt).to(dev),
+                              torch.from_numpy(b).to(dev).reshape(-1), s, 0, "circular", 1e-3, act,
+                              cache=False).cpu().numpy()
+    ref = O.converse2d_module(x, wt, b, s, 0, "circular", 1e-3)
+    if act == "gelu":
+        ref = O.gelu(ref)
+    err = float(np.abs(got - ref).max())
+    print(f"module planned B{B} C{C} {h}x{w} s{s} k{k} psf batch {pb} act {act}: max-abs {err:.3e}")
+    assert err <= TOL
+
+
 @pytest.mark.parametrize("s,h,w", [(1, 30, 26), (4, 30, 26), (1, 32, 48), (2, 24, 20), (4, 16, 12)])
 def test_op_level_large_psf(s, h, w):
     from conversenet_amd import functional as Fh
