@@ -646,9 +646,11 @@ struct RowFwdArgs {
   float2* S;       // (P, NC, h)
 };
 
+// LC > 0: the row length a.w, fixed at compile time (fft_fixed_ct; constant index arithmetic).
+template <int LC>
 __global__ void __launch_bounds__(256) k_rows_fwd(RowFwdArgs a) {
   extern __shared__ float2 sm[];
-  const int L = a.w, ntr = a.rpb / 2, ld = L + 2;
+  const int L = LC > 0 ? LC : a.w, ntr = a.rpb / 2, ld = L + 2;
   float2* tw = sm;
   float2* A = tw + L;
   float2* Bf = A + ntr * ld;
@@ -656,7 +658,12 @@ __global__ void __launch_bounds__(256) k_rows_fwd(RowFwdArgs a) {
   const int r0 = blockIdx.x * a.rpb;
   const int tid = threadIdx.x, nth = blockDim.x;
   char* rad = (char*)sm + a.rad_off;
-  load_plan_tabs(a.plan, a.tabs, tw, rad, tid, nth);
+  if constexpr (LC > 0) {  // the twiddles only (no Rader stage at these lengths)
+    const float2* gt = (const float2*)a.tabs;
+    for (int m = tid; m < LC; m += nth) tw[m] = gt[m];
+  } else {
+    load_plan_tabs(a.plan, a.tabs, tw, rad, tid, nth);
+  }
   const float* xp = a.x + plane * (int64_t)a.Hin * a.Win;
   const FastDiv fL = fast_div(L), frpb = fast_div(a.rpb);
   for (int i0 = tid; i0 < ntr * L; i0 += kBatch * nth) {
@@ -688,7 +695,9 @@ __global__ void __launch_bounds__(256) k_rows_fwd(RowFwdArgs a) {
     }
   }
   __syncthreads();
-  const float2* Z = fft_lds<false>(a.plan, A, Bf, ntr, tw, tid, nth, rad);
+  const float2* Z;
+  if constexpr (LC > 0) Z = fft_fixed_ct<LC, 0, false>(A, Bf, ntr, tw, tid, nth);
+  else Z = fft_lds<false>(a.plan, A, Bf, ntr, tw, tid, nth, rad);
   // unpack two real rows: Ya = (Z[c] + conj Z[-c]) / 2, Yb = (Z[c] - conj Z[-c]) / (2i)
   float2* Sp = a.S + plane * (int64_t)a.NC * a.h;
   for (int idx = tid; idx < a.NC * a.rpb; idx += nth) {
@@ -897,17 +906,23 @@ struct RowInvArgs {
   int rad_off;       // byte offset of the plan's Rader tables in LDS
 };
 
+template <int LC>  // LC > 0: the row length a.Ws, fixed at compile time
 __global__ void __launch_bounds__(256) k_rows_inv(RowInvArgs a) {
   extern __shared__ float2 sm[];
   const int tid = threadIdx.x, nth = blockDim.x;
-  const int L = a.Ws, ntr = a.rpb / 2, ld = L + 2;
+  const int L = LC > 0 ? LC : a.Ws, ntr = a.rpb / 2, ld = L + 2;
   float2* tw = sm;
   float2* A = tw + L;
   float2* Bf = A + ntr * ld;
   const int64_t plane = blockIdx.y;
   const int r0 = blockIdx.x * a.rpb;  // local output row
   char* rad = (char*)sm + a.rad_off;
-  load_plan_tabs(a.plan, a.tabs, tw, rad, tid, nth);
+  if constexpr (LC > 0) {  // the twiddles only (no Rader stage at these lengths)
+    const float2* gt = (const float2*)a.tabs;
+    for (int m = tid; m < LC; m += nth) tw[m] = gt[m];
+  } else {
+    load_plan_tabs(a.plan, a.tabs, tw, rad, tid, nth);
+  }
   int* csrc = (int*)((char*)sm + a.csrc_off);
   if (a.pad >= 0 && a.pmode != CVN_PAD_ZEROS)
     for (int q = tid; q < 2 * a.pad; q += nth)
@@ -946,7 +961,9 @@ __global__ void __launch_bounds__(256) k_rows_inv(RowInvArgs a) {
     A[t * L + v] = make_float2(ha.x - hb.y, ha.y + hb.x);
   }
   __syncthreads();
-  const float2* Z = fft_lds<true>(a.plan, A, Bf, ntr, tw, tid, nth, rad);
+  const float2* Z;
+  if constexpr (LC > 0) Z = fft_fixed_ct<LC, 0, true>(A, Bf, ntr, tw, tid, nth);
+  else Z = fft_lds<true>(a.plan, A, Bf, ntr, tw, tid, nth, rad);
   if (a.pad >= 0) {
     const int pad = a.pad, Hd = a.nrows - 2 * pad, Wd = a.ncols - 2 * pad;
     const int nb = (a.pmode == CVN_PAD_ZEROS) ? 0 : 2 * pad;
@@ -1034,57 +1051,70 @@ constexpr int kColsBwdThreads = 512;  // 2 blocks of 8 waves per CU at the cfg3 
 constexpr int kColRegs = 4;           // per-thread register slots of the scale-1 path
 constexpr int kColLoad = 4;           // column elements per array loaded per thread and batch
 
-__global__ void __launch_bounds__(kColsBwdThreads) k_cols_bwd(ColBwdArgs a) {
+// HC > 0: scale 1 with the column length h = Hs fixed at compile time (fft_fixed_ct).
+// Four waves per SIMD (at most 128 VGPRs): two blocks per CU, which the LDS size allows at cfg3.
+template <int HC>
+__global__ void __launch_bounds__(kColsBwdThreads, 4) k_cols_bwd(ColBwdArgs a) {
   extern __shared__ float2 sm[];
   const int tid = threadIdx.x, nth = blockDim.x;
   const bool wg = a.dphi != nullptr;
-  const int cpb = a.cpb, sH = a.s * a.Hs;
+  // scale, LR and HR column lengths (constants when HC > 0; the argument struct is left unmodified,
+  // so that it is not copied to scratch)
+  const int as = HC > 0 ? 1 : a.s, ah = HC > 0 ? HC : a.h, aHs = HC > 0 ? HC : a.Hs;
+  const int cpb = a.cpb, sH = as * aHs;
   float2* twh = sm;
-  float2* twH = twh + a.h;
-  float2* Ya = twH + a.Hs;           // cpb h: Y (LR column spectra of pad x)
-  float2* Yb = Ya + cpb * a.h;       // cpb h
-  float2* Yc = Yb + cpb * a.h;       // cpb h: dY
-  float2* Xa = Yc + cpb * a.h;       // cpb s Hs: dZ
+  float2* twH = twh + ah;
+  float2* Ya = twH + aHs;           // cpb h: Y (LR column spectra of pad x)
+  float2* Yb = Ya + cpb * ah;       // cpb h
+  float2* Yc = Yb + cpb * ah;       // cpb h: dY
+  float2* Xa = Yc + cpb * ah;       // cpb s Hs: dZ
   float2* Xb = Xa + cpb * sH;        // cpb s Hs
   float2* acc = Xb + cpb * sH;       // cpb s Hs: dPhi (weight gradients only)
   const int vbase = blockIdx.x * cpb;
   const int ncol = min(cpb, a.NC - vbase);
   const int64_t grp = blockIdx.y;    // psf plane: c (psf_batch 1) or the plane (psf_batch B)
-  char* radh = (char*)sm + a.rad_off;
-  char* radH = radh + rader_lds_bytes(a.plan_h);
-  load_plan_tabs(a.plan_h, a.tabs_h, twh, radh, tid, nth);
-  if (a.Hs != a.h) load_plan_tabs(a.plan_H, a.tabs_H, twH, radH, tid, nth);
-  else radH = radh;
-  const float2* tH = (a.Hs != a.h) ? twH : twh;
-  const float2* ph = a.phi + grp * (int64_t)a.NCs * a.Hs;
-  const FastDiv fHs = fast_div(a.Hs), fh = fast_div(a.h), fsH = fast_div(sH);
-  const float norm = 1.0f / ((float)a.Hs * (float)a.Ws);
+  char* radh = nullptr;
+  char* radH = nullptr;
+  if constexpr (HC > 0) {  // the twiddles only (no Rader stage at these lengths)
+    const float2* gt = (const float2*)a.tabs_h;
+    for (int m = tid; m < HC; m += nth) twh[m] = gt[m];
+  } else {
+    radh = (char*)sm + a.rad_off;
+    radH = radh + rader_lds_bytes(a.plan_h);
+    load_plan_tabs(a.plan_h, a.tabs_h, twh, radh, tid, nth);
+    if (aHs != ah) load_plan_tabs(a.plan_H, a.tabs_H, twH, radH, tid, nth);
+    else radH = radh;
+  }
+  const float2* tH = (aHs != ah) ? twH : twh;
+  const float2* ph = a.phi + grp * (int64_t)a.NCs * aHs;
+  const FastDiv fHs = fast_div(aHs), fh = fast_div(ah), fsH = fast_div(sH);
+  const float norm = 1.0f / ((float)aHs * (float)a.Ws);
   if (wg)
     for (int i = tid; i < cpb * sH; i += nth) acc[i] = make_float2(0.f, 0.f);
   // Scale 1 with at most kColRegs elements per thread: every class has one member column (vb =
   // vbase + cl <= Ws / 2) and one row per bin, so element idx = cl h + u of this thread is the same
   // in every plane; its conj(Phi') is read from HBM once and the dPhi sum stays in registers.
-  const bool regs = a.s == 1 && cpb * a.h <= kColRegs * nth;
+  const bool regs = as == 1 && cpb * ah <= kColRegs * nth;
   float2 fr[kColRegs], ar[kColRegs];
   if (regs) {
 #pragma unroll
     for (int k = 0; k < kColRegs; ++k) {
       const int idx = tid + k * nth;
       const int cl = idx / fh;
-      fr[k] = (cl < ncol) ? cconj(ph[(int64_t)(vbase + cl) * a.Hs + (idx - cl * a.h)]) : make_float2(0.f, 0.f);
+      fr[k] = (cl < ncol) ? cconj(ph[(int64_t)(vbase + cl) * aHs + (idx - cl * ah)]) : make_float2(0.f, 0.f);
       ar[k] = make_float2(0.f, 0.f);
     }
   }
   const int64_t nplanes = (a.psf_batch == 1) ? a.B : 1;
   for (int64_t ib = 0; ib < nplanes; ++ib) {
     const int64_t plane = (a.psf_batch == 1) ? ib * a.C + grp : grp;
-    const float2* Sgp = a.Sg + plane * (int64_t)a.NCs * a.Hs;
-    float2* Sxp = a.Sx + plane * (int64_t)a.NC * a.h;
+    const float2* Sgp = a.Sg + plane * (int64_t)a.NCs * aHs;
+    float2* Sxp = a.Sx + plane * (int64_t)a.NC * ah;
     __syncthreads();  // the previous plane's LDS reads are done
     // member columns vb = v0 + b w of each class (row spectra of real rows are Hermitian in the
     // column); the Sg and Sx loads of a batch are all issued before the first LDS store, so a
     // plane waits for one HBM round trip, not two
-    const int nG = cpb * sH, nX = wg ? cpb * a.h : 0;
+    const int nG = cpb * sH, nX = wg ? cpb * ah : 0;
     for (int i0 = tid; i0 < max(nG, nX); i0 += kColLoad * nth) {
       float2 vg[kColLoad], vx[kColLoad];
 #pragma unroll
@@ -1094,13 +1124,13 @@ __global__ void __launch_bounds__(kColsBwdThreads) k_cols_bwd(ColBwdArgs a) {
         vx[k] = make_float2(0.f, 0.f);
         if (idx < nG) {
           const int cl = idx / fsH, r = idx - cl * sH;
-          const int b = r / fHs, u = r - b * a.Hs;
+          const int b = r / fHs, u = r - b * aHs;
           if (cl < ncol) {
             const int vb = vbase + cl + b * a.w;
-            vg[k] = vb <= a.Ws / 2 ? Sgp[(int64_t)vb * a.Hs + u] : cconj(Sgp[(int64_t)(a.Ws - vb) * a.Hs + u]);
+            vg[k] = vb <= a.Ws / 2 ? Sgp[(int64_t)vb * aHs + u] : cconj(Sgp[(int64_t)(a.Ws - vb) * aHs + u]);
           }
         }
-        if (idx < nX && idx < ncol * a.h) vx[k] = Sxp[(int64_t)vbase * a.h + idx];  // columns vbase.. are contiguous
+        if (idx < nX && idx < ncol * ah) vx[k] = Sxp[(int64_t)vbase * ah + idx];  // columns vbase.. are contiguous
       }
 #pragma unroll
       for (int k = 0; k < kColLoad; ++k) {
@@ -1110,13 +1140,19 @@ __global__ void __launch_bounds__(kColsBwdThreads) k_cols_bwd(ColBwdArgs a) {
       }
     }
     __syncthreads();
-    const float2* dZ = fft_lds<false>(a.plan_H, Xa, Xb, cpb * a.s, tH, tid, nth, radH);
-    const float2* Y = wg ? fft_lds<false>(a.plan_h, Ya, Yb, cpb, twh, tid, nth, radh) : nullptr;
+    const float2 *dZ, *Y = nullptr;
+    if constexpr (HC > 0) {
+      dZ = fft_fixed_ct<HC, 0, false>(Xa, Xb, cpb, tH, tid, nth);
+      if (wg) Y = fft_fixed_ct<HC, 0, false>(Ya, Yb, cpb, twh, tid, nth);
+    } else {
+      dZ = fft_lds<false>(a.plan_H, Xa, Xb, cpb * as, tH, tid, nth, radH);
+      if (wg) Y = fft_lds<false>(a.plan_h, Ya, Yb, cpb, twh, tid, nth, radh);
+    }
     if (regs) {
 #pragma unroll
       for (int k = 0; k < kColRegs; ++k) {
         const int idx = tid + k * nth;
-        if (idx < cpb * a.h) {
+        if (idx < cpb * ah) {
           const float2 z = dZ[idx];
           if (wg) {
             const float2 t = cmul(cconj(Y[idx]), z);
@@ -1130,23 +1166,23 @@ __global__ void __launch_bounds__(kColsBwdThreads) k_cols_bwd(ColBwdArgs a) {
       if (wg) {
         for (int idx = tid; idx < cpb * sH; idx += nth) {
           const int cl = idx / fsH, r = idx - cl * sH;
-          const int u = r - (r / fHs) * a.Hs;
-          const float2 t = cmul(cconj(Y[cl * a.h + u - (u / fh) * a.h]), dZ[idx]);
+          const int u = r - (r / fHs) * aHs;
+          const float2 t = cmul(cconj(Y[cl * ah + u - (u / fh) * ah]), dZ[idx]);
           acc[idx].x = fmaf(t.x, norm, acc[idx].x);
           acc[idx].y = fmaf(t.y, norm, acc[idx].y);
         }
       }
-      for (int idx = tid; idx < cpb * a.h; idx += nth) {
-        const int cl = idx / fh, u0 = idx - cl * a.h;
+      for (int idx = tid; idx < cpb * ah; idx += nth) {
+        const int cl = idx / fh, u0 = idx - cl * ah;
         float2 m = make_float2(0.f, 0.f);
         if (cl < ncol) {
-          for (int b = 0; b < a.s; ++b) {
+          for (int b = 0; b < as; ++b) {
             const int vb = vbase + cl + b * a.w;
-            for (int aa = 0; aa < a.s; ++aa) {
-              const int u = u0 + aa * a.h;
-              const float2 f = vb <= a.Ws / 2 ? ph[(int64_t)vb * a.Hs + u]
-                                              : cconj(ph[(int64_t)(a.Ws - vb) * a.Hs + (u == 0 ? 0 : a.Hs - u)]);
-              const float2 t = cmul(cconj(f), dZ[cl * sH + b * a.Hs + u]);
+            for (int aa = 0; aa < as; ++aa) {
+              const int u = u0 + aa * ah;
+              const float2 f = vb <= a.Ws / 2 ? ph[(int64_t)vb * aHs + u]
+                                              : cconj(ph[(int64_t)(a.Ws - vb) * aHs + (u == 0 ? 0 : aHs - u)]);
+              const float2 t = cmul(cconj(f), dZ[cl * sH + b * aHs + u]);
               m.x += t.x;
               m.y += t.y;
             }
@@ -1156,26 +1192,28 @@ __global__ void __launch_bounds__(kColsBwdThreads) k_cols_bwd(ColBwdArgs a) {
       }
     }
     __syncthreads();
-    const float2* R = fft_lds<true>(a.plan_h, Yc, Ya, cpb, twh, tid, nth, radh);
-    for (int idx = tid; idx < ncol * a.h; idx += nth) Sxp[(int64_t)vbase * a.h + idx] = R[idx];
+    const float2* R;
+    if constexpr (HC > 0) R = fft_fixed_ct<HC, 0, true>(Yc, Ya, cpb, twh, tid, nth);
+    else R = fft_lds<true>(a.plan_h, Yc, Ya, cpb, twh, tid, nth, radh);
+    for (int idx = tid; idx < ncol * ah; idx += nth) Sxp[(int64_t)vbase * ah + idx] = R[idx];
   }
   if (wg && regs) {
-    float2* dp = a.dphi + grp * (int64_t)a.Ws * a.Hs;
+    float2* dp = a.dphi + grp * (int64_t)a.Ws * aHs;
 #pragma unroll
     for (int k = 0; k < kColRegs; ++k) {
       const int idx = tid + k * nth;
-      if (idx < ncol * a.h) {
+      if (idx < ncol * ah) {
         const int cl = idx / fh;
-        dp[(int64_t)(vbase + cl) * a.Hs + (idx - cl * a.h)] = ar[k];
+        dp[(int64_t)(vbase + cl) * aHs + (idx - cl * ah)] = ar[k];
       }
     }
   } else if (wg) {
     __syncthreads();
-    float2* dp = a.dphi + grp * (int64_t)a.Ws * a.Hs;
+    float2* dp = a.dphi + grp * (int64_t)a.Ws * aHs;
     for (int idx = tid; idx < ncol * sH; idx += nth) {
       const int cl = idx / fsH, r = idx - cl * sH;
-      const int b = r / fHs, u = r - b * a.Hs;
-      dp[(int64_t)(vbase + cl + b * a.w) * a.Hs + u] = acc[idx];
+      const int b = r / fHs, u = r - b * aHs;
+      dp[(int64_t)(vbase + cl + b * a.w) * aHs + u] = acc[idx];
     }
   }
 }
@@ -1445,11 +1483,13 @@ constexpr size_t kLdsLimit = 160 * 1024;
 std::atomic<uint64_t> g_attr_done{0};
 void set_lds_attrs() {
   once_per_device(g_attr_done, [] {
-    (void)hipFuncSetAttribute((const void*)k_rows_fwd, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
+    for (const void* k : {(const void*)k_rows_fwd<0>, (const void*)k_rows_fwd<132>, (const void*)k_rows_fwd<256>,
+                          (const void*)k_rows_fwd<260>, (const void*)k_rows_inv<0>, (const void*)k_rows_inv<132>,
+                          (const void*)k_rows_inv<256>, (const void*)k_rows_inv<260>, (const void*)k_cols_bwd<0>,
+                          (const void*)k_cols_bwd<132>, (const void*)k_cols_bwd<256>, (const void*)k_cols_bwd<260>})
+      (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
     (void)hipFuncSetAttribute((const void*)k_cols_module, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
     (void)hipFuncSetAttribute((const void*)k_cols_op, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
-    (void)hipFuncSetAttribute((const void*)k_rows_inv, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
-    (void)hipFuncSetAttribute((const void*)k_cols_bwd, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
     (void)hipFuncSetAttribute((const void*)k_phi_grad<1>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
     (void)hipFuncSetAttribute((const void*)k_phi_grad<2>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
     (void)hipFuncSetAttribute((const void*)k_phi_grad<3>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsLimit);
@@ -1615,7 +1655,13 @@ int launch_rows_fwd(const float* x, int64_t P, int Hin, int Win, int pad, int mo
   a.tabs = tabs;
   a.S = S;
   dim3 grid((h + a.rpb - 1) / a.rpb, (unsigned)P);
-  hipLaunchKernelGGL(k_rows_fwd, grid, dim3(kThreads), a.rad_off + rader_lds_bytes(a.plan), st, a);
+  const size_t lds = a.rad_off + rader_lds_bytes(a.plan);
+  switch (w) {  // lengths with a compile-time plan
+    case 132: hipLaunchKernelGGL(k_rows_fwd<132>, grid, dim3(kThreads), lds, st, a); break;
+    case 256: hipLaunchKernelGGL(k_rows_fwd<256>, grid, dim3(kThreads), lds, st, a); break;
+    case 260: hipLaunchKernelGGL(k_rows_fwd<260>, grid, dim3(kThreads), lds, st, a); break;
+    default: hipLaunchKernelGGL(k_rows_fwd<0>, grid, dim3(kThreads), lds, st, a); break;
+  }
   return check_launch("row forward pass");
 }
 
@@ -1632,7 +1678,13 @@ int launch_rows_inv(const float2* SH, const Geo& g, int row0, int nrows, int col
   a.csrc_off = (int)(a.rad_off + rader_lds_bytes(a.plan));
   a.tabs = tabs;
   dim3 grid((nrows + a.rpb - 1) / a.rpb, (unsigned)g.P);
-  hipLaunchKernelGGL(k_rows_inv, grid, dim3(kThreads), a.csrc_off + sizeof(int) * 2 * std::max(pad, 0), st, a);
+  const size_t lds = a.csrc_off + sizeof(int) * 2 * std::max(pad, 0);
+  switch (g.Ws) {  // lengths with a compile-time plan
+    case 132: hipLaunchKernelGGL(k_rows_inv<132>, grid, dim3(kThreads), lds, st, a); break;
+    case 256: hipLaunchKernelGGL(k_rows_inv<256>, grid, dim3(kThreads), lds, st, a); break;
+    case 260: hipLaunchKernelGGL(k_rows_inv<260>, grid, dim3(kThreads), lds, st, a); break;
+    default: hipLaunchKernelGGL(k_rows_inv<0>, grid, dim3(kThreads), lds, st, a); break;
+  }
   return check_launch("row inverse pass");
 }
 
@@ -2090,7 +2142,13 @@ extern "C" int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int
     a.rad_off = (int)align_up(cols_bwd_lds(g.h, g.Hs, g.s, a.cpb, wg), 16);
     const size_t lds = col_lds;
     const dim3 grid((unsigned)((g.NC + a.cpb - 1) / a.cpb), (unsigned)(a.psf_batch == 1 ? g.C : g.P));
-    hipLaunchKernelGGL(k_cols_bwd, grid, dim3(kColsBwdThreads), lds, st, a);
+    const int hc = g.s == 1 ? g.h : 0;  // column lengths with a compile-time plan (scale 1)
+    switch (hc) {
+      case 132: hipLaunchKernelGGL(k_cols_bwd<132>, grid, dim3(kColsBwdThreads), lds, st, a); break;
+      case 256: hipLaunchKernelGGL(k_cols_bwd<256>, grid, dim3(kColsBwdThreads), lds, st, a); break;
+      case 260: hipLaunchKernelGGL(k_cols_bwd<260>, grid, dim3(kColsBwdThreads), lds, st, a); break;
+      default: hipLaunchKernelGGL(k_cols_bwd<0>, grid, dim3(kColsBwdThreads), lds, st, a); break;
+    }
     if ((rc = check_launch("backward column pass")) != CVN_OK) return rc;
   }
   // dx = pad^T(C2R rows of dS): interior rows and the column folds on the row pass's store, the

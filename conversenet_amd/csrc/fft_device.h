@@ -611,4 +611,44 @@ __device__ __forceinline__ float2* fft_lds(const FftPlan& plan, float2* a, float
   return src;
 }
 
+// The fixed-radix decomposition of a compile-time length L (the order fixed_radices uses: 8s, then
+// 4 / 2 for the rest of the power of two, then 3, 5, 7, 11, 13); count 0 when L has another factor.
+struct FixedRadices {
+  int n;
+  int r[kMaxStages];
+};
+constexpr FixedRadices fixed_radices_ct(int L) {
+  FixedRadices f{0, {}};
+  while (L % 8 == 0 && f.n < kMaxStages) { f.r[f.n++] = 8; L /= 8; }
+  while (L % 4 == 0 && f.n < kMaxStages) { f.r[f.n++] = 4; L /= 4; }
+  while (L % 2 == 0 && f.n < kMaxStages) { f.r[f.n++] = 2; L /= 2; }
+  const int odd[5] = {3, 5, 7, 11, 13};
+  for (int i = 0; i < 5; ++i)
+    while (L % odd[i] == 0 && f.n < kMaxStages) { f.r[f.n++] = odd[i]; L /= odd[i]; }
+  if (L != 1) f.n = 0;
+  return f;
+}
+
+// fft_lds on a compile-time length L (fixed radices only): every pass's radix, stride and twiddle
+// step is a constant, so each kernel carries only the butterflies its length uses.  Same placement
+// and twiddle table (exp(-2 pi i m / L), m < L) as fft_lds, same result buffer.
+template <int L, int ST, bool INV>
+__device__ __forceinline__ float2* fft_fixed_ct(float2* a, float2* b, int ntr, const float2* tw, int tid, int nth) {
+  constexpr FixedRadices f = fixed_radices_ct(L);
+  static_assert(f.n > 0, "length without a fixed-radix plan");
+  if constexpr (ST == f.n) {
+    return a;
+  } else {
+    constexpr int R = f.r[ST];
+    constexpr int P = [] {
+      int p = 1;
+      for (int i = 0; i < ST; ++i) p *= fixed_radices_ct(L).r[i];
+      return p;
+    }();
+    stockham_pass<R, INV>(a, b, L, P, ntr, tw, tid, nth);
+    __syncthreads();
+    return fft_fixed_ct<L, ST + 1, INV>(b, a, ntr, tw, tid, nth);
+  }
+}
+
 }  // namespace cvn
