@@ -666,7 +666,55 @@ __global__ void __launch_bounds__(256) k_rows_fwd(RowFwdArgs a) {
   }
   const float* xp = a.x + plane * (int64_t)a.Hin * a.Win;
   const FastDiv fL = fast_div(L), frpb = fast_div(a.rpb);
-  for (int i0 = tid; i0 < ntr * L; i0 += kBatch * nth) {
+  // Compile-time length with 16-byte aligned rows of a multiple of 4 samples: the interior of each
+  // row as float4 loads (one row index map per item instead of three per sample), then the 2 pad
+  // border columns per row from their padding sources
+  const bool vec4 = LC > 0 && a.Win % 4 == 0 && ((uintptr_t)a.x & 15) == 0 && a.Win + 2 * a.pad == L;
+  if (vec4) {
+    const int W4 = a.Win >> 2, nI = ntr * W4, nb = 2 * a.pad;
+    const FastDiv fW4 = fast_div(W4);
+    for (int i0 = tid; i0 < nI; i0 += kBatch * nth) {
+      float4 va[kBatch], vb[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const int idx = i0 + k * nth;
+        va[k] = vb[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (idx < nI) {
+          const int t = idx / fW4, q = idx - t * W4;
+          const int ra = r0 + 2 * t, rb = ra + 1;
+          const int sa = ra < a.h ? pad_src(ra, a.Hin, a.pad, a.mode) : -1;
+          const int sb = rb < a.h ? pad_src(rb, a.Hin, a.pad, a.mode) : -1;
+          if (sa >= 0) va[k] = *(const float4*)(xp + (int64_t)sa * a.Win + 4 * q);
+          if (sb >= 0) vb[k] = *(const float4*)(xp + (int64_t)sb * a.Win + 4 * q);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const int idx = i0 + k * nth;
+        if (idx < nI) {
+          const int t = idx / fW4, q = idx - t * W4;
+          float2* d = A + t * L + a.pad + 4 * q;
+          d[0] = make_float2(va[k].x, vb[k].x);
+          d[1] = make_float2(va[k].y, vb[k].y);
+          d[2] = make_float2(va[k].z, vb[k].z);
+          d[3] = make_float2(va[k].w, vb[k].w);
+        }
+      }
+    }
+    for (int idx = tid; idx < ntr * nb; idx += nth) {
+      const int t = idx / nb, e = idx - t * nb;
+      const int c = e < a.pad ? e : a.Win + e;  // border column of the padded row
+      const int ra = r0 + 2 * t, rb = ra + 1;
+      const int sc = pad_src(c, a.Win, a.pad, a.mode);
+      const int sa = ra < a.h ? pad_src(ra, a.Hin, a.pad, a.mode) : -1;
+      const int sb = rb < a.h ? pad_src(rb, a.Hin, a.pad, a.mode) : -1;
+      float2 v = make_float2(0.f, 0.f);
+      if (sc >= 0 && sa >= 0) v.x = xp[(int64_t)sa * a.Win + sc];
+      if (sc >= 0 && sb >= 0) v.y = xp[(int64_t)sb * a.Win + sc];
+      A[t * L + c] = v;
+    }
+  }
+  for (int i0 = vec4 ? ntr * L : tid; i0 < ntr * L; i0 += kBatch * nth) {
     float2 v[kBatch];
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
@@ -978,12 +1026,42 @@ __global__ void __launch_bounds__(256) k_rows_inv(RowInvArgs a) {
         a.side[(plane * nb + (r < pad ? r : r - Hd)) * (int64_t)Wd + j] = v;
     };
     if (!all_edge) {
-      const FastDiv fW = fast_div(Wd);
-      for (int idx = tid; idx < a.rpb * Wd; idx += nth) {
-        const int rl = idx / fW, j = idx - rl * Wd;
-        if (r0 + rl >= a.nrows || (nb > 0 && (j <= pad || j >= Wd - 1 - pad))) continue;
-        const float2 z = Z[(rl >> 1) * L + j + pad];
-        put(rl, j, (rl & 1) ? z.y : z.x);
+      // non-edge columns [j0, j1): with a compile-time length and 16-byte aligned rows, the aligned
+      // middle [jb0, jb1) as float4 stores and the rest one sample at a time
+      const int j0 = nb > 0 ? pad + 1 : 0, j1 = nb > 0 ? Wd - 1 - pad : Wd;
+      int jb0 = j0, jb1 = j0;
+      if (LC > 0 && Wd % 4 == 0 && ((uintptr_t)a.out & 15) == 0 && ((uintptr_t)a.side & 15) == 0) {
+        jb0 = (j0 + 3) & ~3;
+        jb1 = j1 & ~3;
+        if (jb1 < jb0) jb1 = jb0;
+      }
+      const int nq = (jb1 - jb0) >> 2;
+      if (nq > 0) {
+        const FastDiv fq = fast_div(nq);
+        for (int idx = tid; idx < a.rpb * nq; idx += nth) {
+          const int rl = idx / fq, q = idx - rl * nq;
+          const int r = r0 + rl;
+          if (r >= a.nrows) continue;
+          const int j = jb0 + 4 * q;
+          const float2* zr = Z + (rl >> 1) * L + j + pad;
+          const float4 v = (rl & 1) ? make_float4(zr[0].y, zr[1].y, zr[2].y, zr[3].y)
+                                    : make_float4(zr[0].x, zr[1].x, zr[2].x, zr[3].x);
+          float* dst = (r >= pad && r < pad + Hd) ? a.out + (plane * Hd + (r - pad)) * (int64_t)Wd + j
+                       : (nb > 0 ? a.side + (plane * nb + (r < pad ? r : r - Hd)) * (int64_t)Wd + j : nullptr);
+          if (dst) *(float4*)dst = v;
+        }
+      }
+      const int nrest = (j1 - j0) - 4 * nq;  // columns [j0, jb0) and [jb1, j1)
+      if (nrest > 0) {
+        const FastDiv fr = fast_div(nrest);
+        const int nh = jb0 - j0;
+        for (int idx = tid; idx < a.rpb * nrest; idx += nth) {
+          const int rl = idx / fr, e = idx - rl * nrest;
+          if (r0 + rl >= a.nrows) continue;
+          const int j = e < nh ? j0 + e : jb1 + (e - nh);
+          const float2 z = Z[(rl >> 1) * L + j + pad];
+          put(rl, j, (rl & 1) ? z.y : z.x);
+        }
       }
     }
     for (int idx = tid; idx < a.rpb * ne; idx += nth) {
