@@ -1129,6 +1129,82 @@ constexpr int kColsBwdThreads = 512;  // 2 blocks of 8 waves per CU at the cfg3 
 constexpr int kColRegs = 4;           // per-thread register slots of the scale-1 path
 constexpr int kColLoad = 4;           // column elements per array loaded per thread and batch
 
+// Asynchronous copy of nbytes (a multiple of 16) from global src to LDS dst, both contiguous, with
+// global_load_lds_dwordx4: lane l of a wave's copy instruction writes its 16 bytes at dst + 16 l
+// (the LDS base is wave-uniform), so no register holds the data.  The caller waits with
+// s_waitcnt vmcnt(0) and a barrier before reading dst.
+__device__ __forceinline__ void lds_copy_async(const float2* src, float2* dst, int nbytes, int tid, int nth) {
+  const int lane = tid & 63, wave = tid >> 6, nwaves = nth >> 6;
+  for (int off = wave * 1024; off < nbytes; off += nwaves * 1024)
+    if (off + 16 * lane < nbytes)
+      __builtin_amdgcn_global_load_lds((const void*)((const char*)src + off + 16 * lane),
+                                       (__attribute__((address_space(3))) void*)((char*)dst + off), 16, 0, 0);
+}
+
+// The per-plane loop of k_cols_bwd at scale 1 on a compile-time column length, with conj(Phi') and
+// the dPhi sums in registers (fr, ar: element idx = cl h + u of thread tid, k-th slot).  The block's
+// columns of one plane are two contiguous runs (Sg and Sx columns vbase ..), copied into LDS by
+// lds_copy_async; the next plane's copy is issued right after this plane's product, into the X and Y
+// buffers that its forward transforms have freed, so its HBM round trip overlaps this plane's inverse
+// transform and store.  Buffer roles rotate: xin / yin receive the copies, xfree / ytmp are the
+// forward transforms' work buffers, yout the product, and the inverse transform works in yout and
+// the buffer that held Y.
+template <int HC>
+__device__ __forceinline__ void cols_bwd_ct_planes(const ColBwdArgs& a, float2* Xa, float2* Xb, float2* Ya, float2* Yb,
+                                                   float2* Yc, const float2* twh, const float2 (&fr)[kColRegs],
+                                                   float2 (&ar)[kColRegs], int ncol, int vbase, int64_t grp,
+                                                   int64_t nplanes, bool wg, float norm) {
+  const int tid = threadIdx.x, nth = blockDim.x, cpb = a.cpb;
+  // column slots past ncol are transformed but never stored: start them at zero
+  for (int i = tid; i < cpb * HC; i += nth) {
+    const float2 z = make_float2(0.f, 0.f);
+    Xa[i] = z; Xb[i] = z; Ya[i] = z; Yb[i] = z; Yc[i] = z;
+  }
+  __syncthreads();
+  const int nb = ncol * HC * (int)sizeof(float2);
+  auto issue = [&](int64_t ib, float2* xd, float2* yd) {
+    const int64_t plane = (a.psf_batch == 1) ? ib * a.C + grp : grp;
+    lds_copy_async(a.Sg + plane * (int64_t)a.NCs * HC + (int64_t)vbase * HC, xd, nb, tid, nth);
+    if (wg) lds_copy_async(a.Sx + plane * (int64_t)a.NC * HC + (int64_t)vbase * HC, yd, nb, tid, nth);
+  };
+  float2 *xin = Xa, *xfree = Xb, *yin = Ya, *ytmp = Yb, *yout = Yc;
+  issue(0, xin, yin);
+  for (int64_t ib = 0; ib < nplanes; ++ib) {
+    const int64_t plane = (a.psf_batch == 1) ? ib * a.C + grp : grp;
+    float2* Sxp = a.Sx + plane * (int64_t)a.NC * HC;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's copies (and earlier stores) done
+    __syncthreads();                                  // every wave's copies; the previous plane's reads
+    const float2* dZ = fft_fixed_ct<HC, 0, false>(xin, xfree, cpb, twh, tid, nth);
+    const float2* Y = wg ? fft_fixed_ct<HC, 0, false>(yin, ytmp, cpb, twh, tid, nth) : nullptr;
+#pragma unroll
+    for (int k = 0; k < kColRegs; ++k) {
+      const int idx = tid + k * nth;
+      if (idx < cpb * HC) {
+        const float2 z = dZ[idx];
+        if (wg) {
+          const float2 t = cmul(cconj(Y[idx]), z);
+          ar[k].x = fmaf(t.x, norm, ar[k].x);
+          ar[k].y = fmaf(t.y, norm, ar[k].y);
+        }
+        yout[idx] = cmul(fr[k], z);
+      }
+    }
+    __syncthreads();
+    // free now: the X buffer not holding dZ, the Y buffer not holding Y (both Y buffers without
+    // weight gradients), and the one holding Y (read by the product only)
+    float2* xnext = (dZ == xin) ? xfree : xin;
+    float2* ynext = (wg && Y == yin) ? ytmp : yin;
+    float2* yscr = (ynext == yin) ? ytmp : yin;
+    if (ib + 1 < nplanes) issue(ib + 1, xnext, ynext);
+    const float2* R = fft_fixed_ct<HC, 0, true>(yout, yscr, cpb, twh, tid, nth);
+    for (int idx = tid; idx < ncol * HC; idx += nth) Sxp[(int64_t)vbase * HC + idx] = R[idx];
+    xfree = (xnext == xin) ? xfree : xin;
+    xin = xnext;
+    ytmp = yscr;
+    yin = ynext;
+  }
+}
+
 // HC > 0: scale 1 with the column length h = Hs fixed at compile time (fft_fixed_ct).
 // Four waves per SIMD (at most 128 VGPRs): two blocks per CU, which the LDS size allows at cfg3.
 template <int HC>
@@ -1173,6 +1249,7 @@ __global__ void __launch_bounds__(kColsBwdThreads, 4) k_cols_bwd(ColBwdArgs a) {
   // vbase + cl <= Ws / 2) and one row per bin, so element idx = cl h + u of this thread is the same
   // in every plane; its conj(Phi') is read from HBM once and the dPhi sum stays in registers.
   const bool regs = as == 1 && cpb * ah <= kColRegs * nth;
+  bool nplanes_done = false;
   float2 fr[kColRegs], ar[kColRegs];
   if (regs) {
 #pragma unroll
@@ -1184,7 +1261,13 @@ __global__ void __launch_bounds__(kColsBwdThreads, 4) k_cols_bwd(ColBwdArgs a) {
     }
   }
   const int64_t nplanes = (a.psf_batch == 1) ? a.B : 1;
-  for (int64_t ib = 0; ib < nplanes; ++ib) {
+  if constexpr (HC > 0) {
+    if (regs) {
+      cols_bwd_ct_planes<HC>(a, Xa, Xb, Ya, Yb, Yc, twh, fr, ar, ncol, vbase, grp, nplanes, wg, norm);
+      nplanes_done = true;
+    }
+  }
+  for (int64_t ib = 0; ib < (nplanes_done ? 0 : nplanes); ++ib) {
     const int64_t plane = (a.psf_batch == 1) ? ib * a.C + grp : grp;
     const float2* Sgp = a.Sg + plane * (int64_t)a.NCs * aHs;
     float2* Sxp = a.Sx + plane * (int64_t)a.NC * ah;

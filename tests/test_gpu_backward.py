@@ -92,6 +92,33 @@ def test_backward_partial_scale1(need):
         _close(gb.cpu().numpy(), rb, 2e-4, "grad_bias only")
 
 
+CT_CASES = [
+    # (B, C, H, W, k, p, mode, psf_batch, need): scale 1 on the column lengths with a compile-time plan
+    (3, 2, 128, 128, 5, 2, "circular", 1, (True, True, True)),    # 132: three planes per column block
+    (4, 1, 252, 252, 5, 2, "reflect", 1, (True, False, False)),   # 256, grad_x only (no input columns)
+    (3, 2, 256, 256, 3, 2, "circular", 1, (False, True, True)),   # 260, weight gradients only
+    (2, 2, 256, 256, 5, 0, "circular", 2, (True, True, True)),    # 256, one plane per block (per-sample psf)
+]
+
+
+@pytest.mark.parametrize("B,C,H,W,k,p,mode,pb,need", CT_CASES)
+def test_backward_compile_time_columns(B, C, H, W, k, p, mode, pb, need):
+    """The column pass at 132, 256 and 260 points, whose blocks copy each plane's columns into LDS
+    asynchronously while the previous plane is transformed: several planes per block, with and
+    without the input columns of the weight gradients, and one plane per block."""
+    from conversenet_amd import functional as Fh
+    x, w, b, g = _inputs(B, C, H, W, k, 1, pb, 29 + H + k)
+    eps = 1e-3 if pb > 1 else 1e-5
+    rx, rw, rb = O.converse2d_module_backward(x, w, b, g, 1, p, mode, eps)
+    gx, gw, gb = Fh.converse2d_backward(_t(g), _t(x), _t(w), _t(b), 1, p, mode, eps, *need)
+    torch.cuda.synchronize()
+    if need[0]:
+        _close(gx.cpu().numpy(), rx, 1e-4, "grad_x")
+    if need[1]:
+        _close(gw.cpu().numpy(), rw, 2e-4, "grad_weight")
+        _close(gb.cpu().numpy(), rb, 2e-4, "grad_bias")
+
+
 def test_backward_scale1_plane_past_register_path():
     """A 2100-sample padded side at scale 1: one column class per block holds 2100 elements, more than
     the 4 x 512 register slots, so the column pass reads conj(Phi') per element instead.  grad_x only:
