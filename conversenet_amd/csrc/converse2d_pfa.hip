@@ -493,12 +493,12 @@ __device__ __forceinline__ float2 quad_bfly(float2 v, float sg) {
 // frequency, natural lane order in, bit-reversed out): a = x[s ^ 2] + (+-1) x[s] (minus in lanes 2,
 // 3), lane 3 times -i, then y = a[s ^ 1] + (+-1) a[s] (minus in lanes 1, 3).  Inverse (decimation in
 // time, bit-reversed in, natural out): the same steps in reverse order with +i.
-template <bool INV>
+template <bool INV, int J0 = 0, int J1 = P>
 __device__ __forceinline__ void quad_dft4(float2 (&x)[P], int k) {
   const float s2 = (k & 2) ? -1.f : 1.f, s1 = (k & 1) ? -1.f : 1.f;
   const bool l3 = k == 3;
 #pragma unroll
-  for (int j = 0; j < P; ++j) {
+  for (int j = J0; j < J1; ++j) {
     if (!INV) {
       const float2 a = quad_bfly<kX2>(x[j], s2);
       const float2 b = make_float2(l3 ? a.y : a.x, l3 ? -a.x : a.y);  // lane 3: -i a
@@ -511,12 +511,12 @@ __device__ __forceinline__ void quad_dft4(float2 (&x)[P], int k) {
   }
 }
 
-// x[j] *= W67^(+-dl j) (W67 = exp(-2 pi i / 67); tw holds W67^m)
-template <bool CONJ>
+// x[j] *= W67^(+-dl j) for J0 <= j < J1 (W67 = exp(-2 pi i / 67); tw holds W67^m)
+template <bool CONJ, int J0 = 0, int J1 = P>
 __device__ __forceinline__ void quad_rotate(float2 (&x)[P], const float2* tw, int dl) {
-  int m = 0;
+  int m = (dl * J0) % P;
 #pragma unroll
-  for (int j = 0; j < P; ++j) {
+  for (int j = J0; j < J1; ++j) {
     const float2 t = tw[m];
     x[j] = cmul(x[j], CONJ ? cconj(t) : t);
     m += dl;
@@ -570,15 +570,48 @@ __device__ __forceinline__ int64_t cols_quad(const ColsArgs& a) {
   return ((pl % a.B) * a.C + pl / a.B) * NC + (g - pl * NC);
 }
 
+// Transfer-table entries through LDS: the quad's four entries of register j (32 contiguous bytes of
+// the quad layout) are copied with global_load_lds_dwordx4 into the wave's LDS region, lane k of the
+// quad copying the 16 bytes of register J0 + 2 i + (k >> 1) in instruction i, so that quad q's entry
+// for register j lands at region[(j - J0) / 2 * 128 + 8 q + 4 ((j - J0) & 1) + lane]; no register holds
+// it in flight (a register prefetch does not fit beside the 67 column values).  The first copy
+// (registers 0 .. 33) is requested before the column loads and arrives during the forward
+// transform; the second (registers 33 .. 66, overlapping the first by one so that every lane of
+// every copy instruction is active: a partly masked copy made the compiler spill 105 VGPRs) after
+// the first half's products, and arrives during that half's inverse 4-point DFT and rotation.  A
+// wave's region is 17 KB, so two blocks of four waves fit in LDS.
+constexpr int kPhiHalf = 34;  // registers per copy (even)
+template <int J0, int J1>
+__device__ __forceinline__ void phi_copy(const float2* ph, float2* region, int k) {
+  static_assert((J1 - J0) % 2 == 0, "whole instructions: every lane copies");
+#pragma unroll
+  for (int i = 0; i < (J1 - J0) / 2; ++i) {
+    const int j = J0 + 2 * i + (k >> 1);
+    __builtin_amdgcn_global_load_lds((const void*)(ph + (int64_t)j * NC * 4 + 2 * (k & 1)),
+                                     (__attribute__((address_space(3))) void*)(region + i * 128), 16, 0, 0);
+  }
+}
+// x[j] *= Phi[j] for J0 <= j < J1, from a region filled by phi_copy<B, ...>
+template <int B, int J0, int J1>
+__device__ __forceinline__ void phi_product(float2 (&x)[P], const float2* region, int q, int k) {
+#pragma unroll
+  for (int j = J0; j < J1; ++j) x[j] = cmul(x[j], region[(j - B) / 2 * 128 + 8 * q + 4 * ((j - B) & 1) + k]);
+}
+
 __global__ void __launch_bounds__(256) k_pfa_cols(ColsArgs a) {
   __shared__ QuadTabs T;
+  __shared__ __align__(16) float2 phs[kWaves][kPhiHalf / 2 * 128];  // per wave: 17 KB
   load_quad_tabs(T, 0, 0, 0);
-  const int k = threadIdx.x & 3;
+  const int k = threadIdx.x & 3, q = (threadIdx.x & 63) >> 2;
   const int64_t gq = cols_quad(a);
-  if (gq >= a.nquad) return;
+  if (gq >= a.nquad) return;  // whole quads leave together; each lane copies only its own quad's entries
   const int64_t plane = gq / NC;
   const int c = (int)(gq - plane * NC);
   const int64_t cp = a.psf_batch == 1 ? plane % a.C : plane;
+  // register j of lane k multiplies by Phi at u = 201 br(k) + 68 j, stored at [cp][j][c][k]
+  const float2* ph = a.phi + (cp * P * NC + c) * 4;
+  float2* region = phs[threadIdx.x >> 6];
+  phi_copy<0, kPhiHalf>(ph, region, k);
   float2* col = a.S + gq * (int64_t)LP + quad_sig(k);
   float2 x[P];
 #pragma unroll
@@ -593,24 +626,20 @@ __global__ void __launch_bounds__(256) k_pfa_cols(ColsArgs a) {
   quad_rotate<false>(x, T.tw, dl);
   sched_fence();
   quad_dft4<false>(x, k);
-  // register j of lane k multiplies by Phi at u = 201 br(k) + 68 j, stored at [cp][j][c][k]
-  const float2* ph = a.phi + (cp * P * NC + c) * 4 + k;
-  sched_fence();
-#pragma unroll
-  for (int j0 = 0; j0 < P; j0 += kLoadChunk) {
-    float2 f[kLoadChunk];
-#pragma unroll
-    for (int jj = 0; jj < kLoadChunk && j0 + jj < P; ++jj) f[jj] = ph[(j0 + jj) * NC * 4];
-    sched_fence();
-#pragma unroll
-    for (int jj = 0; jj < kLoadChunk && j0 + jj < P; ++jj) x[j0 + jj] = cmul(x[j0 + jj], f[jj]);
-  }
-  sched_fence();
-  quad_dft4<true>(x, k);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's first table half is in LDS
+  phi_product<0, 0, kPhiHalf>(x, region, q, k);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // its reads are done before the region is reused
+  phi_copy<P - kPhiHalf, P>(ph, region, k);
   sched_fence();
   int dl2 = dl;
   asm volatile("" : "+v"(dl2));  // recompute the twiddle addresses instead of keeping the first pass's live
-  quad_rotate<true>(x, T.tw, dl2);
+  quad_dft4<true, 0, kPhiHalf>(x, k);
+  quad_rotate<true, 0, kPhiHalf>(x, T.tw, dl2);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the second half
+  phi_product<P - kPhiHalf, kPhiHalf, P>(x, region, q, k);
+  sched_fence();
+  quad_dft4<true, kPhiHalf, P>(x, k);
+  quad_rotate<true, kPhiHalf, P>(x, T.tw, dl2);
   sched_fence();
   dft67_reg<true>(x);
   sched_fence();
