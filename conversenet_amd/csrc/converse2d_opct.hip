@@ -475,10 +475,13 @@ __global__ void __launch_bounds__(kOpT) k_modcols(ModColCtArgs a) {
   }
 }
 
-// Rows per block of the row passes, by length (LDS: about L + RPB L complex values, at most ~72 KB).
+// Rows per block of the row passes, by length (LDS: about L + RPB L complex values, and the inverse
+// pass's staging of RPB (L / 2 + 1) more; at most ~108 KB).  8 rows at 768 and 1024 points rather
+// than 4: the stores of a column run then cover 64 bytes instead of 32 (reference grid at s = 3:
+// 0.3215 -> 0.3145 ms; 16 rows measured 0.384 ms, the inverse pass's LDS then allowing one block per CU).
 template <int L>
 constexpr int op_rpb() {
-  return L <= 128 ? 32 : (L <= 256 ? 16 : (L <= 512 ? 8 : 4));
+  return L <= 128 ? 32 : (L <= 256 ? 16 : 8);
 }
 // Staging buffer of the inverse row pass: RPB rows of L / 2 + 1 bins.
 template <int L>
