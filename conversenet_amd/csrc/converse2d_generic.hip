@@ -1262,7 +1262,10 @@ __global__ void __launch_bounds__(kColsBwdThreads, 4) k_cols_bwd(ColBwdArgs a) {
   }
   const int64_t nplanes = (a.psf_batch == 1) ? a.B : 1;
   if constexpr (HC > 0) {
-    if (regs) {
+    // (its 16-byte direct-to-LDS copies need 16-byte aligned spectra: every column offset is a
+    // multiple of 16 bytes, so the bases decide; cvn_converse2d_bwd_f32 aligns them, and other bases
+    // would take the loop below)
+    if (regs && (((uintptr_t)a.Sg | (uintptr_t)a.Sx) & 15) == 0) {
       cols_bwd_ct_planes<HC>(a, Xa, Xb, Ya, Yb, Yc, twh, fr, ar, ncol, vbase, grp, nplanes, wg, norm);
       nplanes_done = true;
     }
@@ -1909,6 +1912,7 @@ int check_mode_act(int64_t H, int64_t W, int pad, int pad_mode, int act) {
 
 // ---- backward workspace: plan tables, module table, HR grad spectra (later dy), LR spectra / dS,
 // and for weight gradients dPhi, dK, the column-transposed DFT T and the per-block lambda sums.
+constexpr size_t kBwdWsAlign = 256;  // alignment of the backward's workspace regions
 struct BwdWs {
   size_t tabs, phi, Sg, Sx, dphi, dK, T, part, total;
   int vc, nchunk, lds;
@@ -2252,7 +2256,7 @@ extern "C" size_t cvn_converse2d_bwd_workspace(int64_t B, int64_t C, int64_t H, 
   if (!plan_tabs(g, &t)) return 0;
   BwdWs w;
   bwd_layout(g, t, &w);
-  return w.total;
+  return w.total + kBwdWsAlign;  // slack to align the caller's pointer (cvn_converse2d_bwd_f32)
 }
 
 extern "C" int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int64_t B, int64_t C, int64_t H,
@@ -2273,11 +2277,14 @@ extern "C" int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int
   int cpb;
   size_t col_lds;
   if ((rc = bwd_check(g, wg, &t, &ws, &cpb, &col_lds)) != CVN_OK) return rc;
-  if (!workspace || workspace_bytes < ws.total)
-    return fail(CVN_ERR_WORKSPACE, "workspace too small: need %zu bytes", ws.total);
+  // the regions are laid out from a 256-byte aligned base inside the caller's workspace, whatever the
+  // pointer's alignment (the kernels read them with 16-byte loads and direct-to-LDS copies)
+  const size_t skew = workspace ? (kBwdWsAlign - (uintptr_t)workspace % kBwdWsAlign) % kBwdWsAlign : 0;
+  if (!workspace || workspace_bytes < ws.total + skew)
+    return fail(CVN_ERR_WORKSPACE, "workspace too small: need %zu bytes", ws.total + kBwdWsAlign);
   hipStream_t st = (hipStream_t)stream;
   set_lds_attrs();
-  char* base = (char*)workspace;
+  char* base = (char*)workspace + skew;
   const char* tabs = base + ws.tabs;
   float2* phi = (float2*)(base + ws.phi);
   float2* Sg = (float2*)(base + ws.Sg);

@@ -742,6 +742,8 @@ size_t pfa268_scratch_bytes(int64_t P) { return align_up((size_t)P * pfa268::NC 
 int pfa268_forward(const float* x, int64_t P, int64_t C, int64_t psf_batch, int H, int W, int pad, int mode, int act,
                    const float2* phi, float2* S, float* out, hipStream_t st) {
   using namespace pfa268;
+  // the column pass copies table entries with 16-byte direct-to-LDS loads
+  if ((uintptr_t)phi & 15) return fail(CVN_ERR_ARG, "the 268 path needs a 16-byte aligned transfer table");
   const int64_t nft = P * LQ, nct = P * NC;
   const int64_t nfb = (nft + kTrPerBlock - 1) / kTrPerBlock;
   if (nfb > 0x7fffffff) return fail(CVN_ERR_UNSUPPORTED, "too many planes for the 268 path");

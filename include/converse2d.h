@@ -111,7 +111,8 @@ int cvn_converse2d_supported(int64_t B, int64_t C, int64_t H, int64_t W, int64_t
  * cvn_converse2d_fwd_f32 == table into workspace[0, align256(table_bytes)) + apply with the rest, on
  * the route cvn_converse2d_route() picks.  On CVN_ROUTE_FUSED the scratch may be null: with at most
  * 128 planes (B C) the route asks for scratch_bytes > 0 so that each plane's two row groups can run in
- * workgroups of their own (twice the CUs busy); given null, the apply runs one workgroup per plane. */
+ * workgroups of their own (twice the CUs busy); given null, the apply runs one workgroup per plane.
+ * On CVN_ROUTE_PFA268 the table must be 16-byte aligned (CVN_ERR_ARG otherwise). */
 size_t cvn_converse2d_table_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch,
                                   int kh, int kw, int scale, int pad, int route);
 size_t cvn_converse2d_scratch_bytes(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch,
@@ -129,7 +130,8 @@ int cvn_converse2d_apply_f32(const float* x, int64_t B, int64_t C, int64_t H, in
  * CompositeImplicitAutograd, converse2d.cpp:223-227; gradient checks in test/test_error.py:51-54).
  * grad_out: (B,C,H*scale,W*scale).  Outputs (each may be null when not wanted): grad_x (B,C,H,W),
  * grad_psf (psf_batch,C,kh,kw), grad_bias (C).  x is read only for grad_psf / grad_bias.  Weight
- * gradients support scale <= 4. */
+ * gradients support scale <= 4.  The workspace may have any alignment: the query includes 256 bytes
+ * of slack, and the regions are laid out from the first 256-byte boundary inside it. */
 size_t cvn_converse2d_bwd_workspace(int64_t B, int64_t C, int64_t H, int64_t W, int64_t psf_batch,
                                     int kh, int kw, int scale, int pad);
 int cvn_converse2d_bwd_f32(const float* grad_out, const float* x, int64_t B, int64_t C, int64_t H,

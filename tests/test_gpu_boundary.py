@@ -208,3 +208,64 @@ def test_registered_ops_outside_library_limits_run_the_composition():
     print(f"op 4100x6 on the composition: max-abs {err:.3e}; forward_fused {err_f:.3e}")
     assert got.shape == (1, 1, 4100, 6) and fused.shape == (1, 1, 4098, 4)
     assert err <= 1e-2 and err_f <= 1e-2  # the reference's fp32 op order (see above)
+
+
+def test_pfa268_route_rejects_misaligned_table():
+    """The 268 path copies table entries with 16-byte direct-to-LDS loads: an apply on
+    CVN_ROUTE_PFA268 with a table that is not 16-byte aligned returns CVN_ERR_ARG before any launch,
+    and the same table aligned runs and matches the oracle."""
+    from conversenet_amd import _lib
+    lib = _lib.load()
+    rng = seeded("pfa268-align")
+    B, C, H, k, p = 1, 2, 256, 7, 6
+    x = _t(rng.standard_normal((B, C, H, H)).astype(np.float32))
+    wt = softmax_psf(rng, C, k)
+    b = np.zeros((1, C, 1, 1), np.float32)
+    wtt, bt = _t(wt), _t(b.reshape(-1))
+    assert lib.cvn_converse2d_route(B, C, H, H, 1, k, k, 1, p) == _lib.ROUTE_PFA268
+    tb = lib.cvn_converse2d_table_bytes(B, C, H, H, 1, k, k, 1, p, _lib.ROUTE_PFA268)
+    sb = lib.cvn_converse2d_scratch_bytes(B, C, H, H, 1, k, k, 1, p, _lib.ROUTE_PFA268)
+    table = torch.empty(tb + 16, dtype=torch.uint8, device=DEV)
+    scratch = torch.empty(sb, dtype=torch.uint8, device=DEV)
+    out = torch.empty((B, C, H, H), dtype=torch.float32, device=DEV)
+    st = torch.cuda.current_stream().cuda_stream
+    assert lib.cvn_converse2d_table_f32(wtt.data_ptr(), 1, k, k, bt.data_ptr(), 1e-5, B, C, H, H, 1, p,
+                                        _lib.ROUTE_PFA268, table.data_ptr(), tb, st) == _lib.CVN_OK
+    args = (x.data_ptr(), B, C, H, H, 1, k, k, 1, p, _lib.PAD_MODES["circular"], 0, _lib.ROUTE_PFA268)
+    rc = lib.cvn_converse2d_apply_f32(*args, table.data_ptr() + 8, tb, scratch.data_ptr(), sb, out.data_ptr(), st)
+    assert rc == _lib.CVN_ERR_ARG
+    rc = lib.cvn_converse2d_apply_f32(*args, table.data_ptr(), tb, scratch.data_ptr(), sb, out.data_ptr(), st)
+    assert rc == _lib.CVN_OK
+    torch.cuda.synchronize()
+    ref = O.converse2d_module(x.cpu().numpy(), wt, b, 1, p, "circular", 1e-5)
+    assert np.abs(out.cpu().numpy() - ref).max() <= TOL
+
+
+def test_backward_with_misaligned_workspace():
+    """The backward lays its workspace regions out from a 256-byte boundary inside the caller's buffer
+    (its kernels use 16-byte loads and direct-to-LDS copies): a workspace pointer 8 bytes past an
+    aligned one, with the queried size, gives the aligned call's gradients."""
+    from conversenet_amd import _lib
+    lib = _lib.load()
+    rng = seeded("bwd-align")
+    B, C, H, k, p = 2, 2, 256, 5, 2
+    x = _t(rng.standard_normal((B, C, H, H)).astype(np.float32))
+    g = _t(rng.standard_normal((B, C, H, H)).astype(np.float32))
+    wt = _t(softmax_psf(rng, C, k))
+    b = _t((0.3 * rng.standard_normal(C)).astype(np.float32))
+    nb = lib.cvn_converse2d_bwd_workspace(B, C, H, H, 1, k, k, 1, p)
+    ws = torch.empty(nb + 64, dtype=torch.uint8, device=DEV)
+    st = torch.cuda.current_stream().cuda_stream
+    res = []
+    for off in (0, 8):
+        gx = torch.empty_like(x)
+        gw = torch.empty((1, C, k, k), dtype=torch.float32, device=DEV)
+        gb = torch.empty(C, dtype=torch.float32, device=DEV)
+        rc = lib.cvn_converse2d_bwd_f32(g.data_ptr(), x.data_ptr(), B, C, H, H, wt.data_ptr(), 1, k, k,
+                                        b.data_ptr(), 1e-5, 1, p, _lib.PAD_MODES["circular"], gx.data_ptr(),
+                                        gw.data_ptr(), gb.data_ptr(), ws.data_ptr() + off, nb, st)
+        assert rc == _lib.CVN_OK
+        torch.cuda.synchronize()
+        res.append((gx.cpu().numpy(), gw.cpu().numpy(), gb.cpu().numpy()))
+    for a0, a1 in zip(*res):
+        assert np.abs(a0 - a1).max() <= 1e-5 * max(1.0, np.abs(a0).max())
