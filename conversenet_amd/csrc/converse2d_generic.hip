@@ -224,6 +224,9 @@ __global__ void k_phi_op(PhiArgs a) {
 // ------------------------------------------------------------------------------------------------
 struct PhiTileLds {
   int zH, phH, hH, zW, phW, hW, P, psf, part, total;  // byte offsets
+  // split-DFT form: column twiddles, fp64 psf, row twiddles per row residue, shifted psf-row sums
+  int tw, psd, tr, Pt;
+  int PS, NTh, Ch;  // row stride (entries) of tr and Pt, 16-row tap groups, row shift 16 Ch - kh / 2
 };
 __host__ __device__ inline int round4(int n) { return (n + 3) & ~3; }
 // The split-DFT evaluation of the tables (phi_tile_rows16) applies: scale 1, 2 or 4, HR height a
@@ -233,8 +236,30 @@ __host__ __device__ inline bool phi_rows16(int s, int Hs, bool q268) {
   return !q268 && (s == 1 || s == 2 || s == 4) && Hs % 16 == 0 && s * (Hs / 16) <= 256;
 }
 __host__ __device__ inline PhiTileLds phi_tile_lds(int s, int Hs, int kh, int kw, int vc, bool fast = false) {
-  PhiTileLds L;
+  PhiTileLds L = {};
   int o = 0;
+  if (fast) {
+    // split-DFT form.  psf row i sits at shifted row index i' = i - kh / 2 + 16 Ch in [0, 16 NTh), so
+    // that i' mod 16 is the residue of the centred row offset.  The first three regions are dead once
+    // the psf-row sums are formed, and the class partial sums (s > 1) reuse them.
+    const int ne = vc * s, ch = kh / 2;
+    L.Ch = (ch + 15) / 16;
+    L.NTh = (16 * L.Ch - ch + kh + 15) / 16;
+    L.PS = 16 * L.NTh + 1;  // odd stride: the 16 row residues' and 4 members' reads spread over the banks
+    L.zH = o; o += Hs * 16;
+    L.tw = o; o += ne * kw * 16;
+    L.psd = o; o += kw * ((kh + 1) & ~1) * 8;
+    o = (o + 15) & ~15;
+    L.part = 0;
+    o = (s > 1 && vc * Hs * 24 > o) ? vc * Hs * 24 : o;
+    o = (o + 15) & ~15;
+    L.hH = o; o += (s > 1 ? Hs : 0) * 16;
+    L.hW = o; o += ne * 16;
+    L.tr = o; o += (Hs / 16) * L.PS * 16;
+    L.Pt = o; o += ne * L.PS * 16;
+    L.total = (o + 15) & ~15;
+    return L;
+  }
   L.zH = o; o += Hs * 16;
   L.phH = o; o += Hs * 16;
   L.hH = o; o += (s > 1 ? Hs : 0) * 16;
@@ -243,8 +268,6 @@ __host__ __device__ inline PhiTileLds phi_tile_lds(int s, int Hs, int kh, int kw
   L.hW = o; o += vc * s * 16;
   L.P = o; o += vc * s * round4(kh) * 16;
   L.psf = o; o += kh * round4(kw) * 4;
-  o = (o + 15) & ~15;
-  L.part = o; o += (fast && s > 1 ? vc * Hs * 24 : 0);  // class partial sums (|K|^2, K h) per column member
   L.total = (o + 15) & ~15;
   return L;
 }
@@ -269,18 +292,20 @@ __device__ __forceinline__ double2 horner4(const double2* P, int n4, double2 z) 
 
 // Per-block LDS tables of the tiled transfer-table kernels (k_phi_tile, k_phi_grad): row tables for
 // every HR row, column tables for the chunk's HR columns vbeg + v + b w (v < nv, b < S), and the psf
-// row sums P[(v S + b) kh4 + i] (rows zero-padded to kh4).
+// row sums P[(v S + b) kh4 + i] (rows zero-padded to kh4).  The split-DFT form (phi_split_prep) fills
+// hH, hW, tr and Pt instead.
 struct PhiTileView {
   double2 *zH, *phH, *hH, *zW, *phW, *hW, *P;
+  double2 *tr, *Pt;
+  int PS, NTh;
 };
 template <int S>
-__device__ PhiTileView phi_tile_prep(const PhiArgs& a, unsigned char* phl, int64_t cp, int vbeg, int nv, int vc,
-                                     bool fast = false) {
+__device__ PhiTileView phi_tile_prep(const PhiArgs& a, unsigned char* phl, int64_t cp, int vbeg, int nv, int vc) {
   const int tid = threadIdx.x, nth = blockDim.x;
   const int Hs = a.Hs, Ws = a.Ws, kh = a.kh, kw = a.kw;
   const int kh4 = round4(kh), kw4 = round4(kw);
-  const PhiTileLds L = phi_tile_lds(S, Hs, kh, kw, vc, fast);
-  PhiTileView t;
+  const PhiTileLds L = phi_tile_lds(S, Hs, kh, kw, vc);
+  PhiTileView t = {};
   t.zH = (double2*)(phl + L.zH);
   t.phH = (double2*)(phl + L.phH);
   t.hH = (double2*)(phl + L.hH);
@@ -300,23 +325,10 @@ __device__ PhiTileView phi_tile_prep(const PhiArgs& a, unsigned char* phl, int64
     const int e = tid + r * nth, i = e / kw4, j = e - i * kw4;
     pv[r] = (e < kh * kw4 && j < kw) ? psf[i * kw + j] : 0.f;
   }
-  if (fast) {
-    // split-DFT form: z^u only (Hs a multiple of 4: a quarter by sincospi, the rest by the exact
-    // rotations z^(Q) = -i, z^(2Q) = -1, z^(3Q) = i); the hold sums follow from it below
-    const int Q = Hs >> 2;
-    for (int u = tid; u < Q; u += nth) {
-      const double2 z = dexpi((double)u, (double)Hs);
-      t.zH[u] = z;
-      t.zH[u + Q] = make_double2(z.y, -z.x);
-      t.zH[u + 2 * Q] = make_double2(-z.x, -z.y);
-      t.zH[u + 3 * Q] = make_double2(-z.y, z.x);
-    }
-  } else {
-    for (int u = tid; u < Hs; u += nth) {
-      t.zH[u] = dexpi((double)u, (double)Hs);
-      t.phH[u] = dexpi(-(double)(((int64_t)u * (kh / 2)) % Hs), (double)Hs);
-      if (S > 1) t.hH[u] = hold(S, u, Hs);
-    }
+  for (int u = tid; u < Hs; u += nth) {
+    t.zH[u] = dexpi((double)u, (double)Hs);
+    t.phH[u] = dexpi(-(double)(((int64_t)u * (kh / 2)) % Hs), (double)Hs);
+    if (S > 1) t.hH[u] = hold(S, u, Hs);
   }
   for (int e = tid; e < nv * S; e += nth) {
     const int v = e / S, b = e - v * S;
@@ -333,18 +345,6 @@ __device__ PhiTileView phi_tile_prep(const PhiArgs& a, unsigned char* phl, int64
     ps[e] = j < kw ? psf[i * kw + j] : 0.f;
   }
   __syncthreads();
-  if (S > 1 && fast)
-    for (int u = tid; u < Hs; u += nth) {  // hold sum sum_{t<S} z^(u t)
-      double2 acc = make_double2(1.0, 0.0);
-      int m = 0;
-      for (int q = 1; q < S; ++q) {
-        m += u;
-        m -= m >= Hs ? Hs : 0;
-        acc.x += t.zH[m].x;
-        acc.y += t.zH[m].y;
-      }
-      t.hH[u] = acc;
-    }
   // row sums (real coefficients, same four-chain Horner); rows zero-padded to kh4
   for (int e = tid; e < nv * S * kh4; e += nth) {
     const int vbq = e / kh4, i = e - vbq * kh4;
@@ -366,6 +366,128 @@ __device__ PhiTileView phi_tile_prep(const PhiArgs& a, unsigned char* phl, int64
   return t;
 }
 
+// exp(-2 pi i k / N) table index of k mod N (k may be negative); N a power of two needs no division
+__device__ __forceinline__ int mod_n(int k, int N, bool pow2) {
+  if (pow2) return k & (N - 1);
+  k %= N;
+  return k < 0 ? k + N : k;
+}
+
+// Tables of the split-DFT form, in three phases separated by barriers:
+//  1. the psf in fp64, transposed (row index fastest, rows padded to an even count), and z^u = exp(-2 pi
+//     i u / Hs) for every HR row (a quarter by sincospi, the rest by the exact rotations by -i, -1, i);
+//     hold sums of the chunk's columns (S > 1);
+//  2. column twiddles tw[m][j] = z_W^(vb (j - kw/2)) for the chunk's column members m = v S + b,
+//     row twiddles tr[u1][i'] = z^(u1 (i' - 16 Ch)) per row residue u1 < Hs / 16, hold sums of every
+//     HR row (S > 1), and zeroed psf-row sums;
+//  3. the psf-row sums Pt[m][i'] = sum_j psf[i][j] tw[m][j] at the shifted row index
+//     i' = i - kh/2 + 16 Ch (real times complex: two fp64 FMAs per tap; each task forms two rows).
+// The 2-D fills give each thread one column c = tid mod C and the rows tid / C + k (nth / C), so a
+// thread divides once per table rather than once per element (integer division is a ~30-instruction
+// sequence here); the host guarantees kw <= nth and 16 NTh <= nth.
+template <int S>
+__device__ PhiTileView phi_split_prep(const PhiArgs& a, unsigned char* phl, int64_t cp, int vbeg, int nv, int vc) {
+  const int tid = threadIdx.x, nth = blockDim.x;
+  const int Hs = a.Hs, Ws = a.Ws, kh = a.kh, kw = a.kw, H1 = Hs >> 4;
+  const int ch = kh / 2, cw = kw / 2, kh2 = (kh + 1) & ~1, nI = kh2 >> 1;
+  const bool h2 = (Hs & (Hs - 1)) == 0, w2 = (Ws & (Ws - 1)) == 0;
+  const PhiTileLds L = phi_tile_lds(S, Hs, kh, kw, vc, true);
+  const int PS = L.PS, Ch = L.Ch, NT16 = 16 * L.NTh, nm = nv * S;
+  PhiTileView t = {};
+  double2* zH = (double2*)(phl + L.zH);
+  double2* tw = (double2*)(phl + L.tw);
+  double* psd = (double*)(phl + L.psd);
+  t.hH = (double2*)(phl + L.hH);
+  t.hW = (double2*)(phl + L.hW);
+  t.tr = (double2*)(phl + L.tr);
+  t.Pt = (double2*)(phl + L.Pt);
+  t.PS = PS;
+  t.NTh = L.NTh;
+  // psf columns: thread column j = cj of rows rj, rj + sj, ... (threads past sj kw idle)
+  const int rj = tid / kw, cj = tid - rj * kw, sj = nth / kw;
+  const bool aj = rj < sj;
+
+  // the psf's first kPsfRegs rows per thread are requested before the sincos work of the row table,
+  // which does not depend on them, so the load latency overlaps it
+  constexpr int kPsfRegs = 4;
+  const float* psf = a.psf + cp * kh * kw;
+  float pv[kPsfRegs];
+#pragma unroll
+  for (int r = 0; r < kPsfRegs; ++r) {
+    const int i = rj + r * sj;
+    pv[r] = aj && i < kh ? psf[i * kw + cj] : 0.f;
+  }
+  const int Q = Hs >> 2;
+  for (int u = tid; u < Q; u += nth) {
+    const double2 z = dexpi((double)u, (double)Hs);
+    zH[u] = z;
+    zH[u + Q] = make_double2(z.y, -z.x);
+    zH[u + 2 * Q] = make_double2(-z.x, -z.y);
+    zH[u + 3 * Q] = make_double2(-z.y, z.x);
+  }
+  if (S > 1)
+    for (int m = tid; m < nm; m += nth) {
+      const int v = m / S, b = m - v * S;
+      t.hW[m] = hold(S, vbeg + v + (int64_t)b * a.w, Ws);
+    }
+  if (aj) {
+    double* col = psd + cj * kh2;
+#pragma unroll
+    for (int r = 0; r < kPsfRegs; ++r)
+      if (rj + r * sj < kh) col[rj + r * sj] = (double)pv[r];
+    for (int i = rj + kPsfRegs * sj; i < kh; i += sj) col[i] = (double)psf[i * kw + cj];
+    if (kh2 > kh && rj == 0) col[kh] = 0.0;
+  }
+  __syncthreads();
+
+  if (aj)
+    for (int m = rj; m < nm; m += sj) {
+      const int v = m / S, b = m - v * S;
+      const int k = mod_n((vbeg + v + b * a.w) * (cj - cw), Ws, w2);
+      tw[m * kw + cj] = Ws == Hs ? zH[k] : dexpi((double)k, (double)Ws);
+    }
+  {
+    const int ri = tid / NT16, ci = tid - ri * NT16, si = nth / NT16;
+    if (ri < si)
+      for (int u1 = ri; u1 < H1; u1 += si) t.tr[u1 * PS + ci] = zH[mod_n(u1 * (ci - 16 * Ch), Hs, h2)];
+  }
+  if (S > 1)
+    for (int u = tid; u < Hs; u += nth) {  // hold sum sum_{t<S} z^(u t)
+      double2 acc = make_double2(1.0, 0.0);
+      int m = 0;
+      for (int q = 1; q < S; ++q) {
+        m += u;
+        m -= m >= Hs ? Hs : 0;
+        acc.x += zH[m].x;
+        acc.y += zH[m].y;
+      }
+      t.hH[u] = acc;
+    }
+  for (int e = tid; e < nm * PS; e += nth) t.Pt[e] = make_double2(0.0, 0.0);
+  __syncthreads();
+
+  const double2* psd2 = (const double2*)psd;  // rows (2 r, 2 r + 1) of column j at psd2[j nI + r]
+  const int rm = tid / nI, r = tid - rm * nI, sm = nth / nI;
+  if (rm < sm)
+    for (int m = rm; m < nm; m += sm) {
+      const double2* twm = tw + m * kw;
+      double2 a0 = make_double2(0.0, 0.0), a1 = make_double2(0.0, 0.0);
+#pragma unroll 5
+      for (int j = 0; j < kw; ++j) {
+        const double2 p = psd2[j * nI + r], z = twm[j];
+        a0.x = fma(p.x, z.x, a0.x);
+        a0.y = fma(p.x, z.y, a0.y);
+        a1.x = fma(p.y, z.x, a1.x);
+        a1.y = fma(p.y, z.y, a1.y);
+      }
+      double2* Pm = t.Pt + m * PS + 2 * r - ch + 16 * Ch;
+      Pm[0] = a0;
+      if (2 * r + 1 < kh) Pm[1] = a1;
+    }
+  __syncthreads();
+  return t;
+}
+
 // 16-point DFT in place, X[k] = sum_i x[i] exp(-2 pi i i k / 16), fp64: radix 4 x 4 (decimation in
 // time: i = i0 + 4 i1, k = k0 + 4 k1; four 4-point DFTs over i1, twiddles w16^(i0 k0), four 4-point
 // DFTs over i0).  Twiddle constants cos / sin (2 pi m / 16), m = i0 k0 <= 9.
@@ -377,7 +499,9 @@ __device__ __forceinline__ void ddft4(double2& x0, double2& x1, double2& x2, dou
   x1 = make_double2(a1.x + b1.y, a1.y - b1.x);  // a1 - i b1
   x3 = make_double2(a1.x - b1.y, a1.y + b1.x);  // a1 + i b1
 }
-__device__ __forceinline__ void ddft16(double2 (&x)[16]) {
+// First half of the 16-point DFT: the four 4-point DFTs over i1 and the twiddles w16^(i0 k0); the
+// output X[k0 + 4 k1] is then ddft4 of x[4 k0 .. 4 k0 + 3], element k1.
+__device__ __forceinline__ void ddft16_first(double2 (&x)[16]) {
   constexpr double kC[10] = {1.0, 0.92387953251128674, 0.70710678118654752, 0.38268343236508977, 0.0,
                              -0.38268343236508977, -0.70710678118654752, -0.92387953251128674, -1.0,
                              -0.92387953251128674};
@@ -392,8 +516,12 @@ __device__ __forceinline__ void ddft16(double2 (&x)[16]) {
     for (int k0 = 1; k0 < 4; ++k0) {
       const int m = i0 * k0;
       const double2 v = x[i0 + 4 * k0];  // times exp(-2 pi i m / 16) = (cos, -sin)
-      x[i0 + 4 * k0] = make_double2(v.x * kC[m] + v.y * kS[m], v.y * kC[m] - v.x * kS[m]);
+      x[i0 + 4 * k0] = m == 4 ? make_double2(v.y, -v.x)
+                              : make_double2(v.x * kC[m] + v.y * kS[m], v.y * kC[m] - v.x * kS[m]);
     }
+}
+__device__ __forceinline__ void ddft16(double2 (&x)[16]) {
+  ddft16_first(x);
 #pragma unroll
   for (int k0 = 0; k0 < 4; ++k0) ddft4(x[4 * k0], x[4 * k0 + 1], x[4 * k0 + 2], x[4 * k0 + 3]);  // X[k0 + 4 k1] in x[4 k0 + k1]
   double2 t[16];
@@ -415,34 +543,28 @@ __device__ __forceinline__ double drcp(double d) {
 }
 
 // Split-DFT evaluation of the transfer function over rows (phi_rows16: Hs a multiple of 16).  One
-// thread per (HR column vb, row residue u1 < H1 = Hs / 16) evaluates K at the 16 rows u = u1 + H1 u2
-// by one split step of the DFT over rows instead of 16 Horner sums: with the centred psf rows
-// p_j = P[j + kh/2] (j in [-kh/2, kh - 1 - kh/2]), K(u) = sum_j p_j z^(u j), z = exp(-2 pi i / Hs), and
-// z^(H1 u2 j) depends on j mod 16 only, so K(u1 + H1 u2) = DFT16_u2( R[r] ), R[r] = sum_{j = r mod 16}
-// p_j z^(u1 j): about a fifth of the Horner form's fp64 operations per entry.
-__device__ __forceinline__ void phi_rows16_k(const PhiTileView& tv, int Hs, int kh, const double2* Pv, int u1,
-                                             double2 (&x)[16]) {
-  const int ch = kh / 2;
-  // R[r]: taps j = r - 16 q, r - 16 q + 16, ... from the lowest j >= -ch; z^(u1 j) as the table index
-  // m = u1 j mod Hs, stepped by A = 16 u1 < Hs (u1 r < Hs is already reduced)
-  const int A = 16 * u1;
+// thread per (HR column member m, row residue u1 < H1 = Hs / 16) evaluates K at the 16 rows
+// u = u1 + H1 u2 by one split step of the DFT over rows instead of 16 Horner sums: with the psf-row
+// sums P_i of the column and the centred row offset i - kh/2 = i' - 16 Ch (i' the shifted row index),
+// K(u) = sum_i P_i z^(u (i' - 16 Ch)), z = exp(-2 pi i / Hs), and z^(H1 u2 (i' - 16 Ch)) = w16^(u2 i')
+// depends on i' mod 16 only, so K(u1 + H1 u2) = DFT16_u2( R[r] ), R[r] = sum_{i' = r mod 16} Pt[m][i']
+// tr[u1][i'].  Every 16-row group of i' is summed whole (the rows past the psf are zero), so the loop
+// body has compile-time register indices and LDS offsets.
+__device__ __forceinline__ void phi_split_r(const PhiTileView& tv, int m, int u1, double2 (&x)[16]) {
+  const double2* P = tv.Pt + m * tv.PS;
+  const double2* T = tv.tr + u1 * tv.PS;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int q = (r + ch) >> 4;
-    int m = u1 * r;
-    for (int t = 0; t < q; ++t) {
-      m -= A;
-      m += m < 0 ? Hs : 0;
+  for (int r = 0; r < 16; ++r) x[r] = make_double2(0.0, 0.0);
+  for (int g = 0; g < tv.NTh; ++g, P += 16, T += 16) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      x[r] = cmadd(P[r], T[r], x[r]);
+      if (r % 8 == 7) __builtin_amdgcn_sched_barrier(0);  // at most 8 taps' operands in flight
     }
-    double2 acc = make_double2(0.0, 0.0);
-    for (int j = r - 16 * q; j < kh - ch; j += 16) {
-      const double2 p = Pv[j + ch], z = tv.zH[m];
-      acc = make_double2(fma(p.x, z.x, fma(-p.y, z.y, acc.x)), fma(p.x, z.y, fma(p.y, z.x, acc.y)));
-      m += A;
-      m -= m >= Hs ? Hs : 0;
-    }
-    x[r] = acc;
   }
+}
+__device__ __forceinline__ void phi_split_k(const PhiTileView& tv, int m, int u1, double2 (&x)[16]) {
+  phi_split_r(tv, m, u1, x);
   ddft16(x);
 }
 
@@ -457,29 +579,37 @@ __device__ __forceinline__ void phi_rows16_k(const PhiTileView& tv, int Hs, int 
 template <int S, int LAYOUT = -1>
 __device__ void phi_tile_rows16(const PhiArgs& a, int op, const PhiTileView& tv, double* part, int64_t cp, int vbeg,
                                 int nv, double lmb) {
-  const int Hs = LAYOUT == kPhiFused256 ? 256 : a.Hs, kh4 = round4(a.kh), H1 = Hs >> 4;
+  const int Hs = LAYOUT == kPhiFused256 ? 256 : a.Hs, H1 = Hs >> 4;
   const double norm = 1.0 / ((double)Hs * (double)a.Ws);
   if constexpr (S == 1) {
     for (int it = threadIdx.x; it < nv * H1; it += blockDim.x) {
       const int v = it / H1, u1 = it - v * H1;
       double2 x[16];
-      phi_rows16_k(tv, Hs, a.kh, tv.P + v * kh4, u1, x);
+      phi_split_r(tv, v, u1, x);
+      ddft16_first(x);
       const int64_t vb = vbeg + v;
+      // each group of four outputs is finished and stored before the next group's last DFT stage, so
+      // the entries' fp64 temporaries are live for four outputs at a time (128 VGPRs, no spills)
 #pragma unroll
-      for (int u2 = 0; u2 < 16; ++u2) {
-        const double2 k = x[u2];
-        const int u = u1 + H1 * u2;
-        const double rD = drcp(k.x * k.x + k.y * k.y + lmb);
-        if (op) {
-          const int64_t o = (cp * a.Ws + vb) * Hs + u;
-          a.kf[o] = make_float2((float)k.x, (float)k.y);
-          a.phi[o] = make_float2((float)(k.x * rD * norm), (float)(-k.y * rD * norm));
-        } else {
-          const int64_t o = LAYOUT == kPhiFused256 ? fused256_phi_index(cp, (int)vb, u)
-                            : LAYOUT == kPhiGeneric ? (cp * a.NCs + vb) * Hs + u
-                                                    : phi_out_index(a, cp, vb, u);
-          a.phi[o] = make_float2((float)((k.x + lmb) * rD * norm), (float)(-k.y * rD * norm));
+      for (int k0 = 0; k0 < 4; ++k0) {
+        ddft4(x[4 * k0], x[4 * k0 + 1], x[4 * k0 + 2], x[4 * k0 + 3]);
+#pragma unroll
+        for (int k1 = 0; k1 < 4; ++k1) {
+          const double2 k = x[4 * k0 + k1];
+          const int u = u1 + H1 * (k0 + 4 * k1);
+          const double rD = drcp(k.x * k.x + k.y * k.y + lmb);
+          if (op) {
+            const int64_t o = (cp * a.Ws + vb) * Hs + u;
+            a.kf[o] = make_float2((float)k.x, (float)k.y);
+            a.phi[o] = make_float2((float)(k.x * rD * norm), (float)(-k.y * rD * norm));
+          } else {
+            const int64_t o = LAYOUT == kPhiFused256 ? fused256_phi_index(cp, (int)vb, u)
+                              : LAYOUT == kPhiGeneric ? (cp * a.NCs + vb) * Hs + u
+                                                      : phi_out_index(a, cp, vb, u);
+            a.phi[o] = make_float2((float)((k.x + lmb) * rD * norm), (float)(-k.y * rD * norm));
+          }
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   } else {
@@ -492,7 +622,7 @@ __device__ void phi_tile_rows16(const PhiArgs& a, int op, const PhiTileView& tv,
     const int e = v * S + b;
     double2 x[16];
     if (act) {
-      phi_rows16_k(tv, Hs, a.kh, tv.P + e * kh4, u1, x);
+      phi_split_k(tv, e, u1, x);
       const double2 hv = tv.hW[e];
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
@@ -555,9 +685,10 @@ __device__ void phi_tile_rows16(const PhiArgs& a, int op, const PhiTileView& tv,
 
 // FAST: the split-DFT form (phi_rows16 holds; the host checks it), a separate instantiation so that
 // the Horner form's registers (S^2 complex K values per item) do not set its occupancy: at S = 4,
-// 130 instead of 220 VGPRs, three waves per SIMD instead of two.
+// 127 instead of 220 VGPRs.  Its four-wave bound costs the S = 1 form a few spilled registers (144
+// VGPRs unbounded) and measured 37.7 against 39.2 us per Converse-USRNet table.
 template <int S, bool FAST>
-__global__ void __launch_bounds__(256) k_phi_tile(PhiArgs a, int op, int vc, int nchunk) {
+__global__ void __launch_bounds__(256, FAST ? 4 : 1) k_phi_tile(PhiArgs a, int op, int vc, int nchunk) {
   extern __shared__ __align__(16) unsigned char phl[];
   const int tid = threadIdx.x, nth = blockDim.x;
   const int64_t cp = blockIdx.x / nchunk;
@@ -567,11 +698,9 @@ __global__ void __launch_bounds__(256) k_phi_tile(PhiArgs a, int op, int vc, int
   const int c = (int)(cp % a.C);
   const int Hs = a.Hs, Ws = a.Ws, h = a.h, kh = a.kh;
   const int kh4 = round4(kh);
-  const PhiTileView tv = phi_tile_prep<S>(a, phl, cp, vbeg, nv, vc, FAST);
-  const double2 *zH = tv.zH, *phH = tv.phH, *hH = tv.hH, *hW = tv.hW, *P = tv.P;
-
   const double lmb = lambda_of(a, c);
   if constexpr (FAST) {
+    const PhiTileView tv = phi_split_prep<S>(a, phl, cp, vbeg, nv, vc);
     static_assert(S != 3, "the split-DFT form serves scales 1, 2 and 4");
     double* part = (double*)(phl + phi_tile_lds(S, Hs, kh, a.kw, vc, true).part);
     if (S == 1 && !op && a.layout == kPhiFused256 && Hs == 256)
@@ -582,6 +711,8 @@ __global__ void __launch_bounds__(256) k_phi_tile(PhiArgs a, int op, int vc, int
       phi_tile_rows16<S>(a, op, tv, part, cp, vbeg, nv, lmb);
     return;
   }
+  const PhiTileView tv = phi_tile_prep<S>(a, phl, cp, vbeg, nv, vc);
+  const double2 *zH = tv.zH, *phH = tv.phH, *hH = tv.hH, *hW = tv.hW, *P = tv.P;
   const double norm = 1.0 / ((double)Hs * (double)Ws);
   const double inv_s2 = 1.0 / (double)(S * S);
   const int items = nv * h;
@@ -1779,7 +1910,9 @@ int launch_phi(const float* psf, const float* bias, float eps, const Geo& g, boo
     int nchunk = (int)std::min<int64_t>(a.nv0, std::max<int64_t>(1, (2048 + g.Cp - 1) / g.Cp));
     int vc = (a.nv0 + nchunk - 1) / nchunk;
     // split-DFT form (phi_tile_rows16): S Hs / 16 threads per LR column class, one round per block
-    const bool fast = phi_rows16(g.s, g.Hs, q268);
+    // (its set-up gives each thread one psf column and one row-twiddle column: kw and 16 NTh <= kThreads)
+    const bool fast = phi_rows16(g.s, g.Hs, q268) && g.kw <= kThreads &&
+                      16 * phi_tile_lds(g.s, g.Hs, g.kh, g.kw, 1, true).NTh <= kThreads;
     if (fast) vc = std::max(1, std::min(a.nv0, 256 / (g.s * (g.Hs / 16))));
     while (vc > 1 && phi_tile_lds(g.s, g.Hs, g.kh, g.kw, vc, fast).total > kTileLds) --vc;
     const int lds = phi_tile_lds(g.s, g.Hs, g.kh, g.kw, vc, fast).total;
