@@ -649,6 +649,13 @@ __device__ void phi_tile_rows16(const PhiArgs& a, int op, const PhiTileView& tv,
     if (act) {
       const int64_t vb = vbeg + v + (int64_t)b * a.w;
       const double2 hv = tv.hW[e];
+      // module form: the host evaluates the column classes v0 <= w / 2 only.  Phi is Hermitian
+      // (Phi(-u, -v) = conj Phi(u, v): real psf, and the hold sums satisfy h(-u) = conj h(u)), and the
+      // class (-u0, -v0) holds the negated bins of this class's members, so a class other than v0 = 0
+      // and v0 = w / 2 (which are their own mirror images) also writes its members past Ws / 2 as the
+      // conjugate entries at the negated bins, which are bins <= Ws / 2 of the mirrored class.
+      const int v0 = vbeg + v;
+      const bool mirror = !op && v0 != 0 && 2 * v0 != a.w;
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
         const double* pp = part + (int64_t)(v * h + u1 + H1 * m) * S * 3;
@@ -671,11 +678,19 @@ __device__ void phi_tile_rows16(const PhiArgs& a, int op, const PhiTileView& tv,
             const int64_t o = (cp * a.Ws + vb) * Hs + u;
             a.kf[o] = make_float2((float)k.x, (float)k.y);
             a.phi[o] = make_float2((float)(k.x * gop), (float)(-k.y * gop));
-          } else if (vb <= a.Ws / 2) {
+          } else if (vb <= a.Ws / 2 || mirror) {
             const double2 hn = dcmul(tv.hH[u], hv);
             const double2 t = dcmul(make_double2(k.x, -k.y), g);
-            const int64_t o = LAYOUT == kPhiGeneric ? (cp * a.NCs + vb) * Hs + u : phi_out_index(a, cp, vb, u);
-            a.phi[o] = make_float2((float)((hn.x + t.x) * norm), (float)((hn.y + t.y) * norm));
+            const float re = (float)((hn.x + t.x) * norm), im = (float)((hn.y + t.y) * norm);
+            if (vb <= a.Ws / 2) {
+              const int64_t o = LAYOUT == kPhiGeneric ? (cp * a.NCs + vb) * Hs + u : phi_out_index(a, cp, vb, u);
+              a.phi[o] = make_float2(re, im);
+            } else {  // the entry of the unevaluated class (-u0, -v0) at the negated bin
+              const int un = u == 0 ? 0 : Hs - u;
+              const int64_t vn = a.Ws - vb;
+              const int64_t o = LAYOUT == kPhiGeneric ? (cp * a.NCs + vn) * Hs + un : phi_out_index(a, cp, vn, un);
+              a.phi[o] = make_float2(re, -im);
+            }
           }
         }
       }
@@ -1913,6 +1928,11 @@ int launch_phi(const float* psf, const float* bias, float eps, const Geo& g, boo
     // (its set-up gives each thread one psf column and one row-twiddle column: kw and 16 NTh <= kThreads)
     const bool fast = phi_rows16(g.s, g.Hs, q268) && g.kw <= kThreads &&
                       16 * phi_tile_lds(g.s, g.Hs, g.kh, g.kw, 1, true).NTh <= kThreads;
+    // the split-DFT form's module tables at s > 1 evaluate the column classes v0 <= w / 2 and write the
+    // others' entries by Hermitian symmetry (the kernels below, if this one does not apply, evaluate
+    // every class: nv0 is restored for them)
+    const int nv0_all = a.nv0;
+    if (fast && !op && g.s > 1) a.nv0 = g.w / 2 + 1;
     if (fast) vc = std::max(1, std::min(a.nv0, 256 / (g.s * (g.Hs / 16))));
     while (vc > 1 && phi_tile_lds(g.s, g.Hs, g.kh, g.kw, vc, fast).total > kTileLds) --vc;
     const int lds = phi_tile_lds(g.s, g.Hs, g.kh, g.kw, vc, fast).total;
@@ -1929,6 +1949,7 @@ int launch_phi(const float* psf, const float* bias, float eps, const Geo& g, boo
       }
       return check_launch("transfer table");
     }
+    a.nv0 = nv0_all;
   }
   if (layout != kPhiGeneric) return fail(CVN_ERR_UNSUPPORTED, "this table layout needs the tiled kernel");
   const size_t lds = (size_t)g.s * g.kh * sizeof(double2);
