@@ -1107,11 +1107,13 @@ struct FusedUpArgs {
   int y_off, tw_off, idx_off;  // LDS offsets (bytes) of the LR spectrum, LR twiddles, kof / qof tables
 };
 
-// Stockham radices of the LR transform length L = 132 / s (fixed butterflies, first to last).
+// Stockham radices of the LR transform length L = N / s (fixed butterflies, first to last).
 template <int L> struct LrRadices;
 template <> struct LrRadices<66> { static constexpr int n = 3, r0 = 2, r1 = 3, r2 = 11; };
 template <> struct LrRadices<44> { static constexpr int n = 2, r0 = 4, r1 = 11, r2 = 1; };
 template <> struct LrRadices<33> { static constexpr int n = 2, r0 = 3, r1 = 11, r2 = 1; };
+// L = 256 / 4 on the 256 x 256 Cooley-Tukey plan
+template <> struct LrRadices<64> { static constexpr int n = 3, r0 = 4, r1 = 4, r2 = 4; };
 
 // LR twiddles exp(-2 pi i m / L), m < L, twice (the row and the column transform of a square LR
 // plane), evaluated at compile time in double and rounded once.
@@ -1148,10 +1150,11 @@ __device__ __forceinline__ float2* lr_fft(float2* a, float2* b, int ntr, const f
 
 // LR padded-plane index maps use the padding map of the LR input (as the reference pads before the
 // upsample, util_converse.py:144-145).
-// Two workgroups per CU (8 waves per SIMD): the even-row group is parked in registers and the LDS
-// holds one group, the slot tables and the LR spectrum.
+// The even-row group is parked in registers and the LDS holds one group, the slot tables and the LR
+// spectrum: two workgroups per CU (8 waves per SIMD) on the 132 x 132 plan, one (4 waves per SIMD,
+// 159 KB of LDS) on the 256 x 256 plan.
 template <class P, int S>
-__global__ void __launch_bounds__(kFT, 8) k_converse2d_fused_up(FusedUpArgs ua) {
+__global__ void __launch_bounds__(kFT, P::kCT ? 4 : 8) k_converse2d_fused_up(FusedUpArgs ua) {
   static_assert(P::N == P::M && P::N % S == 0, "square HR plane, LR side N / S");
   constexpr int h = P::N / S, w = P::M / S, ncl = w / 2 + 1, npl = (h + 1) / 2;
   extern __shared__ float2 smem[];
@@ -1280,6 +1283,13 @@ constexpr bool fused256_index_ok() {
 }
 static_assert(fused256_index_ok(), "fused256_phi_index matches Plan256");
 
+// The 256 x 256 plan as the up kernel uses it: the table block directly after the group buffer (the
+// up kernel parks nothing in LDS; its LR spectrum takes that space), which is where the Cooley-Tukey
+// passes then look for their twiddles (ct_tw).
+struct Plan256Up : Plan256 {
+  static constexpr int PARK_LDS = 0;
+};
+
 // LDS layout of the up kernel after the fused kernel's own regions.
 struct UpLayout {
   int y_off, tw_off, idx_off;
@@ -1299,16 +1309,23 @@ UpLayout up_layout(int h, int w) {
   return L;
 }
 
-// The up path serves HR planes of the 132 x 132 plan from LR planes h = w = 132 / s, s in 2..4,
-// whose transforms use fixed radices only; the LR pair buffers (2 (h + 1) / 2 w) and the column
-// transform's scratch fit in the group buffer and the parked rounds.
-bool fused_up_geometry(int H, int W, int pad, int s) {
-  using P = Plan132;
-  const int h = H + 2 * pad, w = W + 2 * pad;
-  if (s < 2 || s > 4 || h * s != P::N || w * s != P::M || (W * s) % 4 != 0) return false;
+// The up path serves HR planes of the 132 x 132 plan from LR planes h = w = 132 / s, s in 2..4, and
+// of the 256 x 256 plan from h = w = 64 at s = 4 (Converse-USRNet's first data step; at s = 2 the LR
+// spectrum would not fit next to the group buffer), whose transforms use fixed radices only; the LR
+// pair buffers (2 (h + 1) / 2 w) and the column transform's scratch fit in the group buffer.  Returns
+// the HR plan's side, or 0.
+template <class P>
+bool fused_up_fits(int h, int w, size_t lds_max) {
   const int npl = (h + 1) / 2;
   if ((size_t)2 * npl * w > (size_t)P::SLOTS_PAD || (size_t)(w / 2 + 1) * h > (size_t)P::SLOTS_PAD) return false;
-  return up_layout<P>(h, w).bytes <= 80 * 1024;  // two workgroups per CU
+  return up_layout<P>(h, w).bytes <= lds_max;
+}
+int fused_up_plan(int H, int W, int pad, int s) {
+  const int h = H + 2 * pad, w = W + 2 * pad;
+  if (s < 2 || s > 4 || h != w || (W * s) % 4 != 0) return 0;
+  if (h * s == Plan132::N && fused_up_fits<Plan132>(h, w, 80 * 1024)) return Plan132::N;  // two workgroups per CU
+  if (h * s == Plan256Up::N && s == 4 && fused_up_fits<Plan256Up>(h, w, 160 * 1024)) return Plan256Up::N;
+  return 0;
 }
 
 template <class P>
@@ -1377,11 +1394,12 @@ int fused_apply_run(const float* x, int64_t B, int64_t C, int H, int W, int64_t 
 
 // The fused kernel loads rows as float4 per lane: W must be a multiple of 4 and at most 256, or 260
 // on the 260-point plan with no padding (the last 4 columns go through single-word loads and stores).
-// At scale > 1 the HR plane must have a fused plan (fused_up_geometry).
+// At scale > 1 the HR plane must have a fused plan (fused_up_plan).
 int fused_query(int H, int W, int pad, int scale, int64_t Cp, size_t* ws_bytes) {
   if (scale != 1) {
-    if (!fused_up_geometry(H, W, pad, scale)) return 0;
-    *ws_bytes = fused_ws<Plan132>(Cp);
+    const int plan = fused_up_plan(H, W, pad, scale);
+    if (!plan) return 0;
+    *ws_bytes = plan == Plan256Up::N ? fused_ws<Plan256Up>(Cp) : fused_ws<Plan132>(Cp);
     return 1;
   }
   if (W % 4 != 0 || W > 260) return 0;  // past 256 columns only the 260 plan with no padding applies
@@ -1406,7 +1424,10 @@ int fused_table(const float* psf, const float* bias, float eps, int64_t C, int64
   if (scale != 1) {
     const int64_t Cp = psf_batch * C;
     PhiUpArgs pa{psf, bias, C, kh, kw, scale, (double)eps, (float4*)table};
-    hipLaunchKernelGGL(k_phi_fused_up<Plan132>, dim3((unsigned)(Cp * Plan132::NQ)), dim3(256), 0, st, pa);
+    if (fused_up_plan(H, W, pad, scale) == Plan256Up::N)
+      hipLaunchKernelGGL(k_phi_fused_up<Plan256Up>, dim3((unsigned)(Cp * Plan256Up::NQ)), dim3(256), 0, st, pa);
+    else
+      hipLaunchKernelGGL(k_phi_fused_up<Plan132>, dim3((unsigned)(Cp * Plan132::NQ)), dim3(256), 0, st, pa);
     return check_launch("fused transfer table (scale > 1)");
   }
   const int h = H + 2 * pad;
@@ -1415,33 +1436,50 @@ int fused_table(const float* psf, const float* bias, float eps, int64_t C, int64
   return fused_table_run<Plan132>(psf, bias, eps, C, psf_batch, kh, kw, table, st);
 }
 
+template <class P>
+FusedUpArgs up_args(const float* x, int64_t B, int64_t C, int H, int W, int64_t psf_batch, int pad, int mode,
+                    int act, int scale, const void* table, float* out, size_t* lds) {
+  FusedUpArgs ua;
+  const UpLayout L = up_layout<P>(H + 2 * pad, W + 2 * pad);
+  ua.hr = FusedArgs{x, (const float4*)table, out, B, C, psf_batch, H * scale, W * scale, pad * scale, mode, act};
+  ua.Hl = H;
+  ua.Wl = W;
+  ua.padl = pad;
+  ua.y_off = L.y_off;
+  ua.tw_off = L.tw_off;
+  ua.idx_off = L.idx_off;
+  *lds = L.bytes;
+  return ua;
+}
+
 int fused_apply(const float* x, int64_t B, int64_t C, int H, int W, int64_t psf_batch, int pad, int mode, int act,
                 int scale, const void* table, void* scratch, float* out, hipStream_t st) {
   if (scale != 1) {
-    using P = Plan132;
     static std::atomic<uint64_t> attr{0};
     once_per_device(attr, [] {
-      for (const void* k : {(const void*)k_converse2d_fused_up<P, 2>, (const void*)k_converse2d_fused_up<P, 3>,
-                            (const void*)k_converse2d_fused_up<P, 4>})
+      for (const void* k : {(const void*)k_converse2d_fused_up<Plan132, 2>, (const void*)k_converse2d_fused_up<Plan132, 3>,
+                            (const void*)k_converse2d_fused_up<Plan132, 4>})
         (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024);
+      (void)hipFuncSetAttribute((const void*)k_converse2d_fused_up<Plan256Up, 4>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
       (void)hipGetLastError();
     });
-    if (!fused_up_geometry(H, W, pad, scale))
-      return fail(CVN_ERR_UNSUPPORTED, "no fused plan for this upsampling geometry");
-    FusedUpArgs ua;
-    const UpLayout L = up_layout<P>(H + 2 * pad, W + 2 * pad);
-    ua.hr = FusedArgs{x, (const float4*)table, out, B, C, psf_batch, H * scale, W * scale, pad * scale, mode, act};
-    ua.Hl = H;
-    ua.Wl = W;
-    ua.padl = pad;
-    ua.y_off = L.y_off;
-    ua.tw_off = L.tw_off;
-    ua.idx_off = L.idx_off;
+    const int plan = fused_up_plan(H, W, pad, scale);
+    if (!plan) return fail(CVN_ERR_UNSUPPORTED, "no fused plan for this upsampling geometry");
     const dim3 grid((unsigned)(B * C));
+    size_t lds = 0;
+    if (plan == Plan256Up::N) {
+      using P = Plan256Up;
+      const FusedUpArgs ua = up_args<P>(x, B, C, H, W, psf_batch, pad, mode, act, scale, table, out, &lds);
+      hipLaunchKernelGGL((k_converse2d_fused_up<P, 4>), grid, dim3(kFT), lds, st, ua);
+      return check_launch("fused converse2d (scale > 1)");
+    }
+    using P = Plan132;
+    const FusedUpArgs ua = up_args<P>(x, B, C, H, W, psf_batch, pad, mode, act, scale, table, out, &lds);
     switch (scale) {
-      case 2: hipLaunchKernelGGL((k_converse2d_fused_up<P, 2>), grid, dim3(kFT), L.bytes, st, ua); break;
-      case 3: hipLaunchKernelGGL((k_converse2d_fused_up<P, 3>), grid, dim3(kFT), L.bytes, st, ua); break;
-      default: hipLaunchKernelGGL((k_converse2d_fused_up<P, 4>), grid, dim3(kFT), L.bytes, st, ua); break;
+      case 2: hipLaunchKernelGGL((k_converse2d_fused_up<P, 2>), grid, dim3(kFT), lds, st, ua); break;
+      case 3: hipLaunchKernelGGL((k_converse2d_fused_up<P, 3>), grid, dim3(kFT), lds, st, ua); break;
+      default: hipLaunchKernelGGL((k_converse2d_fused_up<P, 4>), grid, dim3(kFT), lds, st, ua); break;
     }
     return check_launch("fused converse2d (scale > 1)");
   }

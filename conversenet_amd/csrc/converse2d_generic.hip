@@ -616,9 +616,11 @@ __device__ void phi_tile_rows16(const PhiArgs& a, int op, const PhiTileView& tv,
     constexpr int NM = 16 / S;  // alias classes per thread
     constexpr double inv_s2 = 1.0 / (double)(S * S);
     const int h = a.h;          // = NM H1
+    // threads (b, v, u1), u1 fastest, then the chunk's column classes: a wave's stores cover runs of
+    // consecutive columns of one member, as at S = 1, rather than S members Ws / S columns apart
     const int it = threadIdx.x;
     const bool act = it < nv * S * H1;
-    const int v = it / (S * H1), rem = it - v * S * H1, b = rem / H1, u1 = rem - b * H1;
+    const int b = it / (nv * H1), rem = it - b * nv * H1, v = rem / H1, u1 = rem - v * H1;
     const int e = v * S + b;
     double2 x[16];
     if (act) {
@@ -683,12 +685,16 @@ __device__ void phi_tile_rows16(const PhiArgs& a, int op, const PhiTileView& tv,
             const double2 t = dcmul(make_double2(k.x, -k.y), g);
             const float re = (float)((hn.x + t.x) * norm), im = (float)((hn.y + t.y) * norm);
             if (vb <= a.Ws / 2) {
-              const int64_t o = LAYOUT == kPhiGeneric ? (cp * a.NCs + vb) * Hs + u : phi_out_index(a, cp, vb, u);
+              const int64_t o = LAYOUT == kPhiFused256 ? fused256_phi_index(cp, (int)vb, u)
+                                : LAYOUT == kPhiGeneric ? (cp * a.NCs + vb) * Hs + u
+                                                        : phi_out_index(a, cp, vb, u);
               a.phi[o] = make_float2(re, im);
             } else {  // the entry of the unevaluated class (-u0, -v0) at the negated bin
               const int un = u == 0 ? 0 : Hs - u;
               const int64_t vn = a.Ws - vb;
-              const int64_t o = LAYOUT == kPhiGeneric ? (cp * a.NCs + vn) * Hs + un : phi_out_index(a, cp, vn, un);
+              const int64_t o = LAYOUT == kPhiFused256 ? fused256_phi_index(cp, (int)vn, un)
+                                : LAYOUT == kPhiGeneric ? (cp * a.NCs + vn) * Hs + un
+                                                        : phi_out_index(a, cp, vn, un);
               a.phi[o] = make_float2(re, -im);
             }
           }
@@ -718,12 +724,12 @@ __global__ void __launch_bounds__(256, FAST ? 4 : 1) k_phi_tile(PhiArgs a, int o
     const PhiTileView tv = phi_split_prep<S>(a, phl, cp, vbeg, nv, vc);
     static_assert(S != 3, "the split-DFT form serves scales 1, 2 and 4");
     double* part = (double*)(phl + phi_tile_lds(S, Hs, kh, a.kw, vc, true).part);
-    if (S == 1 && !op && a.layout == kPhiFused256 && Hs == 256)
+    // the host runs this form for the generic layout and for the fused 256 x 256 plan's slot order
+    // only (the op form writes its own layout), so both are compile-time layouts here
+    if (!op && a.layout == kPhiFused256)
       phi_tile_rows16<S, kPhiFused256>(a, op, tv, part, cp, vbeg, nv, lmb);
-    else if (!op && a.layout == kPhiGeneric)
-      phi_tile_rows16<S, kPhiGeneric>(a, op, tv, part, cp, vbeg, nv, lmb);
     else
-      phi_tile_rows16<S>(a, op, tv, part, cp, vbeg, nv, lmb);
+      phi_tile_rows16<S, kPhiGeneric>(a, op, tv, part, cp, vbeg, nv, lmb);
     return;
   }
   const PhiTileView tv = phi_tile_prep<S>(a, phl, cp, vbeg, nv, vc);
@@ -1927,7 +1933,8 @@ int launch_phi(const float* psf, const float* bias, float eps, const Geo& g, boo
     // split-DFT form (phi_tile_rows16): S Hs / 16 threads per LR column class, one round per block
     // (its set-up gives each thread one psf column and one row-twiddle column: kw and 16 NTh <= kThreads)
     const bool fast = phi_rows16(g.s, g.Hs, q268) && g.kw <= kThreads &&
-                      16 * phi_tile_lds(g.s, g.Hs, g.kh, g.kw, 1, true).NTh <= kThreads;
+                      16 * phi_tile_lds(g.s, g.Hs, g.kh, g.kw, 1, true).NTh <= kThreads &&
+                      (op || layout == kPhiGeneric || (layout == kPhiFused256 && g.Hs == 256 && g.Ws == 256));
     // the split-DFT form's module tables at s > 1 evaluate the column classes v0 <= w / 2 and write the
     // others' entries by Hermitian symmetry (the kernels below, if this one does not apply, evaluate
     // every class: nv0 is restored for them)
@@ -2158,10 +2165,11 @@ extern "C" int cvn_converse2d_table_f32(const float* psf, int64_t psf_batch, int
     return fail(CVN_ERR_WORKSPACE, "table buffer too small: need %zu bytes", r.table_bytes);
   hipStream_t st = (hipStream_t)stream;
   if (r.id == CVN_ROUTE_FUSED) {
-    // 256 x 256 planes: the split-DFT table kernel writes the fused plan's slot order directly (a
-    // per-sample 25 x 25 psf, Converse-USRNet's data step, is several times faster there than in
-    // k_phi_fused); the fused kernels' own table kernel otherwise
-    if (g.s == 1 && g.h == 256 && g.w == 256 &&
+    // 256 x 256 HR planes (s = 1, or the up kernel at s = 4): the split-DFT table kernel writes the
+    // fused plan's slot order directly (a per-sample 25 x 25 psf, Converse-USRNet's data steps, is
+    // several times faster there than in k_phi_fused / k_phi_fused_up); the fused kernels' own table
+    // kernels otherwise
+    if (g.Hs == 256 && g.Ws == 256 &&
         launch_phi(psf, bias, eps, g, false, (float2*)table, nullptr, st, kPhiFused256) == CVN_OK)
       return CVN_OK;
     return fused_table(psf, bias, eps, g.C, g.Cp / g.C, kh, kw, g.H, g.W, g.pad, g.s, table, st);

@@ -81,7 +81,8 @@ def test_route_query_and_environment(monkeypatch):
     assert lib.cvn_converse2d_route(4, 64, 256, 256, 4, 25, 25, 1, 0) == _lib.ROUTE_FUSED
     assert lib.cvn_converse2d_route(1, 2, 240, 240, 1, 7, 7, 1, 8) == _lib.ROUTE_FUSED
     assert lib.cvn_converse2d_route(1, 2, 250, 250, 1, 7, 7, 1, 3) == _lib.ROUTE_GENERIC  # 250 % 4 != 0
-    assert lib.cvn_converse2d_route(4, 64, 64, 64, 4, 25, 25, 4, 0) == _lib.ROUTE_GENERIC  # 64 -> 256: no up plan
+    assert lib.cvn_converse2d_route(4, 64, 64, 64, 4, 25, 25, 4, 0) == _lib.ROUTE_FUSED  # 64 -> 256 up plan
+    assert lib.cvn_converse2d_route(4, 64, 128, 128, 4, 25, 25, 2, 0) == _lib.ROUTE_GENERIC  # 128 -> 256: no up plan
     monkeypatch.setenv("CVN_DISABLE_FUSED", "1")
     assert lib.cvn_converse2d_route(16, 64, 256, 256, 1, 5, 5, 1, 2) == _lib.ROUTE_GENERIC
     assert lib.cvn_converse2d_route(8, 128, 256, 256, 1, 7, 7, 1, 6) == _lib.ROUTE_GENERIC

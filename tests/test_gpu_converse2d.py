@@ -469,11 +469,13 @@ MODULE_PLANNED = [(4, 8, 64, 64, 4, 25, 4, None), (2, 3, 64, 128, 2, 5, 1, "gelu
 
 
 @pytest.mark.parametrize("B,C,h,w,s,k,pb,act", MODULE_PLANNED)
-def test_module_planned_scale(B, C, h, w, s, k, pb, act):
+def test_module_planned_scale(B, C, h, w, s, k, pb, act, monkeypatch):
     """Converse2D module path (util_converse.py:142-192) at scale > 1 without padding on the compile-time
-    plans, against the fp64 oracle, max-abs <= 1e-4."""
+    plans, against the fp64 oracle, max-abs <= 1e-4.  The generic route is forced (64 -> 256 at s = 4
+    would otherwise take the fused upsampling kernel, tested in test_fused_upsampling_path)."""
     from conversenet_amd import _lib
     from conversenet_amd import functional as Fh
+    monkeypatch.setenv("CVN_DISABLE_FUSED", "1")
     lib = _lib.load()
     assert lib.cvn_converse2d_route(B, C, h, w, pb, k, k, s, 0) == _lib.ROUTE_GENERIC
     assert lib.cvn_converse2d_op_route(h, w, s) == _lib.ROUTE_OP_PLANNED  # the lengths have plans
@@ -542,7 +544,8 @@ def test_module_biaseps_after_hip_forward():
 
 
 # ---------------------------------------------------------------------------------------------
-# Fused upsampling path: HR plane 132 x 132 from LR planes of 66 (s = 2), 44 (s = 3), 33 (s = 4)
+# Fused upsampling path: HR plane 132 x 132 from LR planes of 66 (s = 2), 44 (s = 3), 33 (s = 4);
+# HR plane 256 x 256 from LR planes of 64 (s = 4, Converse-USRNet's first data step)
 # ---------------------------------------------------------------------------------------------
 UP_CASES = [
     # (B, C, H, W, k, s, p, mode, psf batch)
@@ -551,6 +554,10 @@ UP_CASES = [
     (2, 2, 40, 40, 5, 3, 2, "replicate", 1),
     (1, 3, 31, 31, 4, 4, 1, "constant", 1),
     (2, 2, 33, 33, 7, 4, 0, "circular", 2),   # per-sample psf, no padding
+    (2, 2, 64, 64, 25, 4, 0, "circular", 2),  # 256 plan: Converse-USRNet's data step (per-sample 25 x 25)
+    (1, 3, 64, 64, 9, 4, 0, "replicate", 1),
+    (1, 2, 62, 62, 5, 4, 1, "reflect", 1),    # 256 plan, padded LR plane, 248 x 248 output
+    (2, 2, 60, 60, 4, 4, 2, "constant", 2),
 ]
 
 

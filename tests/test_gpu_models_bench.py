@@ -106,11 +106,8 @@ def test_converse_usrnet_b4_routes(usrnet_b4):
     steps = (4, 64, 256, 256, 4, 25, 25, 1, 0)
     seen = [geo for geo, _ in calls]
     assert seen.count(body) == 35 and seen.count(step0) == 1 and seen.count(steps) == 4 and len(seen) == 40
-    for geo, (route, _, sb) in calls:
-        if geo == step0:
-            assert route == _lib.ROUTE_GENERIC
-        else:  # one 1024-thread workgroup per plane: no split scratch requested
-            assert route == _lib.ROUTE_FUSED and sb == 0
+    for geo, (route, _, sb) in calls:  # one 1024-thread workgroup per plane: no split scratch requested
+        assert route == _lib.ROUTE_FUSED and sb == 0
 
 
 @pytest.mark.parametrize("i", range(4))
