@@ -558,6 +558,7 @@ UP_CASES = [
     (1, 3, 64, 64, 9, 4, 0, "replicate", 1),
     (1, 2, 62, 62, 5, 4, 1, "reflect", 1),    # 256 plan, padded LR plane, 248 x 248 output
     (2, 2, 60, 60, 4, 4, 2, "constant", 2),
+    (2, 2, 64, 64, 61, 4, 0, "circular", 2),  # 256 plan, psf past the split-DFT table's LDS budget
 ]
 
 
