@@ -81,7 +81,9 @@ int cvn_converse2d_fwd_noalloc_f32(const float* x, int64_t B, int64_t C, int64_t
                                    cvn_stream_t stream);
 
 /* Which kernels serve a module-level call, and so which layout its transfer table has:
- * CVN_ROUTE_FUSED    one kernel per call, a plane per workgroup (132 x 132, 260 x 260 padded planes, s = 1)
+ * CVN_ROUTE_FUSED    a plane per workgroup: padded planes of 132 x 132, 256 x 256 and 260 x 260 at
+ *                    s = 1 (one kernel; two when scratch is given and there are at most 128 planes),
+ *                    and upsampling onto 132 x 132 (s = 2-4) or 256 x 256 (s = 4, from 64 x 64)
  * CVN_ROUTE_PFA268   the three-pass 268 x 268 path (Converse-DnCNN's k7 p6 layers on 256 x 256 inputs)
  * CVN_ROUTE_GENERIC  the three-pass path for any plane up to 4096 x 4096, any scale, any psf size
  * CVN_ROUTE_AUTO     (argument only) the route cvn_converse2d_route() picks. */
