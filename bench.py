@@ -2,7 +2,7 @@
 """Benchmark of the Converse2D forward hot path on one MI355X.
 
 Headline (value): Converse2D forward throughput in Gpix*ch/s on the roofline workload
-(BASELINE cfg3): B=16, C=64, 256x256, k=5, scale=1, padding=2 circular, fp32, synthetic N(0,1)
+(cfg3): B=16, C=64, 256x256, k=5, scale=1, padding=2 circular, fp32, synthetic N(0,1)
 input, softmax-normalised seeded psf, zero bias.  One step = one module-level Converse2D forward
 of that batch (padding, solve and crop fused; inputs resident in HBM).
 
