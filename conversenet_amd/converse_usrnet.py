@@ -116,6 +116,27 @@ def _conv(m, x):
     return m(x)
 
 
+def _psf_maps(model, k, b, h, w):
+    """Every iteration's psf convs[i](k).view(b, 64, h, w) (converse_usrnet.py:203-211 computes each in
+    its loop; they depend on k only).  On HIP the 1x1 convolutions (16 -> 64 channels on psf-sized maps,
+    a few microseconds of work each, bound by launch and memory latency) run as one launch with the
+    weights stacked (kept while the parameters are unchanged), and one transposing copy lays the
+    output out iteration-major, so that each iteration's psf is a contiguous (b, 64, h, w) view."""
+    convs = model.convs
+    if all(_hip_eligible(k, m.weight, m.bias) for m in convs):
+        params = [t for m in convs for t in (m.weight, m.bias)]
+        key = tuple((t.data_ptr(), t._version) for t in params)
+        cached = getattr(model, "_psf_stack", None)
+        if cached is None or cached[0] != key:
+            cached = (key, torch.cat([m.weight for m in convs]), torch.cat([m.bias for m in convs]))
+            model._psf_stack = cached
+        n, m_ = convs[0].weight.shape[0], len(convs)
+        y = functional.conv1x1(k, cached[1], cached[2])  # (b, m n, kh, kw)
+        z = y.view(b, m_, n * y.shape[2] * y.shape[3]).transpose(0, 1).contiguous()
+        return [z[i].view(b, n, h, w) for i in range(m_)]
+    return [_conv(m, k).view(b, 64, h, w) for m in convs]
+
+
 class ConverseUSRNet(nn.Module):
     def __init__(self, num_iterations=5, in_channels=64, num_blocks=7, kernel_size=7):
         super().__init__()
@@ -131,11 +152,10 @@ class ConverseUSRNet(nn.Module):
         b, c, h, w = k.shape
         k = self.kernelnet(k)
         x = _conv(self.conv1, x)
-        k_1 = _conv(self.convs[0], k).view(b, 64, h, w)
-        x = self.d(x, k_1, sf)
+        ks = _psf_maps(self, k, b, h, w)
+        x = self.d(x, ks[0], sf)
         x = self.p(x)
         for i in range(1, self.num_iterations):
-            k_ = _conv(self.convs[i], k).view(b, 64, h, w)
-            x = self.d(x, k_, 1)
+            x = self.d(x, ks[i], 1)
             x = self.p(x)
         return _conv(self.conv2, x)
